@@ -1,0 +1,93 @@
+"""ctypes binding of the C-ABI in ``include/unok.h`` (library ``uno_amd/libunok.so``).
+
+The library is built in-tree by ``uno_amd.build`` (``__graft_entry__.build()``). There is no
+fallback: if the library is missing or a kernel fails, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libunok.so"
+
+F32, BF16 = 0, 1
+_EINVAL, _EALIGN, _EUNSUPPORTED = -1, -2, -3
+
+_i, _i64, _p, _f = C.c_int, C.c_int64, C.c_void_p, C.c_float
+_ip = C.POINTER(C.c_int)
+
+# name -> (restype, argtypes); must match include/unok.h exactly.
+SIGNATURES: dict[str, tuple] = {
+    "unok_abi_version": (_i, []),
+    "unok_last_error": (C.c_char_p, []),
+    "unok_gemm_nt": (_i, [_i, _i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i,
+                          _i, _ip, _ip, _p, _i64, _p, _i64, _p, _f, _p]),
+    "unok_gemm_tn_workspace": (_i64, [_i, _i, _i]),
+    "unok_gemm_tn": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _f, _f, _p, _i64, _p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib():
+    """Loads libunok.so once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"uno_amd kernel library not found at {LIB_PATH}; build it with "
+                    "`python -m uno_amd.build` (no non-HIP fallback exists)")
+            handle = C.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = handle
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)
+
+
+def check(rc: int, what: str) -> None:
+    if rc == 0:
+        return
+    msg = lib().unok_last_error().decode(errors="replace")
+    if rc == _EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    raise ValueError(f"unsupported dtype {dt}; the kernels take float32 or bfloat16")
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def int_array(values) -> C.Array:
+    arr = (C.c_int * max(1, len(values)))()
+    for i, v in enumerate(values):
+        arr[i] = int(v)
+    return arr

@@ -1,0 +1,521 @@
+// GEMM kernels for the conditional-LoRA linears.
+//
+// All large products of the step are expressed as "NT" GEMMs, C = A * B^T with both operands
+// K-contiguous: forward linears use the frozen weight W[out,in]; data gradients use a
+// transposed frozen copy W^T[in,out] kept resident in HBM; the LM head uses W_lm[V,H] and
+// W_lm^T[H,V]. One MFMA kernel therefore serves every large product.
+//
+// The LoRA update is fused as a K-extension of the same product:
+//   C = alpha * gate (.) ( A[M,K] B[N,K]^T  +  A2[M, col(n) : col(n)+K2] B2[N,K2]^T ) + R
+// where, for the forward of a linear, A2 = h = m (.) (x A_lora^T) and B2 = s * B_lora, i.e.
+// y = x W^T + s B (m (.) A x) (PEFT LoRA with the token gate, training/lora.py:164-174 and
+// peft 0.15.2 lora.Linear.forward). Fused projections (q|k|v, gate|up) carry up to four
+// N-segments, each with its own column offset into A2, so the block-diagonal LoRA update
+// of a fused projection costs exactly K2 extra K per output column.
+//
+// The LoRA weight gradients dB = s h^T dY and dA = g^T x are "TN" products (reduction over
+// token rows); gemm_tn computes them with split-K partials into a caller workspace.
+#include "common.h"
+
+struct GemmNT {
+  const void* A; int64_t lda;
+  const void* B; int64_t ldb;
+  const void* A2; int64_t lda2;
+  const void* B2; int64_t ldb2;
+  void* C; int64_t ldc;
+  const void* R; int64_t ldr;
+  const uint8_t* gate;
+  int M, N, K, K2;
+  int nseg;
+  int seg_end[4];
+  int seg_col[4];
+  float alpha;
+};
+
+template <typename T> __device__ __forceinline__ float ld_f(const T* p);
+template <> __device__ __forceinline__ float ld_f<float>(const float* p) { return *p; }
+template <> __device__ __forceinline__ float ld_f<bf16_t>(const bf16_t* p) { return bf16_to_f32(*p); }
+
+__device__ __forceinline__ int find_seg(const GemmNT& p, int n0) {
+  int s = 0;
+  while (s + 1 < p.nseg && n0 >= p.seg_end[s]) ++s;
+  return s;
+}
+
+// ---------------------------------------------------------------------------------------
+// bf16 MFMA NT kernel: BM x BN x 64 tiles, 4 waves in a 2x2 grid, each wave computing a
+// (BM/2) x (BN/2) sub-tile with v_mfma_f32_32x32x16_bf16. Operand tiles are double
+// buffered in LDS (row stride 72 bf16 = 144 B, which makes the 16-byte operand reads of a
+// quarter-wave hit distinct banks); the next K tile is fetched into registers while the
+// current one is multiplied.
+// ---------------------------------------------------------------------------------------
+template <int BM, int BN, typename OutT>
+__global__ __launch_bounds__(256) void gemm_nt_bf16_kernel(const GemmNT p) {
+  constexpr int BK = 64, LDSS = BK + 8;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int ACH = BM * BK / 8 / 256;
+  constexpr int BCH = BN * BK / 8 / 256;
+  static_assert(ACH >= 1 && BCH >= 1, "tile too small for 256 threads");
+  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * LDSS];
+  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BN * LDSS];
+
+  const int tid = threadIdx.x;
+  const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
+  const int lin = xcd_remap(blockIdx.x, nM * nN);
+  constexpr int GROUP = 8;
+  const int group = lin / (GROUP * nN);
+  const int first_m = group * GROUP;
+  const int gsz = min(nM - first_m, GROUP);
+  const int ing = lin % (GROUP * nN);
+  const int m0 = (first_m + ing % gsz) * BM;
+  const int n0 = (ing / gsz) * BN;
+
+  const bf16_t* A = (const bf16_t*)p.A;
+  const bf16_t* B = (const bf16_t*)p.B;
+  const bf16_t* A2 = nullptr;
+  const bf16_t* B2 = (const bf16_t*)p.B2;
+  if (p.A2 != nullptr && p.K2 > 0) A2 = (const bf16_t*)p.A2 + p.seg_col[find_seg(p, n0)];
+  const int nk1 = (p.K + BK - 1) / BK;
+  const int nk2 = A2 ? (p.K2 + BK - 1) / BK : 0;
+  const int nk = nk1 + nk2;
+
+  uint4 ra[ACH], rb[BCH];
+  auto load = [&](int kt) {
+    const bf16_t* a; const bf16_t* b; int64_t la, lb; int kk, kmax;
+    if (kt < nk1) { a = A; b = B; la = p.lda; lb = p.ldb; kk = kt * BK; kmax = p.K; }
+    else { a = A2; b = B2; la = p.lda2; lb = p.ldb2; kk = (kt - nk1) * BK; kmax = p.K2; }
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i, r = c >> 3, kc = (c & 7) * 8;
+      const int gm = m0 + r, gk = kk + kc;
+      ra[i] = (gm < p.M && gk < kmax) ? *(const uint4*)(a + (int64_t)gm * la + gk) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i, r = c >> 3, kc = (c & 7) * 8;
+      const int gn = n0 + r, gk = kk + kc;
+      rb[i] = (gn < p.N && gk < kmax) ? *(const uint4*)(b + (int64_t)gn * lb + gk) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i, r = c >> 3, kc = (c & 7) * 8;
+      *(uint4*)&As[buf][r * LDSS + kc] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i, r = c >> 3, kc = (c & 7) * 8;
+      *(uint4*)&Bs[buf][r * LDSS + kc] = rb[i];
+    }
+  };
+
+  const int lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lrow = lane & 31, lk = (lane >> 5) * 8;
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8_t a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        a[i] = *(const bf16x8_t*)&As[buf][(wm * WM + i * 32 + lrow) * LDSS + ks * 16 + lk];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        b[j] = *(const bf16x8_t*)&Bs[buf][(wn * WN + j * 32 + lrow) * LDSS + ks * 16 + lk];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) load(kt + 1);
+    compute(kt & 1);
+    if (kt + 1 < nk) store((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  OutT* C = (OutT*)p.C;
+  const OutT* R = (const OutT*)p.R;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (row >= p.M) continue;
+      const bool on = (p.gate == nullptr) || (p.gate[row] != 0);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + lrow;
+        if (col >= p.N) continue;
+        float v = on ? acc[i][j][r] * p.alpha : 0.f;
+        if (R) v += ld_f(R + (int64_t)row * p.ldr + col);
+        Elem<OutT>::store(C + (int64_t)row * p.ldc + col, v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// fp32 NT kernel (fp32 parity mode): 64x64 tiles, 16-deep K slices, 4x4 outputs per thread.
+// ---------------------------------------------------------------------------------------
+template <typename OutT>
+__global__ __launch_bounds__(256) void gemm_nt_f32_kernel(const GemmNT p) {
+  __shared__ float As[16][65], Bs[16][65];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const float* A = (const float*)p.A;
+  const float* B = (const float*)p.B;
+  const float* A2 = nullptr;
+  if (p.A2 != nullptr && p.K2 > 0) A2 = (const float*)p.A2 + p.seg_col[find_seg(p, n0)];
+  const float* B2 = (const float*)p.B2;
+  float acc[4][4] = {};
+  for (int part = 0; part < 2; ++part) {
+    const float* a = part ? A2 : A;
+    const float* b = part ? B2 : B;
+    if (a == nullptr) continue;
+    const int64_t la = part ? p.lda2 : p.lda, lb = part ? p.ldb2 : p.ldb;
+    const int K = part ? p.K2 : p.K;
+    for (int k0 = 0; k0 < K; k0 += 16) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = tid + 256 * q, r = e >> 4, k = e & 15;
+        const int gm = m0 + r, gn = n0 + r, gk = k0 + k;
+        As[k][r] = (gm < p.M && gk < K) ? a[(int64_t)gm * la + gk] : 0.f;
+        Bs[k][r] = (gn < p.N && gk < K) ? b[(int64_t)gn * lb + gk] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        float av[4], bv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) av[i] = As[k][ty + 16 * i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bv[j] = Bs[k][tx + 16 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+      }
+      __syncthreads();
+    }
+  }
+  OutT* C = (OutT*)p.C;
+  const OutT* R = (const OutT*)p.R;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + ty + 16 * i;
+    if (row >= p.M) continue;
+    const bool on = (p.gate == nullptr) || (p.gate[row] != 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + tx + 16 * j;
+      if (col >= p.N) continue;
+      float v = on ? acc[i][j] * p.alpha : 0.f;
+      if (R) v += ld_f(R + (int64_t)row * p.ldr + col);
+      Elem<OutT>::store(C + (int64_t)row * p.ldc + col, v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// TN products for LoRA weight gradients: WS[z][P][Q] = alpha * sum_{m in split z} A[m,p] B[m,q].
+// The bf16 kernel stages A^T and B^T tiles in LDS (transposing 16-byte global loads into
+// m-contiguous rows) and then runs the same MFMA inner loop as the NT kernel.
+// ---------------------------------------------------------------------------------------
+struct GemmTN {
+  const void* A; int64_t lda;   // [Mrows, P]
+  const void* B; int64_t ldb;   // [Mrows, Q]
+  float* WS;                     // [nsplit, P, Q]
+  int Mrows, P, Q, rows_per_split;
+  float alpha;
+};
+
+template <int BP, int BQ>
+__global__ __launch_bounds__(256) void gemm_tn_bf16_kernel(const GemmTN p) {
+  constexpr int BK = 64, LDSS = BK + 8;
+  constexpr int WP = BP / 2, WQ = BQ / 2;
+  constexpr int TM = WP / 32, TN = WQ / 32;
+  constexpr int ACH = BP * BK / 8 / 256;
+  constexpr int BCH = BQ * BK / 8 / 256;
+  __shared__ __attribute__((aligned(16))) bf16_t As[BP * LDSS];
+  __shared__ __attribute__((aligned(16))) bf16_t Bs[BQ * LDSS];
+  const int tid = threadIdx.x;
+  const int nQ = (p.Q + BQ - 1) / BQ;
+  const int p0 = (blockIdx.x / nQ) * BP, q0 = (blockIdx.x % nQ) * BQ;
+  const int mbeg = blockIdx.y * p.rows_per_split;
+  const int mend = min(p.Mrows, mbeg + p.rows_per_split);
+  const bf16_t* A = (const bf16_t*)p.A;
+  const bf16_t* B = (const bf16_t*)p.B;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lrow = lane & 31, lk = (lane >> 5) * 8;
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  for (int mk = mbeg; mk < mend; mk += BK) {
+    uint4 ra[ACH], rb[BCH];
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i, r = c / (BP / 8), pc = (c % (BP / 8)) * 8;
+      const int gm = mk + r, gp = p0 + pc;
+      ra[i] = (gm < mend && gp < p.P) ? *(const uint4*)(A + (int64_t)gm * p.lda + gp) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i, r = c / (BQ / 8), qc = (c % (BQ / 8)) * 8;
+      const int gm = mk + r, gq = q0 + qc;
+      rb[i] = (gm < mend && gq < p.Q) ? *(const uint4*)(B + (int64_t)gm * p.ldb + gq) : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i, r = c / (BP / 8), pc = (c % (BP / 8)) * 8;
+      const bf16_t* v = (const bf16_t*)&ra[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) As[(pc + e) * LDSS + r] = v[e];
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i, r = c / (BQ / 8), qc = (c % (BQ / 8)) * 8;
+      const bf16_t* v = (const bf16_t*)&rb[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Bs[(qc + e) * LDSS + r] = v[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8_t a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = *(const bf16x8_t*)&As[(wm * WP + i * 32 + lrow) * LDSS + ks * 16 + lk];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = *(const bf16x8_t*)&Bs[(wn * WQ + j * 32 + lrow) * LDSS + ks * 16 + lk];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  float* W = p.WS + (int64_t)blockIdx.y * p.P * p.Q;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = p0 + wm * WP + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (row >= p.P) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = q0 + wn * WQ + j * 32 + lrow;
+        if (col < p.Q) W[(int64_t)row * p.Q + col] = acc[i][j][r] * p.alpha;
+      }
+    }
+}
+
+__global__ __launch_bounds__(256) void gemm_tn_f32_kernel(const GemmTN p) {
+  __shared__ float As[16][65], Bs[16][65];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int nQ = (p.Q + 63) / 64;
+  const int p0 = (blockIdx.x / nQ) * 64, q0 = (blockIdx.x % nQ) * 64;
+  const int mbeg = blockIdx.y * p.rows_per_split;
+  const int mend = min(p.Mrows, mbeg + p.rows_per_split);
+  const float* A = (const float*)p.A;
+  const float* B = (const float*)p.B;
+  float acc[4][4] = {};
+  for (int mk = mbeg; mk < mend; mk += 16) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = tid + 256 * q, k = e >> 6, c = e & 63;
+      const int gm = mk + k;
+      As[k][c] = (gm < mend && p0 + c < p.P) ? A[(int64_t)gm * p.lda + p0 + c] : 0.f;
+      Bs[k][c] = (gm < mend && q0 + c < p.Q) ? B[(int64_t)gm * p.ldb + q0 + c] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[k][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[k][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  float* W = p.WS + (int64_t)blockIdx.y * p.P * p.Q;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = p0 + ty + 16 * i;
+    if (row >= p.P) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = q0 + tx + 16 * j;
+      if (col < p.Q) W[(int64_t)row * p.Q + col] = acc[i][j] * p.alpha;
+    }
+  }
+}
+
+// C[P,Q] (row stride ldc, fp32) = beta * C + sum_z WS[z]
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, float* C, int64_t ldc,
+                                                             int P, int Q, int nsplit, float beta) {
+  const int64_t total = (int64_t)P * Q;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int z = 0; z < nsplit; ++z) s += ws[z * total + i];
+    const int64_t r = i / Q, c = i % Q;
+    float* dst = C + r * ldc + c;
+    *dst = (beta != 0.f ? beta * *dst : 0.f) + s;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------------------
+template <int BM, int BN>
+static void launch_nt_bf16(const GemmNT& p, int out_dtype, hipStream_t st) {
+  const int nb = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  if (out_dtype == UNOK_BF16)
+    hipLaunchKernelGGL((gemm_nt_bf16_kernel<BM, BN, bf16_t>), dim3(nb), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_nt_bf16_kernel<BM, BN, float>), dim3(nb), dim3(256), 0, st, p);
+}
+
+static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+// C = alpha * gate (.) (A B^T + A2[:, seg_col] B2^T) + R.
+// in_dtype: dtype of A, B, A2, B2; out_dtype: dtype of C and R.
+// seg_end/seg_col: `nseg` (<= 4) extension segments over N (ignored when A2 is null).
+UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
+                             const void* A, int64_t lda, const void* B, int64_t ldb,
+                             const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,
+                             int nseg, const int* seg_end, const int* seg_col,
+                             void* C, int64_t ldc, const void* R, int64_t ldr,
+                             const uint8_t* gate, float alpha, void* stream) {
+  UNOK_REQUIRE(M >= 0 && N >= 0 && K >= 0, UNOK_EINVAL, "gemm_nt: negative size M=%d N=%d K=%d", M, N, K);
+  if (M == 0 || N == 0) return 0;
+  UNOK_REQUIRE(in_dtype == UNOK_F32 || in_dtype == UNOK_BF16, UNOK_EINVAL, "gemm_nt: bad in_dtype %d", in_dtype);
+  UNOK_REQUIRE(out_dtype == UNOK_F32 || out_dtype == UNOK_BF16, UNOK_EINVAL, "gemm_nt: bad out_dtype %d", out_dtype);
+  UNOK_REQUIRE(nseg >= 0 && nseg <= 4, UNOK_EINVAL, "gemm_nt: nseg=%d outside [0,4]", nseg);
+  GemmNT p{};
+  p.A = A; p.lda = lda; p.B = B; p.ldb = ldb;
+  p.A2 = (A2 && K2 > 0) ? A2 : nullptr; p.lda2 = lda2; p.B2 = B2; p.ldb2 = ldb2;
+  p.C = C; p.ldc = ldc; p.R = R; p.ldr = ldr; p.gate = gate;
+  p.M = M; p.N = N; p.K = K; p.K2 = p.A2 ? K2 : 0; p.alpha = alpha;
+  p.nseg = p.A2 ? (nseg > 0 ? nseg : 1) : 1;
+  for (int i = 0; i < 4; ++i) { p.seg_end[i] = N; p.seg_col[i] = 0; }
+  if (p.A2 && nseg > 0) {
+    for (int i = 0; i < nseg; ++i) { p.seg_end[i] = seg_end[i]; p.seg_col[i] = seg_col[i]; }
+    UNOK_REQUIRE(p.seg_end[nseg - 1] == N, UNOK_EINVAL, "gemm_nt: last segment must end at N");
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (in_dtype == UNOK_F32) {
+    // The fp32 kernel uses 64-wide N tiles; segment boundaries must align to them.
+    for (int i = 0; p.A2 && i + 1 < p.nseg; ++i)
+      UNOK_REQUIRE(p.seg_end[i] % 64 == 0, UNOK_EINVAL, "gemm_nt(f32): segment end %d not a multiple of 64", p.seg_end[i]);
+    dim3 grid((N + 63) / 64, (M + 63) / 64);
+    if (out_dtype == UNOK_BF16)
+      hipLaunchKernelGGL((gemm_nt_f32_kernel<bf16_t>), grid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_nt_f32_kernel<float>), grid, dim3(256), 0, st, p);
+    return unok::check_launch("gemm_nt_f32");
+  }
+  // bf16 MFMA path: 16-byte vector loads need K-contiguous rows with 8-element granularity.
+  UNOK_REQUIRE(K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B), UNOK_EALIGN,
+               "gemm_nt(bf16): K=%d lda=%lld ldb=%lld must be multiples of 8 and A/B 16-byte aligned", K,
+               (long long)lda, (long long)ldb);
+  if (p.A2) {
+    UNOK_REQUIRE(K2 % 8 == 0 && lda2 % 8 == 0 && ldb2 % 8 == 0 && aligned16(A2) && aligned16(B2), UNOK_EALIGN,
+                 "gemm_nt(bf16): extension K2=%d lda2=%lld ldb2=%lld must be multiples of 8", K2,
+                 (long long)lda2, (long long)ldb2);
+    for (int i = 0; i < p.nseg; ++i)
+      UNOK_REQUIRE(p.seg_col[i] % 8 == 0, UNOK_EALIGN, "gemm_nt(bf16): segment column %d not a multiple of 8", p.seg_col[i]);
+  }
+  // Tile choice: the largest tile whose N-segment boundaries stay tile-aligned.
+  auto segs_ok = [&](int bn) {
+    for (int i = 0; p.A2 && i + 1 < p.nseg; ++i) if (p.seg_end[i] % bn) return false;
+    return true;
+  };
+  const long long big_tiles = (long long)((M + 255) / 256) * ((N + 255) / 256);
+  if (N <= 64 || !segs_ok(128)) {
+    UNOK_REQUIRE(segs_ok(64), UNOK_EINVAL, "gemm_nt(bf16): segment ends must be multiples of 64");
+    launch_nt_bf16<128, 64>(p, out_dtype, st);
+  } else if (N <= 128 || !segs_ok(256) || big_tiles < 512) {
+    if ((long long)((M + 127) / 128) * ((N + 127) / 128) < 256) launch_nt_bf16<64, 128>(p, out_dtype, st);
+    else launch_nt_bf16<128, 128>(p, out_dtype, st);
+  } else {
+    launch_nt_bf16<256, 256>(p, out_dtype, st);
+  }
+  return unok::check_launch("gemm_nt_bf16");
+}
+
+// Workspace bytes gemm_tn needs for a given problem (partials of the split-K reduction).
+UNOK_EXPORT int64_t unok_gemm_tn_workspace(int Mrows, int P, int Q) {
+  const int64_t tiles = (int64_t)((P + 63) / 64) * ((Q + 63) / 64);
+  int64_t nsplit = (512 + tiles - 1) / tiles;
+  const int64_t max_split = (Mrows + 255) / 256;
+  if (nsplit > max_split) nsplit = max_split;
+  if (nsplit < 1) nsplit = 1;
+  return nsplit * (int64_t)P * Q * 4;
+}
+
+// C[P,Q] (fp32, row stride ldc) = beta * C + alpha * A[Mrows,P]^T B[Mrows,Q]
+UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* A, int64_t lda,
+                             const void* B, int64_t ldb, float* C, int64_t ldc, float alpha, float beta,
+                             void* workspace, int64_t ws_bytes, void* stream) {
+  UNOK_REQUIRE(Mrows >= 0 && P >= 0 && Q >= 0, UNOK_EINVAL, "gemm_tn: negative size");
+  if (P == 0 || Q == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t need = unok_gemm_tn_workspace(Mrows, P, Q);
+  UNOK_REQUIRE(workspace != nullptr && ws_bytes >= need, UNOK_EINVAL,
+               "gemm_tn: workspace of %lld bytes needed, %lld given", (long long)need, (long long)ws_bytes);
+  const int nsplit = (int)(need / ((int64_t)P * Q * 4));
+  int rps = (Mrows + nsplit - 1) / nsplit;
+  rps = ((rps + 63) / 64) * 64;
+  if (rps == 0) rps = 64;
+  const int nz = Mrows > 0 ? (Mrows + rps - 1) / rps : 1;
+  GemmTN p{A, lda, B, ldb, (float*)workspace, Mrows, P, Q, rps, alpha};
+  if (in_dtype == UNOK_F32) {
+    dim3 grid(((P + 63) / 64) * ((Q + 63) / 64), nz);
+    hipLaunchKernelGGL(gemm_tn_f32_kernel, grid, dim3(256), 0, st, p);
+  } else {
+    UNOK_REQUIRE(in_dtype == UNOK_BF16, UNOK_EINVAL, "gemm_tn: bad dtype %d", in_dtype);
+    UNOK_REQUIRE(P % 8 == 0 && Q % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B),
+                 UNOK_EALIGN, "gemm_tn(bf16): P, Q, lda, ldb must be multiples of 8 (P=%d Q=%d)", P, Q);
+    if (P <= Q) {
+      dim3 grid(((P + 63) / 64) * ((Q + 255) / 256), nz);
+      hipLaunchKernelGGL((gemm_tn_bf16_kernel<64, 256>), grid, dim3(256), 0, st, p);
+    } else {
+      dim3 grid(((P + 255) / 256) * ((Q + 63) / 64), nz);
+      hipLaunchKernelGGL((gemm_tn_bf16_kernel<256, 64>), grid, dim3(256), 0, st, p);
+    }
+  }
+  int rc = unok::check_launch("gemm_tn");
+  if (rc) return rc;
+  const int64_t total = (int64_t)P * Q;
+  const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, (const float*)workspace, C, ldc, P, Q, nz, beta);
+  return unok::check_launch("gemm_tn_reduce");
+}
