@@ -1,0 +1,218 @@
+"""Benchmark of the Uno conditional-LoRA block-diffusion training step on one MI355X.
+
+Workload (one "step" = compute_loss + backward + global-norm clip + AdamW over the LoRA tensors):
+Qwen3-8B shape (36 layers, hidden 4096, 32 q / 8 kv heads, head_dim 128, FFN 12288, vocab 151936,
+qk-norm), bf16 frozen base with random N(0, 0.02) weights, LoRA rank 64 / alpha 128 on
+q/k/v/o/gate/up/down, micro-batch 4 x 4096 tokens (512 prompt + 3584 response), block size 16,
+t ~ U(0.05, 1) per block, uniform token ids, objective CE with data targets and 1/t weighting.
+
+Prints ONE JSON line. ``value`` = training tokens/s (B*L input tokens per step, the reference's
+accounting). ``roofline`` = the dominant kernel (256x256 bf16 MFMA GEMM of the fused LoRA
+linears): algorithmic FLOPs per launch / mean launch time, HIP events around every such launch
+in the timed region. ``cpu_baseline`` = the CPU oracle of the same step timed on this host on a
+bounded sample (see cpu_baseline()).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+METRIC = "train tokens/s/GPU, Qwen3-8B cond-LoRA step seq4096 blk16; % bf16 MFMA peak"
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_HBM_GBS = 8000.0
+
+QWEN3_8B = dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
+                num_attention_heads=32, num_key_value_heads=8, head_dim=128)
+WORKLOAD = dict(batch=4, seq_len=4096, prompt=512, block_size=16, lora_rank=64, lora_alpha=128)
+
+
+def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813):
+    from uno_amd.model import UnoQwen3Config, UnoQwen3ForCausalLM
+    from uno_amd.training.config import LoraSettings, UnoObjectiveConfig
+    from uno_amd.training.curriculum import BlockCurriculumPlan
+    from uno_amd.training.lora import create_lora_model
+    from uno_amd.training.trainer import UnoTrainer, UnoTrainingArguments
+
+    cfg = UnoQwen3Config(**cfg_kw, block_size=wl["block_size"], noise_seed=seed)
+    model = UnoQwen3ForCausalLM(cfg, device=device, dtype=torch.bfloat16)
+    model.random_init(seed, std=0.02)
+    lm, _ = create_lora_model(model, LoraSettings("all", wl["lora_rank"], wl["lora_alpha"], 0.0), seed=seed + 1)
+    trainer = UnoTrainer(model=lm, objective=UnoObjectiveConfig(ce_target="ground_truth", ce_weight=1.0,
+                                                                 kl_weight=0.0, tv_weight=0.0),
+                         curriculum=BlockCurriculumPlan.fixed(wl["block_size"], 10 ** 6, wl["seq_len"], wl["batch"]),
+                         args=UnoTrainingArguments(learning_rate=1e-4))
+    g = torch.Generator(device=device).manual_seed(seed + 2)
+    B, L = wl["batch"], wl["seq_len"]
+    ids = torch.randint(0, cfg.vocab_size - 1, (B, L), device=device, generator=g)
+    labels = ids.clone()
+    labels[:, :wl["prompt"]] = -100
+    batch = {"input_ids": ids, "labels": labels, "attention_mask": torch.ones_like(ids)}
+    return model, lm, trainer, batch
+
+
+def algorithmic_flops(cfg: dict, wl: dict, mask, ce_rows: int, r: int) -> dict:
+    """Algorithmically necessary FLOPs of one step from realised counts (recompute excluded):
+    base linears forward on both streams + data gradient of the noisy stream, LoRA forward /
+    dgrad / wgrad on noisy rows, attention over allowed pairs only (forward for both streams,
+    dQ for noisy queries and dK/dV for intra-block pairs), LM head forward + dgrad of CE rows."""
+    H, F, d = cfg["hidden_size"], cfg["intermediate_size"], cfg["head_dim"]
+    q, kv, Lyr, V = cfg["num_attention_heads"] * d, cfg["num_key_value_heads"] * d, cfg["num_hidden_layers"], cfg["vocab_size"]
+    Hq = cfg["num_attention_heads"]
+    n_lin = Lyr * (H * (q + 2 * kv) + q * H + 3 * H * F)
+    n_lora = Lyr * r * ((H + q) + 2 * (H + kv) + (q + H) + 2 * (H + F) + (F + H))
+    T = wl["batch"] * wl["seq_len"]
+    ivc, ivn = mask.iv_clean.long(), mask.iv_noisy.long()
+    p_clean = int((ivc[:, 1] - ivc[:, 0]).sum())
+    p_intra = int((ivn[:, 3] - ivn[:, 2]).sum())
+    p_noisy = int((ivn[:, 1] - ivn[:, 0]).sum()) + p_intra
+    f = {
+        "linear_fwd": 2 * n_lin * 2 * T,
+        "linear_dgrad": 2 * n_lin * T,
+        "lora": 6 * n_lora * T,
+        "attn_fwd": 4 * d * Hq * Lyr * (p_clean + p_noisy),
+        "attn_bwd": (6 * d * Hq * p_noisy + 4 * d * Hq * p_intra) * Lyr,
+        "lm_head": 2 * H * V * ce_rows * 2,
+    }
+    f["total"] = sum(f.values())
+    return f
+
+
+def cpu_baseline(threads: int) -> dict:
+    """CPU oracle (fp32 PyTorch restatement of the reference step) at the Qwen3-8B widths on a
+    bounded sample: one decoder layer and the LM head/CE on one 4096-token sequence (forward and
+    backward), timed separately from a zero-layer run; the full step is extrapolated as
+    4 sequences x (36 x layer + head)."""
+    from oracle import step as ostep
+    from oracle.model import Cfg, init_lora, init_params
+
+    torch.set_num_threads(threads)
+    L, P = WORKLOAD["seq_len"], WORKLOAD["prompt"]
+
+    def run(layers: int) -> float:
+        cfg = Cfg(QWEN3_8B["vocab_size"], QWEN3_8B["hidden_size"], QWEN3_8B["intermediate_size"], layers,
+                  QWEN3_8B["num_attention_heads"], QWEN3_8B["num_key_value_heads"], QWEN3_8B["head_dim"],
+                  lora_rank=WORKLOAD["lora_rank"], lora_alpha=WORKLOAD["lora_alpha"])
+        params = init_params(cfg, seed=0)
+        lora = {k: v.requires_grad_(True) for k, v in init_lora(cfg, seed=1).items()}
+        g = torch.Generator().manual_seed(2)
+        ids = torch.randint(0, cfg.vocab_size - 1, (1, L), generator=g)
+        labels = ids.clone()
+        labels[:, :P] = -100
+        t0 = time.perf_counter()
+        loss, _ = ostep.compute_loss(params, lora, cfg, {"input_ids": ids, "labels": labels},
+                                     ostep.Objective(1, 0, 0, "data"), block_size=WORKLOAD["block_size"],
+                                     mask_token_id=cfg.vocab_size - 1, seed=20260813, step=0)
+        if lora:
+            loss.backward()
+        return time.perf_counter() - t0
+
+    t_head = run(0)
+    t_one = run(1)
+    t_layer = max(t_one - t_head, 0.0)
+    t_step = WORKLOAD["batch"] * (QWEN3_8B["num_hidden_layers"] * t_layer + t_head)
+    tokens = WORKLOAD["batch"] * L
+    return {"value": round(tokens / t_step, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"fp32 CPU oracle, Qwen3-8B widths, 1 x {L} tokens: 1 decoder layer fwd+bwd "
+                       f"({t_layer:.2f} s) and LM head + CE ({t_head:.2f} s); step extrapolated to 36 layers "
+                       f"x {WORKLOAD['batch']} sequences = {t_step:.1f} s"),
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--layers", type=int, default=QWEN3_8B["num_hidden_layers"],
+                    help="decoder layers (the reported workload uses all 36)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported in this build "
+              "(the step is data-parallel across GPUs with only the LoRA gradients exchanged).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from uno_amd import kernels as K
+
+    cfg = dict(QWEN3_8B, num_hidden_layers=args.layers)
+    dev = "cuda:0"
+    model, lm, trainer, batch = build_step(cfg, WORKLOAD, dev)
+    print(f"[bench] model built: {args.layers} layers; warmup {args.warmup} steps", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        trainer.train_step(batch)
+        torch.cuda.synchronize()
+        print(f"[bench] warmup step {i} done", file=sys.stderr, flush=True)
+
+    # realised counts of one step for the FLOP accounting
+    from uno_amd.training.modeling import prepare_uno_layout
+    base = lm.get_base_model()
+    pos, mpos, _ = prepare_uno_layout(base, batch["input_ids"], None)
+    _, _, mask, noised, _, _ = base.prepare_for_bd_training(batch["input_ids"], mpos, batch["labels"] == -100,
+                                                            step=10 ** 6)
+    from uno_amd.training.losses import shift_labels_for_next_token
+    shifted = shift_labels_for_next_token(batch["labels"], pos)
+    ce_rows = int((noised & (shifted != -100)).sum())
+    flops = algorithmic_flops(cfg, WORKLOAD, mask, ce_rows, WORKLOAD["lora_rank"])
+
+    rec = K.LaunchRecorder(lambda dt, M, N, Kd, K2, segs: dt == torch.bfloat16 and K.nt_uses_256_tiles(M, N, segs))
+    torch.cuda.synchronize()
+    K.set_recorder(rec)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        trainer.train_step(batch)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    K.set_recorder(None)
+    ms_step = (t1 - t0) * 1000.0 / args.steps
+    ms, fl = rec.elapsed()
+    tokens = WORKLOAD["batch"] * WORKLOAD["seq_len"]
+    value = tokens / (ms_step / 1000.0)
+    mfu = flops["total"] / (ms_step / 1000.0) / (PEAK_BF16_TFLOPS * 1e12)
+    gemm_ms = sum(ms) / max(len(ms), 1)
+    gemm_tflops = (sum(fl) / max(len(fl), 1)) / (gemm_ms / 1000.0) / 1e12 if ms else 0.0
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (uniform token ids, random N(0,0.02) weights)",
+        "config": {"workload": "Qwen3-8B-shape cond-LoRA block-diffusion step (config 3)",
+                   "layers": args.layers, "global_batch": WORKLOAD["batch"], "seq_len": WORKLOAD["seq_len"],
+                   "block_size": WORKLOAD["block_size"], "lora_rank": WORKLOAD["lora_rank"],
+                   "objective": "CE (data targets, 1/t weights)", "parallelism": "single GPU"},
+        "mfu": round(mfu, 4), "algorithmic_tflop_per_step": round(flops["total"] / 1e12, 2),
+        "flops_breakdown_tflop": {k: round(v / 1e12, 2) for k, v in flops.items() if k != "total"},
+        "roofline": {"kernel": "gemm_nt_bf16_kernel<256,256> (fused LoRA linears)", "bound": "mfma",
+                     "achieved": round(gemm_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "launches": len(ms), "mean_launch_ms": round(gemm_ms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] timing CPU baseline", file=sys.stderr, flush=True)
+        del model, lm, trainer, batch
+        torch.cuda.empty_cache()
+        out["cpu_baseline"] = cpu_baseline(args.cpu_threads)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

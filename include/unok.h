@@ -1,0 +1,184 @@
+/*
+ * unok.h -- C-ABI of the uno_amd kernel library (libunok.so, gfx950 / MI355X).
+ *
+ * The drop-in boundary for Uno's conditional-LoRA block-diffusion training step. The reference
+ * (ifm-ai/uno) has no native code: every hot op of its step runs in library kernels reached from
+ * Python. Each entry point below replaces one of those call sites; the citation after each
+ * declaration names the reference code (file:line) whose semantics it implements.
+ *
+ * Conventions
+ *   - Return 0 on success, a positive hipError_t for a failed launch, or a negative code for an
+ *     argument error (-1 invalid value, -2 alignment, -3 unsupported); unok_last_error() returns
+ *     the message of the calling thread's last failure.
+ *   - Tensors are device pointers with explicit row strides in ELEMENTS (unless named *_bytes);
+ *     dtype codes: 0 = float32, 1 = bfloat16. The caller owns all memory; no entry point
+ *     allocates or frees device memory. All work is enqueued on `stream` (a hipStream_t).
+ *   - Attention masks are per-row key intervals: int32[8] per row =
+ *     {lo1, hi1, lo2, hi2, qlo2, qhi2, 0, segment_length}; source 1 = clean-stream K/V,
+ *     source 2 = noisy-stream K/V; [qlo2, qhi2) = source-2 query rows that see this key row.
+ */
+#ifndef UNOK_H
+#define UNOK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int unok_abi_version(void);
+const char* unok_last_error(void);
+
+/* ---- Linear layers with the token-gated LoRA update fused in ---------------------------- */
+
+/* C = alpha * gate (.) (A[M,K] B[N,K]^T + A2[:, seg_col(n) : +K2] B2[N,K2]^T) + R.
+ * Forward of a LoRA linear: A = x, B = W, A2 = h = m (.) (x A_lora^T), B2 = (alpha/r) B_lora.
+ * Data gradient: A = dY, B = W^T (resident transposed copy), A2 = g, B2 = A_lora^T.
+ * Replaces: PEFT lora.Linear.forward (peft 0.15.2) with the token gate of
+ * training/lora.py:164-174 and the frozen base F.linear of the Qwen3 projections
+ * (transformers/models/qwen3/modeling_qwen3.py:81-82,241-253); LM head of
+ * training/losses.py:30 and training/trainer.py:238-247. */
+int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
+                 const void* A, int64_t lda, const void* B, int64_t ldb,
+                 const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,
+                 int nseg, const int* seg_end, const int* seg_col,
+                 void* C, int64_t ldc, const void* R, int64_t ldr,
+                 const uint8_t* gate, float alpha, void* stream);
+
+/* C[P,Q] (fp32) = beta * C + alpha * A[Mrows,P]^T B[Mrows,Q] (split-K over rows through a
+ * caller workspace of unok_gemm_tn_workspace() bytes). LoRA weight gradients
+ * dB = s dY^T h, dA = g^T x. Replaces: autograd of lora_A / lora_B (peft 0.15.2) under
+ * training/lora.py:83-91 (fp32 adapter weights). */
+int64_t unok_gemm_tn_workspace(int Mrows, int P, int Q);
+int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* A, int64_t lda,
+                 const void* B, int64_t ldb, float* C, int64_t ldc, float alpha, float beta,
+                 void* workspace, int64_t ws_bytes, void* stream);
+
+/* ---- Row-wise decoder ops ----------------------------------------------------------------- */
+
+/* y = w * round(x * rsqrt(mean(x^2) + eps)), rstd[M] saved. Qwen3RMSNorm
+ * (modeling_qwen3.py:50-64); input/post-attention/final norms of the remote decoder. */
+int unok_rmsnorm_fwd(int dtype, int M, int H, const void* x, int64_t ldx, const void* w,
+                     void* y, int64_t ldy, float* rstd, float eps, void* stream);
+/* dx = rstd (g - xhat mean(g xhat)) + dres, g = dy * w. dx may alias dres. */
+int unok_rmsnorm_bwd(int dtype, int M, int H, const void* dy, const void* x, const void* w,
+                     const float* rstd, const void* dres, void* dx, void* stream);
+
+/* Per-head q/k RMSNorm (wq/wk may both be null: RoPE only) then rotate_half RoPE with
+ * angle fl32(pos * inv_freq[i]); writes contiguous q [M, nq*d] and k [M, nk*d].
+ * modeling_qwen3.py:140-160 (rotary), :237-253 (q_norm/k_norm before RoPE). */
+int unok_qknorm_rope_fwd(int dtype, int M, int nq, int nk, int d, const void* qkv, int64_t ld,
+                         const void* wq, const void* wk, const int64_t* pos,
+                         const float* inv_freq, float eps, void* q_out, void* k_out,
+                         float* rstd, void* stream);
+int unok_qknorm_rope_bwd(int dtype, int M, int nq, int nk, int d, const void* dq,
+                         const void* dk, const void* qkv, int64_t ld, const void* wq,
+                         const void* wk, const int64_t* pos, const float* inv_freq,
+                         const float* rstd, void* dqkv, int64_t ldd, void* stream);
+
+/* out = round(silu(gate)) * up over the fused [gate | up] projection (modeling_qwen3.py:81-82). */
+int unok_swiglu_fwd(int dtype, int M, int F, const void* gu, int64_t ld, void* out, void* stream);
+int unok_swiglu_bwd(int dtype, int M, int F, const void* dout, const void* gu, int64_t ld,
+                    void* dgu, int64_t ldd, void* stream);
+
+/* Embedding lookup (remote Qwen3 embed_tokens) and index-mapped row copies (the region
+ * split of training/modeling.py:101-113 and the [noisy|clean] layout of :65-81). */
+int unok_embedding(int elem_bytes, int M, int H, const int64_t* ids, const void* table,
+                   int64_t vocab, void* out, void* stream);
+int unok_rows_copy(int row_bytes, int M, const void* src, int64_t ld_src_bytes,
+                   const int32_t* smap, void* dst, int64_t ld_dst_bytes,
+                   const int32_t* dmap, void* stream);
+
+/* ---- Block-diffusion attention ------------------------------------------------------------- */
+
+/* O = softmax(Q K^T / sqrt(d) over the row's key intervals) V with GQA (q head h -> kv head
+ * h / (Hq/Hkv)); LSE[Mq,Hq] = log2-sum-exp2 of the scaled scores. Replaces torch flex_attention
+ * with the BlockMask of the remote prepare_for_bd_training (training/train.py:142,
+ * training/trainer.py:198-218). */
+int unok_attn_fwd(int dtype, int Mq, int Hq, int Hkv, int D, const void* Q, int64_t ldq,
+                  const void* K1, int64_t ldk1, const void* V1, int64_t ldv1,
+                  const void* K2, int64_t ldk2, const void* V2, int64_t ldv2,
+                  const int32_t* iv, void* O, int64_t ldo, float* LSE, float scale,
+                  void* stream);
+/* dQ for every query; dK/dV for the source-2 keys when dK/dV are non-null (source-1 keys are
+ * the detached clean stream). Dsum [Mq,Hq] fp32 is caller scratch. */
+int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D, const void* Q, int64_t ldq,
+                  const void* K1, int64_t ldk1, const void* V1, int64_t ldv1,
+                  const void* K2, int64_t ldk2, const void* V2, int64_t ldv2,
+                  const int32_t* iv, const int32_t* ivk, const void* O, int64_t ldo,
+                  const float* LSE, const void* dO, int64_t lddo, float* Dsum,
+                  void* dQ, int64_t lddq, void* dK, int64_t lddk, void* dV, int64_t lddv,
+                  float scale, void* stream);
+
+/* ---- Block-diffusion batch preparation ----------------------------------------------------- */
+
+/* Noising, [noisy | clean] concatenation, stream maps and interval tables of one batch.
+ * The model-side contract of prepare_for_bd_training (call site training/trainer.py:198-209;
+ * region layout training/modeling.py:65-81; uniform replacement range [1, mask_id) of
+ * nano_vllm_uno/engine/noise.py:24-26). */
+int unok_bd_prepare(int B, int L, const int64_t* ids, const int64_t* pos, const uint8_t* prompt,
+                    int block_size, int mask_id, int noise_mask_mode, int intra_causal,
+                    uint64_t key, int64_t* concat_ids, int64_t* concat_pos, uint8_t* region,
+                    uint8_t* noised, float* tfull, int32_t* noisy_src, int32_t* clean_src,
+                    int32_t* noisy_iv, int32_t* clean_iv, int64_t* noisy_ids,
+                    int64_t* clean_ids, void* stream);
+/* p_mask = noise level of every noised token in row-major order (training/trainer.py:278). */
+int unok_bd_compact(int64_t n, const uint8_t* noised, const float* tfull, float* p_mask,
+                    int32_t* count, void* stream);
+
+/* ---- Objectives ------------------------------------------------------------------------------ */
+
+/* Chunked LM-head cross-entropy with 1/t row weights (training/trainer.py:267-283): per vocab
+ * chunk, merge running (max, sum-exp) and capture the target logit; then the weighted sum. */
+int unok_row_lse_update(int dtype, int R, int Vc, const void* z, int64_t ldz, int c0,
+                        const int64_t* tgt, float* run_max, float* run_sum, float* zt,
+                        int first, void* stream);
+int unok_ce_finish(int R, const float* run_max, const float* run_sum, const float* zt,
+                   const float* w, const float* inv_n, float* lse, float* loss, void* stream);
+int unok_ce_grad_chunk(int out_dtype, int R, int Vc, const float* z, int64_t ldz, int c0,
+                       const float* lse, const int64_t* tgt, const float* w, const float* gscale,
+                       const float* inv_n, void* dz, int64_t lddz, void* stream);
+/* First-index argmax over vocab chunks: the "clean_argmax" CE target (training/losses.py:38-56). */
+int unok_row_argmax_update(int dtype, int R, int Vc, const void* z, int64_t ldz, int c0,
+                           float* best_val, int64_t* best_idx, int first, void* stream);
+/* Total variation / reverse KL over full-vocabulary logits (training/losses.py:59-183). */
+int unok_softmax_stats(int dtype, int R, int V, const void* z, int64_t ldz, float* mx, float* se,
+                       void* stream);
+int unok_tv_fwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
+                const float* ms, const float* ss, const float* mt, const float* st,
+                float* row_l1, float* row_S, void* stream);
+int unok_tv_bwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
+                const float* ms, const float* ss, const float* mt, const float* st,
+                const float* row_S, const float* gscale, const float* inv_n, void* grad,
+                int64_t ldg, void* stream);
+int unok_kl_fwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
+                const float* ms, const float* ss, const float* mt, const float* st,
+                float* row_kl, void* stream);
+int unok_kl_bwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
+                const float* ms, const float* ss, const float* mt, const float* st,
+                const float* row_kl, const float* gscale, const float* inv_n, void* grad,
+                int64_t ldg, void* stream);
+int unok_sum_scaled(int64_t n, const float* x, const float* inv_n, float* out, void* stream);
+
+/* ---- Optimizer ------------------------------------------------------------------------------- */
+
+/* Global L2 norm of the flat LoRA gradient and clip coefficient min(1, max/(norm+1e-6))
+ * (torch.nn.utils.clip_grad_norm_ with max_grad_norm=1.0, training/train.py:287). */
+int unok_grad_clip_coef(int64_t n, const float* g, float* partials, int nparts, float max_norm,
+                        float* clip_out, void* stream);
+/* torch.optim.AdamW step over the flat LoRA state (training/train.py:282-288), refreshing the
+ * compute copy (B range scaled by alpha/r). */
+int unok_adamw_step(int64_t n, float* p, float* g, float* m, float* v, const float* clip,
+                    float lr, float beta1, float beta2, float eps, float weight_decay, int step,
+                    int copy_dtype, void* copy, int64_t n_unscaled, float copy_scale,
+                    void* stream);
+int unok_cast_copy(int copy_dtype, int64_t n, int64_t n_unscaled, float scale, const float* p,
+                   void* copy, void* stream);
+int unok_transpose_jobs(int dtype, const int64_t* jobs, int njobs, int64_t total_tiles,
+                        const void* src, void* dst, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UNOK_H */

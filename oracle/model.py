@@ -74,6 +74,7 @@ def lora_linear(x, W, A, B, gate, scale):
     y = x @ W.T
     if A is None:
         return y
+    A, B = A.to(x.dtype), B.to(x.dtype)   # adapters compute in the activation dtype
     h = x @ A.T
     if gate is not None:
         h = h * gate.to(h.dtype)[..., None]
@@ -88,7 +89,9 @@ def decoder(params: dict, lora: dict, cfg: Cfg, ids: torch.Tensor, pos: torch.Te
     s = cfg.lora_scale
     h = params["model.embed_tokens.weight"][ids]
     cos, sin = rope_cos_sin(pos, d, cfg.rope_theta)
-    cos, sin = cos[:, None], sin[:, None]  # [B,1,T,d]
+    # cos/sin are cast to the activation dtype as in Qwen3RotaryEmbedding (no-op in fp32)
+    dt = params["model.embed_tokens.weight"].dtype
+    cos, sin = cos[:, None].to(dt), sin[:, None].to(dt)  # [B,1,T,d]
     bias = torch.zeros(mask.shape, dtype=torch.float32).masked_fill(~mask, float("-inf"))[:, None]
 
     def lin(i, name, x):
@@ -112,7 +115,8 @@ def decoder(params: dict, lora: dict, cfg: Cfg, ids: torch.Tensor, pos: torch.Te
         k = k.repeat_interleave(rep, dim=1)
         v = v.repeat_interleave(rep, dim=1)
         scores = (q @ k.transpose(-1, -2)) * d ** -0.5 + bias
-        attn = torch.softmax(scores, dim=-1) @ v
+        # softmax in fp32 then back to the activation dtype (eager Qwen3 attention)
+        attn = torch.softmax(scores.float() if scores.dtype != torch.float64 else scores, dim=-1).to(q.dtype) @ v
         attn = attn.transpose(1, 2).reshape(Bsz, T, Hq * d)
         h = h + lin(i, "o_proj", attn)
         x = rms_norm(h, params[pre + "post_attention_layernorm.weight"], cfg.rms_norm_eps)

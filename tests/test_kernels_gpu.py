@@ -1,0 +1,306 @@
+"""GPU parity of the row-wise, attention, loss, optimizer and batch-preparation kernels.
+
+Each HIP kernel is compared with a plain fp32 PyTorch restatement of the same op (or with the
+CPU oracle for the bit-exact integer work)."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import bd as obd
+from oracle import layout as olay
+from oracle import losses as olosses
+from uno_amd import kernels as K
+from uno_amd.model import bd_prepare
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    return ((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30)).item()
+
+
+def cos(a, b):
+    return F.cosine_similarity(a.float().flatten(), b.float().flatten(), dim=0).item()
+
+
+# ------------------------------------------------------------------------------------------
+# RMSNorm / qk-norm + RoPE / SwiGLU
+# ------------------------------------------------------------------------------------------
+def ref_rmsnorm(x, w, eps):
+    xf = x.float()
+    return w.float() * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps))
+
+
+@pytest.mark.parametrize("dtype,M,H", [(torch.float32, 37, 256), (torch.bfloat16, 300, 4096), (torch.bfloat16, 5, 2048)])
+def test_rmsnorm_fwd_bwd(dev, dtype, M, H):
+    torch.manual_seed(0)
+    x = torch.randn(M, H, device=dev).to(dtype)
+    w = (1 + 0.1 * torch.randn(H, device=dev)).to(dtype)
+    y, rstd = K.rmsnorm_fwd(x, w, 1e-6)
+    xr = x.float().clone().requires_grad_(True)
+    yr = ref_rmsnorm(xr, w, 1e-6)
+    tol = 1e-6 if dtype == torch.float32 else 8e-3
+    assert rel(y, yr) < tol
+    dy = torch.randn(M, H, device=dev).to(dtype)
+    dres = torch.randn(M, H, device=dev).to(dtype)
+    yr.backward(dy.float())
+    dx = K.rmsnorm_bwd(dy, x, w, rstd, dres=dres)
+    assert rel(dx, xr.grad + dres.float()) < (1e-5 if dtype == torch.float32 else 8e-3)
+
+
+def ref_qknorm_rope(qkv, nq, nk, d, wq, wk, pos, theta, eps):
+    M = qkv.shape[0]
+    q = qkv[:, :nq * d].float().view(M, nq, d)
+    k = qkv[:, nq * d:(nq + nk) * d].float().view(M, nk, d)
+    if wq is not None:
+        q = ref_rmsnorm(q, wq, eps)
+        k = ref_rmsnorm(k, wk, eps)
+    inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))
+    fr = pos.float().cpu()[:, None] * inv
+    emb = torch.cat([fr, fr], -1).to(qkv.device)
+    c, s = emb.cos()[:, None], emb.sin()[:, None]
+
+    def rot(x):
+        return torch.cat([-x[..., d // 2:], x[..., :d // 2]], -1)
+    return (q * c + rot(q) * s).reshape(M, -1), (k * c + rot(k) * s).reshape(M, -1)
+
+
+@pytest.mark.parametrize("dtype,d,norm", [(torch.float32, 64, True), (torch.bfloat16, 128, True),
+                                          (torch.bfloat16, 128, False)])
+def test_qknorm_rope_fwd_bwd(dev, dtype, d, norm):
+    torch.manual_seed(1)
+    M, nq, nk, theta = 96, 4, 2, 1e6
+    qkv = torch.randn(M, (nq + 2 * nk) * d, device=dev).to(dtype)
+    wq = (1 + 0.1 * torch.randn(d, device=dev)).to(dtype) if norm else None
+    wk = (1 + 0.1 * torch.randn(d, device=dev)).to(dtype) if norm else None
+    pos = torch.randint(0, 16384, (M,), device=dev)
+    inv = (1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))).to(dev)
+    q, k, rstd = K.qknorm_rope_fwd(qkv, nq, nk, d, wq, wk, pos, inv, 1e-6)
+    x = qkv.float().clone().requires_grad_(True)
+    qr, kr = ref_qknorm_rope(x, nq, nk, d, wq, wk, pos, theta, 1e-6)
+    tol = 2e-5 if dtype == torch.float32 else 1e-2
+    assert rel(q, qr) < tol and rel(k, kr) < tol
+    dq = torch.randn_like(q)
+    dk = torch.randn_like(k)
+    (qr * dq.float()).sum().add_((kr * dk.float()).sum()).backward()
+    dqkv = torch.zeros_like(qkv)
+    K.qknorm_rope_bwd(dq, dk, qkv, nq, nk, d, wq, wk, pos, inv, rstd, dqkv)
+    e = (nq + nk) * d
+    assert rel(dqkv[:, :e], x.grad[:, :e]) < (5e-5 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_swiglu_fwd_bwd(dev, dtype):
+    torch.manual_seed(2)
+    M, Fd = 77, 768
+    gu = torch.randn(M, 2 * Fd, device=dev).to(dtype)
+    x = gu.float().clone().requires_grad_(True)
+    ref = F.silu(x[:, :Fd]) * x[:, Fd:]
+    out = K.swiglu_fwd(gu, Fd)
+    assert rel(out, ref) < (1e-6 if dtype == torch.float32 else 8e-3)
+    d = torch.randn(M, Fd, device=dev).to(dtype)
+    ref.backward(d.float())
+    dgu = K.swiglu_bwd(d, gu, Fd)
+    assert rel(dgu, x.grad) < (1e-5 if dtype == torch.float32 else 1e-2)
+
+
+def test_embedding_and_rows_copy(dev):
+    torch.manual_seed(3)
+    table = torch.randn(1000, 256, device=dev).bfloat16()
+    ids = torch.randint(0, 1000, (333,), device=dev)
+    assert torch.equal(K.embedding(ids, table), table[ids])
+    src = torch.randn(50, 128, device=dev)
+    perm = torch.randperm(50, device=dev).to(torch.int32)
+    dst = torch.zeros(50, 128, device=dev)
+    K.rows_copy(src, dst, 50, dmap=perm)
+    assert torch.equal(dst[perm.long()], src)
+    out = torch.zeros(50, 128, device=dev)
+    K.rows_copy(src, out, 50, smap=perm)
+    assert torch.equal(out, src[perm.long()])
+
+
+# ------------------------------------------------------------------------------------------
+# Batch preparation: bit-exact against the oracle contract
+# ------------------------------------------------------------------------------------------
+def _batch(B, L, V, prompt, seed, packed=False):
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, V - 1, (B, L), generator=g)
+    labels = ids.clone()
+    labels[:, :prompt] = -100
+    pos = torch.arange(L)[None].repeat(B, 1)
+    if packed:
+        cuts = [0, L // 3, L // 3 + L // 5, L]
+        for b in range(1, B):
+            for a, c in zip(cuts[:-1], cuts[1:]):
+                pos[b, a:c] = torch.arange(c - a)
+                labels[b, a:a + max(1, (c - a) // 10)] = -100
+    return ids, labels, pos
+
+
+@pytest.mark.parametrize("L,bs,packed,noise", [(64, 4, False, "uniform"), (96, 6, True, "uniform"),
+                                               (256, 16, True, "mask"), (4096, 16, False, "uniform")])
+def test_bd_prepare_bit_exact(dev, L, bs, packed, noise):
+    B, V = 3, 4096
+    ids, labels, pos = _batch(B, L, V, L // 8, seed=L + bs, packed=packed)
+    prompt = labels == -100
+    out = bd_prepare(ids.to(dev), pos.to(dev), prompt.to(dev), block_size=bs, mask_token_id=V - 1, noise=noise,
+                     seed=20260813, step=5)
+    cids, cpos, mask, noised, tfull, p_mask = out
+    ref = obd.prepare_for_bd_training(ids, pos, prompt, block_size=bs, mask_token_id=V - 1, seed=20260813,
+                                      step=5, noise=noise)
+    assert torch.equal(cids.cpu(), ref[0])
+    assert torch.equal(cpos.cpu(), ref[1])
+    assert torch.equal(noised.cpu(), ref[3])
+    assert torch.equal(tfull.cpu().view(torch.int32), ref[4].view(torch.int32))       # bit-exact floats
+    assert torch.equal(p_mask.cpu().view(torch.int32), ref[5].view(torch.int32))
+    _, _, region = olay.prepare_uno_layout(ids, pos)
+    assert torch.equal(mask.region.cpu(), region)
+    if L <= 256:
+        assert torch.equal(mask.to_dense(), ref[2])
+
+
+# ------------------------------------------------------------------------------------------
+# Attention: two-stream kernels against dense attention over the oracle's mask
+# ------------------------------------------------------------------------------------------
+def _dense_attn(q, k, v, allow, D):
+    """q [Mq,Hq,D], k/v [Mk,Hkv,D] fp32, allow [Mq,Mk] bool -> O [Mq,Hq,D], lse2 [Mq,Hq]."""
+    rep = q.shape[1] // k.shape[1]
+    k = k.repeat_interleave(rep, 1).permute(1, 2, 0).contiguous()     # [Hq, D, Mk]
+    v = v.repeat_interleave(rep, 1).permute(1, 0, 2).contiguous()     # [Hq, Mk, D]
+    qh = q.permute(1, 0, 2).contiguous()                              # [Hq, Mq, D]
+    s = torch.matmul(qh, k) * D ** -0.5
+    s = s.masked_fill(~allow[None], float("-inf"))
+    o = torch.matmul(torch.softmax(s, -1), v).permute(1, 0, 2)
+    lse2 = torch.logsumexp(s, -1).T / math.log(2.0)
+    return o, lse2
+
+
+@pytest.mark.parametrize("dtype,D,L,bs,packed", [(torch.bfloat16, 128, 256, 16, False),
+                                                 (torch.bfloat16, 128, 320, 6, True),
+                                                 (torch.bfloat16, 64, 192, 12, True),
+                                                 (torch.float32, 64, 128, 4, True)])
+def test_block_diffusion_attention(dev, dtype, D, L, bs, packed):
+    torch.manual_seed(4)
+    B, Hq, Hkv = 2, 4, 2
+    ids, labels, pos = _batch(B, L, 512, 8, seed=7, packed=packed)
+    _, _, mask, _, _, _ = bd_prepare(ids.to(dev), pos.to(dev), (labels == -100).to(dev), block_size=bs,
+                                     mask_token_id=511)
+    M = B * L
+    dense = obd.dense_mask(pos, bs)                       # oracle mask over the concat layout
+    ns, cs = mask.noisy_src.long().cpu(), mask.clean_src.long().cpu()
+    full = torch.zeros(B * 2 * L, B * 2 * L, dtype=torch.bool)
+    for b in range(B):
+        full[b * 2 * L:(b + 1) * 2 * L, b * 2 * L:(b + 1) * 2 * L] = dense[b]
+    allow_c = full[cs[:, None], cs[None, :]].to(dev)                                  # clean q -> clean k
+    allow_n = torch.cat([full[ns[:, None], cs[None, :]], full[ns[:, None], ns[None, :]]], 1).to(dev)
+    qc, qn = (torch.randn(M, Hq, D, device=dev).to(dtype) for _ in range(2))
+    kc, vc, kn, vn = (torch.randn(M, Hkv, D, device=dev).to(dtype) for _ in range(4))
+    flat = lambda t: t.reshape(M, -1)
+    oc, lc = K.attn_fwd(flat(qc), flat(kc), flat(vc), mask.iv_clean, Hq, Hkv, D)
+    on, ln = K.attn_fwd(flat(qn), flat(kc), flat(vc), mask.iv_noisy, Hq, Hkv, D, k2=flat(kn), v2=flat(vn))
+    ref_oc, ref_lc = _dense_attn(qc.float(), kc.float(), vc.float(), allow_c, D)
+    qn_r, kn_r, vn_r = (t.float().clone().requires_grad_(True) for t in (qn, kn, vn))
+    ref_on, ref_ln = _dense_attn(qn_r, torch.cat([kc.float(), kn_r]), torch.cat([vc.float(), vn_r]), allow_n, D)
+    tol = 1e-5 if dtype == torch.float32 else 1.2e-2
+    assert rel(oc, flat(ref_oc)) < tol and rel(on, flat(ref_on)) < tol
+    assert (lc - ref_lc).abs().max().item() < (1e-4 if dtype == torch.float32 else 2e-2)
+    assert (ln - ref_ln).abs().max().item() < (1e-4 if dtype == torch.float32 else 2e-2)
+    do = torch.randn(M, Hq * D, device=dev).to(dtype)
+    (flat(ref_on) * do.float()).sum().backward()
+    dk = torch.empty(M, Hkv * D, device=dev, dtype=dtype)
+    dv = torch.empty(M, Hkv * D, device=dev, dtype=dtype)
+    dq = K.attn_bwd(flat(qn), flat(kc), flat(vc), mask.iv_noisy, on, ln, do, Hq, Hkv, D, k2=flat(kn), v2=flat(vn),
+                    ivk=mask.iv_noisy, dk=dk, dv=dv)
+    gtol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert rel(dq, flat(qn_r.grad)) < gtol
+    assert rel(dk, flat(kn_r.grad)) < gtol
+    assert rel(dv, flat(vn_r.grad)) < gtol
+
+
+# ------------------------------------------------------------------------------------------
+# Objectives
+# ------------------------------------------------------------------------------------------
+class _Head:
+    def __init__(self, w):
+        self.weight = w
+        self.weight_t = w.t().contiguous()
+
+
+@pytest.mark.parametrize("dtype,R,H,V,chunk", [(torch.float32, 50, 64, 5000, 2048),
+                                               (torch.bfloat16, 300, 256, 8192, 3000),
+                                               (torch.bfloat16, 1000, 512, 151936, 16384)])
+def test_chunked_weighted_ce(dev, dtype, R, H, V, chunk):
+    from uno_amd.objectives import fused_weighted_ce, teacher_argmax
+    torch.manual_seed(5)
+    h = (torch.randn(R, H, device=dev) * 0.5).to(dtype)
+    w = (torch.randn(V, H, device=dev) * 0.05).to(dtype)
+    y = torch.randint(0, V, (R,), device=dev)
+    p = torch.rand(R, device=dev) * 0.95 + 0.05
+    inv_n = torch.tensor(1.0 / 777, device=dev)
+    hr = h.float().clone().requires_grad_(True)
+    logits = hr @ w.float().T
+    ref = (F.cross_entropy(logits, y, reduction="none") / p).sum() / 777
+    ref.backward()
+    hh = h.clone().requires_grad_(True)
+    loss = fused_weighted_ce(_Head(w), hh, y, 1.0 / p, inv_n, chunk=chunk)
+    loss.backward()
+    assert abs(loss.item() - ref.item()) / abs(ref.item()) < (1e-5 if dtype == torch.float32 else 1e-3)
+    assert rel(hh.grad, hr.grad) < (1e-4 if dtype == torch.float32 else 1e-2)
+    am = teacher_argmax(_Head(w), h, chunk=chunk)
+    lg = (h.float() @ w.float().T) if dtype == torch.float32 else (h.float() @ w.float().T).bfloat16().float()
+    assert (am == lg.argmax(-1)).float().mean().item() > (0.999 if dtype == torch.float32 else 0.98)
+
+
+@pytest.mark.parametrize("kind", ["tv", "kl"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_distribution_losses_match_oracle(dev, kind, dtype):
+    from uno_amd.training.losses import token_normalized_reverse_kl, token_normalized_total_variation
+    torch.manual_seed(6)
+    R, V = 40, 4099
+    s = (torch.randn(R, V, device=dev) * 2).to(dtype)
+    t = (torch.randn(R, V, device=dev) * 2).to(dtype)
+    t[3] = s[3]
+    sv = s.clone().requires_grad_(True)
+    fn = token_normalized_total_variation if kind == "tv" else token_normalized_reverse_kl
+    val = fn(sv, t, 17)
+    val.backward()
+    so = s.float().cpu().requires_grad_(True)
+    ref = (olosses.total_variation if kind == "tv" else olosses.reverse_kl)(so, t.float().cpu(), 17)
+    ref.backward()
+    assert abs(val.item() - ref.item()) / abs(ref.item()) < (1e-5 if dtype == torch.float32 else 1e-4)
+    assert rel(sv.grad.cpu(), so.grad) < (1e-4 if dtype == torch.float32 else 1e-2)
+
+
+# ------------------------------------------------------------------------------------------
+# Optimizer
+# ------------------------------------------------------------------------------------------
+def test_fused_adamw_matches_torch(dev):
+    from uno_amd import _native as N
+    torch.manual_seed(7)
+    n = 100_003
+    p0 = torch.randn(n, device=dev)
+    parts = [slice(0, 40_000), slice(40_000, 100_003)]
+    ref = [p0[s].clone().requires_grad_(True) for s in parts]
+    opt = torch.optim.AdamW(ref, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    p, m, v = p0.clone(), torch.zeros(n, device=dev), torch.zeros(n, device=dev)
+    partial = torch.empty(256, device=dev)
+    clip = torch.empty(2, device=dev)
+    copy = torch.empty(n, device=dev, dtype=torch.bfloat16)
+    for step in range(1, 4):
+        g = torch.randn(n, device=dev) * (0.02 if step < 3 else 3.0)
+        for t, s in zip(ref, parts):
+            t.grad = g[s].clone()
+        torch.nn.utils.clip_grad_norm_(ref, 1.0)
+        opt.step()
+        gg = g.clone()
+        N.call("unok_grad_clip_coef", n, N.ptr(gg), N.ptr(partial), 256, 1.0, N.ptr(clip), N.stream())
+        N.call("unok_adamw_step", n, N.ptr(p), N.ptr(gg), N.ptr(m), N.ptr(v), N.ptr(clip), 1e-3, 0.9, 0.999, 1e-8,
+               0.01, step, N.BF16, N.ptr(copy), 40_000, 2.0, N.stream())
+        assert abs(clip[0].item() - g.norm().item()) / g.norm().item() < 1e-5
+    mine = torch.cat([p[s] for s in parts])
+    theirs = torch.cat([t.detach() for t in ref])
+    assert (mine - theirs).abs().max().item() < 1e-6
+    assert torch.equal(copy[:40_000], p[:40_000].bfloat16())
+    assert torch.equal(copy[40_000:], (p[40_000:] * 2.0).bfloat16())

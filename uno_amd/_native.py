@@ -17,6 +17,7 @@ F32, BF16 = 0, 1
 _EINVAL, _EALIGN, _EUNSUPPORTED = -1, -2, -3
 
 _i, _i64, _p, _f = C.c_int, C.c_int64, C.c_void_p, C.c_float
+_u64 = C.c_uint64
 _ip = C.POINTER(C.c_int)
 
 # name -> (restype, argtypes); must match include/unok.h exactly.
@@ -27,6 +28,35 @@ SIGNATURES: dict[str, tuple] = {
                           _i, _ip, _ip, _p, _i64, _p, _i64, _p, _f, _p]),
     "unok_gemm_tn_workspace": (_i64, [_i, _i, _i]),
     "unok_gemm_tn": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _f, _f, _p, _i64, _p]),
+    "unok_rmsnorm_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _p, _i64, _p, _f, _p]),
+    "unok_rmsnorm_bwd": (_i, [_i, _i, _i, _p, _p, _p, _p, _p, _p, _p]),
+    "unok_qknorm_rope_fwd": (_i, [_i, _i, _i, _i, _i, _p, _i64, _p, _p, _p, _p, _f, _p, _p, _p, _p]),
+    "unok_qknorm_rope_bwd": (_i, [_i, _i, _i, _i, _i, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "unok_swiglu_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _p]),
+    "unok_swiglu_bwd": (_i, [_i, _i, _i, _p, _p, _i64, _p, _i64, _p]),
+    "unok_embedding": (_i, [_i, _i, _i, _p, _p, _i64, _p, _p]),
+    "unok_rows_copy": (_i, [_i, _i, _p, _i64, _p, _p, _i64, _p, _p]),
+    "unok_attn_fwd": (_i, [_i, _i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
+                           _p, _p, _i64, _p, _f, _p]),
+    "unok_attn_bwd": (_i, [_i, _i, _i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
+                           _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _f, _p]),
+    "unok_bd_prepare": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _u64, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                             _p, _p, _p]),
+    "unok_bd_compact": (_i, [_i64, _p, _p, _p, _p, _p]),
+    "unok_row_lse_update": (_i, [_i, _i, _i, _p, _i64, _i, _p, _p, _p, _p, _i, _p]),
+    "unok_row_argmax_update": (_i, [_i, _i, _i, _p, _i64, _i, _p, _p, _i, _p]),
+    "unok_ce_finish": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p]),
+    "unok_ce_grad_chunk": (_i, [_i, _i, _i, _p, _i64, _i, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "unok_softmax_stats": (_i, [_i, _i, _i, _p, _i64, _p, _p, _p]),
+    "unok_tv_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p]),
+    "unok_tv_bwd": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "unok_kl_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p]),
+    "unok_kl_bwd": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "unok_sum_scaled": (_i, [_i64, _p, _p, _p, _p]),
+    "unok_grad_clip_coef": (_i, [_i64, _p, _p, _i, _f, _p, _p]),
+    "unok_adamw_step": (_i, [_i64, _p, _p, _p, _p, _p, _f, _f, _f, _f, _f, _i, _i, _p, _i64, _f, _p]),
+    "unok_cast_copy": (_i, [_i, _i64, _i64, _f, _p, _p, _p]),
+    "unok_transpose_jobs": (_i, [_i, _p, _i, _i64, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,162 @@
+"""Flat storage of all LoRA adapters of a model (MI355X-first layout).
+
+Every ``lora_A`` / ``lora_B`` tensor (PEFT shapes: A [r, in], B [out, r], fp32 master weights as
+in training/lora.py:83-91) is a view into ONE flat fp32 buffer; gradients, AdamW moments and
+the compute copies are parallel buffers with the same layout. The layout is
+
+    [ A region: per layer  A_q A_k A_v A_o A_gate A_up A_down ]
+    [ B region: per layer  B_q B_k B_v B_o B_gate B_up B_down ]
+
+so that each fused projection's adapters are contiguous (A_qkv = [A_q; A_k; A_v] is a [3r, H]
+matrix; B_qkv = [B_q; B_k; B_v] is [q+2kv, r]), the optimizer is one flat pass, and the
+compute copy (B scaled by alpha/r) is refreshed by that same pass. Transposed compute copies
+(A^T per group, (sB)^T per group) feed the data-gradient GEMMs and are rebuilt by one batched
+transpose launch after every update.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as N
+
+MODULES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+GROUPS = {"qkv": ("q_proj", "k_proj", "v_proj"), "o": ("o_proj",), "gu": ("gate_proj", "up_proj"),
+          "d": ("down_proj",)}
+
+
+def module_dims(cfg) -> dict[str, tuple[int, int]]:
+    """(out, in) per projection."""
+    H, d = cfg.hidden_size, cfg.head_dim
+    q, kv, f = cfg.num_attention_heads * d, cfg.num_key_value_heads * d, cfg.intermediate_size
+    return {"q_proj": (q, H), "k_proj": (kv, H), "v_proj": (kv, H), "o_proj": (H, q),
+            "gate_proj": (f, H), "up_proj": (f, H), "down_proj": (H, f)}
+
+
+@dataclass
+class _Slot:
+    a_off: int
+    b_off: int
+    out: int
+    inp: int
+
+
+class LoraState:
+    def __init__(self, cfg, rank: int, alpha: float, device, compute_dtype: torch.dtype,
+                 targets=MODULES):
+        if tuple(sorted(targets)) != tuple(sorted(MODULES)):
+            raise NotImplementedError(
+                "The fused MI355X path adapts all seven projections (q,k,v,o,gate,up,down); "
+                f"got targets {tuple(targets)}.")
+        self.cfg = cfg
+        self.rank = int(rank)
+        self.alpha = float(alpha)
+        self.scale = self.alpha / self.rank
+        self.targets = tuple(MODULES)
+        self.compute_dtype = compute_dtype
+        self.device = torch.device(device)
+        dims = module_dims(cfg)
+        r = self.rank
+        self.slots: list[dict[str, _Slot]] = []
+        a = 0
+        for _ in range(cfg.num_hidden_layers):
+            layer = {}
+            for name in MODULES:
+                out, inp = dims[name]
+                layer[name] = _Slot(a, 0, out, inp)
+                a += r * inp
+            self.slots.append(layer)
+        self.n_a = a
+        b = a
+        for layer in self.slots:
+            for name in MODULES:
+                layer[name].b_off = b
+                b += layer[name].out * r
+        self.numel = b
+        f32 = dict(device=self.device, dtype=torch.float32)
+        self.master = torch.zeros(self.numel, **f32)
+        self.grad = torch.zeros(self.numel, **f32)
+        self.exp_avg = torch.zeros(self.numel, **f32)
+        self.exp_avg_sq = torch.zeros(self.numel, **f32)
+        self.copy = torch.empty(self.numel, device=self.device, dtype=compute_dtype)
+        self.copy_t = torch.empty(self.numel, device=self.device, dtype=compute_dtype)
+        self.step = 0
+        self._build_transpose_jobs()
+        # autograd anchor: the decoder's stream Functions take it as an input so that backward
+        # runs; the LoRA gradients are accumulated straight into ``grad`` by the kernels.
+        self.anchor = torch.zeros(1, **f32).requires_grad_(True)
+
+    # ---- views of the fp32 master / grad ----------------------------------------------
+    def a_view(self, buf: torch.Tensor, layer: int, name: str) -> torch.Tensor:
+        s = self.slots[layer][name]
+        return buf[s.a_off:s.a_off + self.rank * s.inp].view(self.rank, s.inp)
+
+    def b_view(self, buf: torch.Tensor, layer: int, name: str) -> torch.Tensor:
+        s = self.slots[layer][name]
+        return buf[s.b_off:s.b_off + s.out * self.rank].view(s.out, self.rank)
+
+    def group_a(self, buf: torch.Tensor, layer: int, group: str) -> torch.Tensor:
+        names = GROUPS[group]
+        first = self.slots[layer][names[0]]
+        rows = self.rank * len(names)
+        return buf[first.a_off:first.a_off + rows * first.inp].view(rows, first.inp)
+
+    def group_b(self, buf: torch.Tensor, layer: int, group: str) -> torch.Tensor:
+        names = GROUPS[group]
+        first = self.slots[layer][names[0]]
+        rows = sum(self.slots[layer][n].out for n in names)
+        return buf[first.b_off:first.b_off + rows * self.rank].view(rows, self.rank)
+
+    # ---- transposed compute copies ------------------------------------------------------
+    def _build_transpose_jobs(self):
+        jobs = []
+        self._t_views = []
+        tile = 0
+        for li in range(len(self.slots)):
+            views = {}
+            for g in GROUPS:
+                for kind in ("a", "b"):
+                    src = self.group_a(self.copy, li, g) if kind == "a" else self.group_b(self.copy, li, g)
+                    rows, cols = src.shape
+                    src_off = src.storage_offset() - self.copy.storage_offset()
+                    dst_off = src_off   # same footprint, transposed shape
+                    jobs.append([src_off, rows, cols, dst_off, tile, 0, 0, 0])
+                    tile += ((rows + 63) // 64) * ((cols + 63) // 64)
+                    views[(g, kind)] = self.copy_t[dst_off:dst_off + rows * cols].view(cols, rows)
+            self._t_views.append(views)
+        self._jobs = torch.tensor(jobs, dtype=torch.int64, device=self.device)
+        self._tiles = tile
+
+    def a_t(self, layer: int, group: str) -> torch.Tensor:
+        """A_group^T [in, rows] compute copy."""
+        return self._t_views[layer][(group, "a")]
+
+    def sb_t(self, layer: int, group: str) -> torch.Tensor:
+        """(s * B_group)^T [r, out_rows] compute copy."""
+        return self._t_views[layer][(group, "b")]
+
+    def a_c(self, layer: int, group: str) -> torch.Tensor:
+        return self.group_a(self.copy, layer, group)
+
+    def sb_c(self, layer: int, group: str) -> torch.Tensor:
+        return self.group_b(self.copy, layer, group)
+
+    def grad_a(self, layer: int, group: str) -> torch.Tensor:
+        return self.group_a(self.grad, layer, group)
+
+    def grad_b(self, layer: int, group: str) -> torch.Tensor:
+        return self.group_b(self.grad, layer, group)
+
+    def refresh_copies(self) -> None:
+        """Rebuilds the compute copies from the master weights (after init/load)."""
+        N.call("unok_cast_copy", N.dtype_code(self.compute_dtype), self.numel, self.n_a, float(self.scale),
+               N.ptr(self.master), N.ptr(self.copy), N.stream())
+        self.refresh_transposes()
+
+    def refresh_transposes(self) -> None:
+        N.call("unok_transpose_jobs", N.dtype_code(self.compute_dtype), N.ptr(self._jobs), self._jobs.shape[0],
+               self._tiles, N.ptr(self.copy), N.ptr(self.copy_t), N.stream())
+
+    def zero_grad(self) -> None:
+        self.grad.zero_()

@@ -1,0 +1,703 @@
+// Block-diffusion attention, forward and backward (bf16 MFMA and fp32 kernels).
+//
+// Visibility is given per query row as key intervals over two K/V sources:
+//   source 1 = clean-stream K/V, keys [lo1, hi1);  source 2 = noisy-stream K/V, keys [lo2, hi2)
+// which expresses every pattern of the step exactly (bd mask contract, A.4 of the survey):
+//   clean query i (segment start s):  src1 [s, i+1)                      -- causal clean stream
+//   noisy query i in block k:         src1 [s, s+k*b)  +  src2 [s+k*b, s+min((k+1)b, len))
+// Row tables are int32[8] per row: lo1, hi1, lo2, hi2, qlo2, qhi2, 0, 0, where [qlo2, qhi2) is
+// the range of source-2 query rows that may see this row as a key (used by dK/dV).
+//
+// The bf16 kernels compute S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so that each lane owns
+// one query (its softmax statistics are per-lane scalars); P^T is fed to the P.V product
+// directly from the accumulator registers, with the MFMA k-index permuted to match the
+// accumulator's key order. K tiles are staged row-major in LDS and V tiles transposed.
+// Tiles outside a wave's key range are skipped; tiles wholly inside every query's interval
+// run without evaluating the mask. Softmax runs in the exp2 domain; LSE is stored as
+// log2-sum-exp2 of the scaled scores (lse2) for the backward pass.
+#include "common.h"
+
+struct AttnArgs {
+  const void* Q; int64_t ldq;          // [Mq, Hq*D]
+  const void* K1; int64_t ldk1;        // source 1 keys  [Mk1, Hkv*D]
+  const void* V1; int64_t ldv1;
+  const void* K2; int64_t ldk2;        // source 2 keys (may be null)
+  const void* V2; int64_t ldv2;
+  const int32_t* iv;                   // [Mq, 8] query intervals
+  void* O; int64_t ldo;                // [Mq, Hq*D]
+  float* LSE;                          // [Mq, Hq]
+  // backward
+  const void* dO; int64_t lddo;
+  const float* Dsum;                   // [Mq, Hq] rowsum(dO * O)
+  void* dQ; int64_t lddq;
+  const int32_t* ivk;                  // [Mk2, 8] key-side table (qlo2, qhi2 at 4, 5)
+  void* dK; int64_t lddk;              // [Mk2, Hkv*D]
+  void* dV; int64_t lddv;
+  int Mq, Mk2, Hq, Hkv;
+  float scale;                         // d^-0.5
+  float scale_log2;                    // d^-0.5 * log2(e)
+};
+
+__device__ __forceinline__ bf16x8_t ld_bf16x8(const bf16_t* p) { return *(const bf16x8_t*)p; }
+
+__device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
+  uint4 u;
+  bf16_t* h = (bf16_t*)&u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = f32_to_bf16(v[i]);
+  return __builtin_bit_cast(bf16x8_t, u);
+}
+
+// A operand for a 16-key MFMA step read from a transposed [D][keys] LDS tile, with the key
+// permutation of the accumulator layout: lane group g supplies keys base+4g+{0..3} and
+// base+8+4g+{0..3}.
+__device__ __forceinline__ bf16x8_t ld_perm(const bf16_t* row, int base, int g) {
+  const uint2 lo = *(const uint2*)(row + base + 4 * g);
+  const uint2 hi = *(const uint2*)(row + base + 8 + 4 * g);
+  uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  return __builtin_bit_cast(bf16x8_t, u);
+}
+
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Loads a [64 rows x D] tile of a row-major [rows, *] bf16 matrix (column offset col0) into
+// LDS, row-major with stride RS and/or transposed ([D][64] with stride TS). Rows >= rend are 0.
+template <int D, bool ROW, bool TRN, int RS, int TS>
+__device__ __forceinline__ void stage_tile(const bf16_t* src, int64_t ld, int col0, int r0, int rend, bf16_t* rowdst,
+                                           bf16_t* trndst) {
+  constexpr int CPR = D / 8;               // 16-byte chunks per row
+  constexpr int ITER = 64 * CPR / 256;
+#pragma unroll
+  for (int i = 0; i < ITER; ++i) {
+    const int c = threadIdx.x + 256 * i, r = c / CPR, dc = (c % CPR) * 8;
+    const int row = r0 + r;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < rend) v = *(const uint4*)(src + (int64_t)row * ld + col0 + dc);
+    if (ROW) *(uint4*)&rowdst[r * RS + dc] = v;
+    if (TRN) {
+      const bf16_t* h = (const bf16_t*)&v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) trndst[(dc + e) * TS + r] = h[e];
+    }
+  }
+}
+
+// Interval bounds reduced over a workgroup's 4 waves. Empty intervals are ignored.
+struct Bounds { int lo, hi, maxlo, minhi; };
+
+__device__ __forceinline__ Bounds wave_bounds(bool valid, int lo, int hi) {
+  const bool use = valid && lo < hi;
+  Bounds b;
+  b.lo = wave_min_i(use ? lo : INT_MAX);
+  b.hi = wave_max_i(use ? hi : INT_MIN);
+  // for the "whole tile visible" test every valid query counts (an empty one forces the mask)
+  b.maxlo = wave_max_i(valid ? lo : INT_MIN);
+  b.minhi = wave_min_i(valid ? (lo < hi ? hi : INT_MIN) : INT_MAX);
+  return b;
+}
+
+__device__ __forceinline__ void wg_bounds(const Bounds& w, int* sh, int& lo, int& hi) {
+  const int wid = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sh[wid * 2] = w.lo; sh[wid * 2 + 1] = w.hi; }
+  __syncthreads();
+  lo = min(min(sh[0], sh[2]), min(sh[4], sh[6]));
+  hi = max(max(sh[1], sh[3]), max(sh[5], sh[7]));
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------
+// Forward, bf16: one workgroup = 128 queries (4 waves x 32) of one q-head.
+// ---------------------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void attn_fwd_bf16_kernel(const AttnArgs p) {
+  constexpr int BK = 64, KS = D + 8, VS = BK + 4, NKS = D / 16, NDT = D / 32;
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[BK * KS];
+  __shared__ __attribute__((aligned(16))) bf16_t Vt[D * VS];
+  __shared__ int sh[8];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
+  const int nqt = (p.Mq + 127) / 128;
+  const int lin = xcd_remap(blockIdx.x, nqt * p.Hq);
+  const int h = lin % p.Hq, qt = lin / p.Hq;
+  const int kvh = h / (p.Hq / p.Hkv);
+  const int qrow = qt * 128 + w * 32 + lq;
+  const bool qvalid = qrow < p.Mq;
+  int4 ivq = make_int4(0, 0, 0, 0);
+  if (qvalid) ivq = *(const int4*)(p.iv + (int64_t)qrow * 8);
+
+  const bf16_t* Q = (const bf16_t*)p.Q;
+  bf16x8_t qreg[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    if (qvalid) qreg[ks] = ld_bf16x8(Q + (int64_t)qrow * p.ldq + h * D + ks * 16 + g * 8);
+    else qreg[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+  }
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16_t oacc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
+
+#pragma unroll 1
+  for (int src = 0; src < 2; ++src) {
+    const bf16_t* Kp = (const bf16_t*)(src ? p.K2 : p.K1);
+    const bf16_t* Vp = (const bf16_t*)(src ? p.V2 : p.V1);
+    const int64_t ldk = src ? p.ldk2 : p.ldk1, ldv = src ? p.ldv2 : p.ldv1;
+    if (Kp == nullptr) continue;
+    const int lo = src ? ivq.z : ivq.x, hi = src ? ivq.w : ivq.y;
+    const Bounds wb = wave_bounds(qvalid, lo, hi);
+    int kb, ke;
+    wg_bounds(wb, sh, kb, ke);
+    if (kb >= ke) continue;
+#pragma unroll 1
+    for (int kt = (kb / BK) * BK; kt < ke; kt += BK) {
+      __syncthreads();
+      stage_tile<D, true, false, KS, VS>(Kp, ldk, kvh * D, kt, ke, Ks, nullptr);
+      stage_tile<D, false, true, KS, VS>(Vp, ldv, kvh * D, kt, ke, nullptr, Vt);
+      __syncthreads();
+      if (kt >= wb.hi || kt + BK <= wb.lo) continue;
+      const bool full = kt >= wb.maxlo && kt + BK <= wb.minhi;
+      f32x16_t sacc[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kk][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+          sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Ks[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
+                                                              qreg[ks], sacc[kk], 0, 0, 0);
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float v = sacc[kk][j] * p.scale_log2;
+          if (!full) {
+            const int key = kt + kk * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
+            if (key < lo || key >= hi) v = -INFINITY;
+          }
+          sacc[kk][j] = v;
+          tmax = fmaxf(tmax, v);
+        }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      // Branch-free when nothing is visible yet (m_new = -inf): every lane must keep feeding
+      // the shared MFMAs, so exp2 is taken against 0 and yields p = 0, alpha = 0.
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m_run - m_use);
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float e = exp2f(sacc[kk][j] - m_use);
+          sacc[kk][j] = e;
+          l_run += e;
+        }
+      m_run = m_new;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float pv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) pv[i] = sacc[kk][8 * hh + i];
+          const bf16x8_t b = pack_bf16x8(pv);
+#pragma unroll
+          for (int t = 0; t < NDT; ++t)
+            oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Vt[(t * 32 + lq) * VS], kk * 32 + 16 * hh, g),
+                                                               b, oacc[t], 0, 0, 0);
+        }
+    }
+  }
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (qvalid) {
+    bf16_t* O = (bf16_t*)p.O + (int64_t)qrow * p.ldo + h * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        uint2 u;
+        bf16_t* hv = (bf16_t*)&u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hv[e] = f32_to_bf16(oacc[t][j4 * 4 + e] * inv);
+        *(uint2*)(O + t * 32 + 8 * j4 + 4 * g) = u;
+      }
+    if (g == 0) p.LSE[(int64_t)qrow * p.Hq + h] = l_tot > 0.f ? m_run + log2f(l_tot) : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Backward: Dsum = rowsum(dO * O) per (row, head); one wavefront per item.
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void attn_dsum_kernel(const T* __restrict__ dO, int64_t lddo, const T* __restrict__ O,
+                                                        int64_t ldo, float* __restrict__ Dsum, int Mq, int Hq, int D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= (int64_t)Mq * Hq) return;
+  const int64_t row = item / Hq;
+  const int h = (int)(item % Hq);
+  float s = 0.f;
+  for (int i = lane; i < D; i += 64)
+    s += Elem<T>::load(dO + row * lddo + h * D + i) * Elem<T>::load(O + row * ldo + h * D + i);
+  s = wave_sum(s);
+  if (lane == 0) Dsum[item] = s;
+}
+
+// dQ, bf16: per workgroup 128 queries of one head; same tile walk as the forward.
+template <int D>
+__global__ __launch_bounds__(256) void attn_dq_bf16_kernel(const AttnArgs p) {
+  constexpr int BK = 64, KS = D + 8, TS = BK + 4, NKS = D / 16, NDT = D / 32;
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[BK * KS];
+  __shared__ __attribute__((aligned(16))) bf16_t Kt[D * TS];
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[BK * KS];
+  __shared__ int sh[8];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
+  const int nqt = (p.Mq + 127) / 128;
+  const int lin = xcd_remap(blockIdx.x, nqt * p.Hq);
+  const int h = lin % p.Hq, qt = lin / p.Hq;
+  const int kvh = h / (p.Hq / p.Hkv);
+  const int qrow = qt * 128 + w * 32 + lq;
+  const bool qvalid = qrow < p.Mq;
+  int4 ivq = make_int4(0, 0, 0, 0);
+  float lse = 0.f, dsum = 0.f;
+  if (qvalid) {
+    ivq = *(const int4*)(p.iv + (int64_t)qrow * 8);
+    lse = p.LSE[(int64_t)qrow * p.Hq + h];
+    dsum = p.Dsum[(int64_t)qrow * p.Hq + h];
+  }
+  const bf16_t* Q = (const bf16_t*)p.Q;
+  const bf16_t* dO = (const bf16_t*)p.dO;
+  bf16x8_t qreg[NKS], oreg[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    if (qvalid) {
+      qreg[ks] = ld_bf16x8(Q + (int64_t)qrow * p.ldq + h * D + ks * 16 + g * 8);
+      oreg[ks] = ld_bf16x8(dO + (int64_t)qrow * p.lddo + h * D + ks * 16 + g * 8);
+    } else {
+      qreg[ks] = oreg[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+    }
+  }
+  f32x16_t dq[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[t][r] = 0.f;
+
+#pragma unroll 1
+  for (int src = 0; src < 2; ++src) {
+    const bf16_t* Kp = (const bf16_t*)(src ? p.K2 : p.K1);
+    const bf16_t* Vp = (const bf16_t*)(src ? p.V2 : p.V1);
+    const int64_t ldk = src ? p.ldk2 : p.ldk1, ldv = src ? p.ldv2 : p.ldv1;
+    if (Kp == nullptr) continue;
+    const int lo = src ? ivq.z : ivq.x, hi = src ? ivq.w : ivq.y;
+    const Bounds wb = wave_bounds(qvalid, lo, hi);
+    int kb, ke;
+    wg_bounds(wb, sh, kb, ke);
+    if (kb >= ke) continue;
+#pragma unroll 1
+    for (int kt = (kb / BK) * BK; kt < ke; kt += BK) {
+      __syncthreads();
+      stage_tile<D, true, true, KS, TS>(Kp, ldk, kvh * D, kt, ke, Ks, Kt);
+      stage_tile<D, true, false, KS, TS>(Vp, ldv, kvh * D, kt, ke, Vs, nullptr);
+      __syncthreads();
+      if (kt >= wb.hi || kt + BK <= wb.lo) continue;
+      const bool full = kt >= wb.maxlo && kt + BK <= wb.minhi;
+      f32x16_t sacc[2], dpacc[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { sacc[kk][r] = 0.f; dpacc[kk][r] = 0.f; }
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Ks[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
+                                                              qreg[ks], sacc[kk], 0, 0, 0);
+          dpacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Vs[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
+                                                               oreg[ks], dpacc[kk], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float pr = exp2f(sacc[kk][j] * p.scale_log2 - lse);
+          if (!full) {
+            const int key = kt + kk * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
+            if (key < lo || key >= hi) pr = 0.f;
+          }
+          sacc[kk][j] = pr * (dpacc[kk][j] - dsum);
+        }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float dv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dv[i] = sacc[kk][8 * hh + i];
+          const bf16x8_t b = pack_bf16x8(dv);
+#pragma unroll
+          for (int t = 0; t < NDT; ++t)
+            dq[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Kt[(t * 32 + lq) * TS], kk * 32 + 16 * hh, g), b,
+                                                             dq[t], 0, 0, 0);
+        }
+    }
+  }
+  if (qvalid) {
+    bf16_t* out = (bf16_t*)p.dQ + (int64_t)qrow * p.lddq + h * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        uint2 u;
+        bf16_t* hv = (bf16_t*)&u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hv[e] = f32_to_bf16(dq[t][j4 * 4 + e] * p.scale);
+        *(uint2*)(out + t * 32 + 8 * j4 + 4 * g) = u;
+      }
+  }
+}
+
+// dK, dV of source-2 keys, bf16: per workgroup 128 keys (4 waves x 32) of one kv-head; walks
+// the query rows [qlo2, qhi2) of those keys for every q-head of the GQA group.
+template <int D>
+__global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
+  constexpr int BQ = 64, RS = D + 8, TS = BQ + 4, NKS = D / 16, NDT = D / 32;
+  __shared__ __attribute__((aligned(16))) bf16_t Qs[BQ * RS];
+  __shared__ __attribute__((aligned(16))) bf16_t Qt[D * TS];
+  __shared__ __attribute__((aligned(16))) bf16_t Os[BQ * RS];
+  __shared__ __attribute__((aligned(16))) bf16_t Ot[D * TS];
+  __shared__ float s_lse[BQ], s_dsum[BQ];
+  __shared__ int s_lo[BQ], s_hi[BQ];
+  __shared__ int sh[8];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
+  const int nkt = (p.Mk2 + 127) / 128;
+  const int lin = xcd_remap(blockIdx.x, nkt * p.Hkv);
+  const int kvh = lin % p.Hkv, kt = lin / p.Hkv;
+  const int rep = p.Hq / p.Hkv;
+  const int krow = kt * 128 + w * 32 + lq;
+  const bool kvalid = krow < p.Mk2;
+  int qlo = 0, qhi = 0;
+  if (kvalid) {
+    const int2 a = *(const int2*)(p.ivk + (int64_t)krow * 8 + 4);
+    qlo = a.x;
+    qhi = a.y;
+  }
+  const bf16_t* K = (const bf16_t*)p.K2;
+  const bf16_t* V = (const bf16_t*)p.V2;
+  bf16x8_t kreg[NKS], vreg[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    if (kvalid) {
+      kreg[ks] = ld_bf16x8(K + (int64_t)krow * p.ldk2 + kvh * D + ks * 16 + g * 8);
+      vreg[ks] = ld_bf16x8(V + (int64_t)krow * p.ldv2 + kvh * D + ks * 16 + g * 8);
+    } else {
+      kreg[ks] = vreg[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+    }
+  }
+  const Bounds wb = wave_bounds(kvalid, qlo, qhi);
+  int qb, qe;
+  wg_bounds(wb, sh, qb, qe);
+  f32x16_t dk[NDT], dv[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { dk[t][r] = 0.f; dv[t][r] = 0.f; }
+  const bf16_t* Q = (const bf16_t*)p.Q;
+  const bf16_t* dO = (const bf16_t*)p.dO;
+  if (qb < qe) {
+#pragma unroll 1
+    for (int hr = 0; hr < rep; ++hr) {
+      const int h = kvh * rep + hr;
+#pragma unroll 1
+      for (int q0 = (qb / BQ) * BQ; q0 < qe; q0 += BQ) {
+        __syncthreads();
+        stage_tile<D, true, true, RS, TS>(Q, p.ldq, h * D, q0, qe, Qs, Qt);
+        stage_tile<D, true, true, RS, TS>(dO, p.lddo, h * D, q0, qe, Os, Ot);
+        if (tid < BQ) {
+          const int qr = q0 + tid;
+          const bool ok = qr < qe;
+          s_lse[tid] = ok ? p.LSE[(int64_t)qr * p.Hq + h] : 0.f;
+          s_dsum[tid] = ok ? p.Dsum[(int64_t)qr * p.Hq + h] : 0.f;
+          s_lo[tid] = ok ? p.iv[(int64_t)qr * 8 + 2] : 0;
+          s_hi[tid] = ok ? p.iv[(int64_t)qr * 8 + 3] : 0;
+        }
+        __syncthreads();
+        if (q0 >= wb.hi || q0 + BQ <= wb.lo) continue;
+        f32x16_t sacc[2], dpacc[2];
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) { sacc[qq][r] = 0.f; dpacc[qq][r] = 0.f; }
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            sacc[qq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Qs[(qq * 32 + lq) * RS + ks * 16 + g * 8]),
+                                                                kreg[ks], sacc[qq], 0, 0, 0);
+            dpacc[qq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Os[(qq * 32 + lq) * RS + ks * 16 + g * 8]),
+                                                                 vreg[ks], dpacc[qq], 0, 0, 0);
+          }
+        }
+        // lane holds rows q = q0 + qq*32 + 8(j/4) + 4g + (j%4), key = krow
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int ql = qq * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
+            float pr = 0.f;
+            if (kvalid && krow >= s_lo[ql] && krow < s_hi[ql]) pr = exp2f(sacc[qq][j] * p.scale_log2 - s_lse[ql]);
+            sacc[qq][j] = pr;
+            dpacc[qq][j] = pr * (dpacc[qq][j] - s_dsum[ql]);
+          }
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            float pv[8], dsv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { pv[i] = sacc[qq][8 * hh + i]; dsv[i] = dpacc[qq][8 * hh + i]; }
+            const bf16x8_t bp = pack_bf16x8(pv), bds = pack_bf16x8(dsv);
+#pragma unroll
+            for (int t = 0; t < NDT; ++t) {
+              dv[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Ot[(t * 32 + lq) * TS], qq * 32 + 16 * hh, g), bp,
+                                                               dv[t], 0, 0, 0);
+              dk[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Qt[(t * 32 + lq) * TS], qq * 32 + 16 * hh, g), bds,
+                                                               dk[t], 0, 0, 0);
+            }
+          }
+      }
+    }
+  }
+  if (kvalid) {
+    bf16_t* ok = (bf16_t*)p.dK + (int64_t)krow * p.lddk + kvh * D;
+    bf16_t* ov = (bf16_t*)p.dV + (int64_t)krow * p.lddv + kvh * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        uint2 uk, uv;
+        bf16_t* hk = (bf16_t*)&uk;
+        bf16_t* hv = (bf16_t*)&uv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hk[e] = f32_to_bf16(dk[t][j4 * 4 + e] * p.scale);
+          hv[e] = f32_to_bf16(dv[t][j4 * 4 + e]);
+        }
+        *(uint2*)(ok + t * 32 + 8 * j4 + 4 * g) = uk;
+        *(uint2*)(ov + t * 32 + 8 * j4 + 4 * g) = uv;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// fp32 kernels (fp32 parity mode): one wavefront per (row, head), keys walked one at a time.
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const AttnArgs p, int D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= (int64_t)p.Mq * p.Hq) return;
+  const int qrow = (int)(item / p.Hq), h = (int)(item % p.Hq);
+  const int kvh = h / (p.Hq / p.Hkv);
+  const int4 iv = *(const int4*)(p.iv + (int64_t)qrow * 8);
+  const float* q = (const float*)p.Q + (int64_t)qrow * p.ldq + h * D;
+  float qv[2] = {0.f, 0.f}, acc[2] = {0.f, 0.f};
+  for (int t = 0; t < 2; ++t) if (lane + 64 * t < D) qv[t] = q[lane + 64 * t];
+  float m = -INFINITY, l = 0.f;
+  for (int src = 0; src < 2; ++src) {
+    const float* K = (const float*)(src ? p.K2 : p.K1);
+    const float* V = (const float*)(src ? p.V2 : p.V1);
+    if (!K) continue;
+    const int64_t ldk = src ? p.ldk2 : p.ldk1, ldv = src ? p.ldv2 : p.ldv1;
+    const int lo = src ? iv.z : iv.x, hi = src ? iv.w : iv.y;
+    for (int k = lo; k < hi; ++k) {
+      const float* kr = K + (int64_t)k * ldk + kvh * D;
+      float s = 0.f;
+      for (int t = 0; t < 2; ++t) if (lane + 64 * t < D) s += qv[t] * kr[lane + 64 * t];
+      s = wave_sum(s) * p.scale_log2;
+      const float mn = fmaxf(m, s);
+      const float a = exp2f(m - mn), e = exp2f(s - mn);
+      l = l * a + e;
+      const float* vr = V + (int64_t)k * ldv + kvh * D;
+      for (int t = 0; t < 2; ++t) if (lane + 64 * t < D) acc[t] = acc[t] * a + e * vr[lane + 64 * t];
+      m = mn;
+    }
+  }
+  float* o = (float*)p.O + (int64_t)qrow * p.ldo + h * D;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  for (int t = 0; t < 2; ++t) if (lane + 64 * t < D) o[lane + 64 * t] = acc[t] * inv;
+  if (lane == 0) p.LSE[item] = l > 0.f ? m + log2f(l) : -INFINITY;
+}
+
+__global__ __launch_bounds__(256) void attn_dq_f32_kernel(const AttnArgs p, int D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= (int64_t)p.Mq * p.Hq) return;
+  const int qrow = (int)(item / p.Hq), h = (int)(item % p.Hq);
+  const int kvh = h / (p.Hq / p.Hkv);
+  const int4 iv = *(const int4*)(p.iv + (int64_t)qrow * 8);
+  const float* q = (const float*)p.Q + (int64_t)qrow * p.ldq + h * D;
+  const float* go = (const float*)p.dO + (int64_t)qrow * p.lddo + h * D;
+  const float lse = p.LSE[item], ds = p.Dsum[item];
+  float qv[2] = {0.f, 0.f}, gv[2] = {0.f, 0.f}, acc[2] = {0.f, 0.f};
+  for (int t = 0; t < 2; ++t) if (lane + 64 * t < D) { qv[t] = q[lane + 64 * t]; gv[t] = go[lane + 64 * t]; }
+  for (int src = 0; src < 2; ++src) {
+    const float* K = (const float*)(src ? p.K2 : p.K1);
+    const float* V = (const float*)(src ? p.V2 : p.V1);
+    if (!K) continue;
+    const int64_t ldk = src ? p.ldk2 : p.ldk1, ldv = src ? p.ldv2 : p.ldv1;
+    const int lo = src ? iv.z : iv.x, hi = src ? iv.w : iv.y;
+    for (int k = lo; k < hi; ++k) {
+      const float* kr = K + (int64_t)k * ldk + kvh * D;
+      const float* vr = V + (int64_t)k * ldv + kvh * D;
+      float s = 0.f, dp = 0.f;
+      for (int t = 0; t < 2; ++t)
+        if (lane + 64 * t < D) { s += qv[t] * kr[lane + 64 * t]; dp += gv[t] * vr[lane + 64 * t]; }
+      s = wave_sum(s);
+      dp = wave_sum(dp);
+      const float pr = exp2f(s * p.scale_log2 - lse);
+      const float dsc = pr * (dp - ds);
+      for (int t = 0; t < 2; ++t) if (lane + 64 * t < D) acc[t] += dsc * kr[lane + 64 * t];
+    }
+  }
+  float* o = (float*)p.dQ + (int64_t)qrow * p.lddq + h * D;
+  for (int t = 0; t < 2; ++t) if (lane + 64 * t < D) o[lane + 64 * t] = acc[t] * p.scale;
+}
+
+__global__ __launch_bounds__(256) void attn_dkv_f32_kernel(const AttnArgs p, int D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= (int64_t)p.Mk2 * p.Hkv) return;
+  const int krow = (int)(item / p.Hkv), kvh = (int)(item % p.Hkv);
+  const int rep = p.Hq / p.Hkv;
+  const int qlo = p.ivk[(int64_t)krow * 8 + 4], qhi = p.ivk[(int64_t)krow * 8 + 5];
+  const float* kr = (const float*)p.K2 + (int64_t)krow * p.ldk2 + kvh * D;
+  const float* vr = (const float*)p.V2 + (int64_t)krow * p.ldv2 + kvh * D;
+  float kv[2] = {0.f, 0.f}, vv[2] = {0.f, 0.f}, dk[2] = {0.f, 0.f}, dvv[2] = {0.f, 0.f};
+  for (int t = 0; t < 2; ++t) if (lane + 64 * t < D) { kv[t] = kr[lane + 64 * t]; vv[t] = vr[lane + 64 * t]; }
+  for (int hr = 0; hr < rep; ++hr) {
+    const int h = kvh * rep + hr;
+    for (int qr = qlo; qr < qhi; ++qr) {
+      const int lo = p.iv[(int64_t)qr * 8 + 2], hi = p.iv[(int64_t)qr * 8 + 3];
+      if (krow < lo || krow >= hi) continue;
+      const float* q = (const float*)p.Q + (int64_t)qr * p.ldq + h * D;
+      const float* go = (const float*)p.dO + (int64_t)qr * p.lddo + h * D;
+      float s = 0.f, dp = 0.f;
+      for (int t = 0; t < 2; ++t)
+        if (lane + 64 * t < D) { s += q[lane + 64 * t] * kv[t]; dp += go[lane + 64 * t] * vv[t]; }
+      s = wave_sum(s);
+      dp = wave_sum(dp);
+      const float pr = exp2f(s * p.scale_log2 - p.LSE[(int64_t)qr * p.Hq + h]);
+      const float dsc = pr * (dp - p.Dsum[(int64_t)qr * p.Hq + h]);
+      for (int t = 0; t < 2; ++t)
+        if (lane + 64 * t < D) { dvv[t] += pr * go[lane + 64 * t]; dk[t] += dsc * q[lane + 64 * t]; }
+    }
+  }
+  float* ok = (float*)p.dK + (int64_t)krow * p.lddk + kvh * D;
+  float* ov = (float*)p.dV + (int64_t)krow * p.lddv + kvh * D;
+  for (int t = 0; t < 2; ++t)
+    if (lane + 64 * t < D) { ok[lane + 64 * t] = dk[t] * p.scale; ov[lane + 64 * t] = dvv[t]; }
+}
+
+// ---------------------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------------------
+static int check_geom(int dtype, int D, int Hq, int Hkv) {
+  UNOK_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0, UNOK_EINVAL, "attention: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+  if (dtype == UNOK_BF16)
+    UNOK_REQUIRE(D == 64 || D == 128, UNOK_EUNSUPPORTED, "attention(bf16): head_dim %d not in {64,128}", D);
+  else
+    UNOK_REQUIRE(D > 0 && D <= 128, UNOK_EUNSUPPORTED, "attention(f32): head_dim %d > 128", D);
+  return 0;
+}
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Forward. K2/V2 may be null (single source). Strides in elements.
+UNOK_EXPORT int unok_attn_fwd(int dtype, int Mq, int Hq, int Hkv, int D, const void* Q, int64_t ldq, const void* K1,
+                              int64_t ldk1, const void* V1, int64_t ldv1, const void* K2, int64_t ldk2, const void* V2,
+                              int64_t ldv2, const int32_t* iv, void* O, int64_t ldo, float* LSE, float scale,
+                              void* stream) {
+  if (Mq == 0) return 0;
+  int rc = check_geom(dtype, D, Hq, Hkv);
+  if (rc) return rc;
+  AttnArgs a{};
+  a.Q = Q; a.ldq = ldq; a.K1 = K1; a.ldk1 = ldk1; a.V1 = V1; a.ldv1 = ldv1;
+  a.K2 = K2; a.ldk2 = ldk2; a.V2 = V2; a.ldv2 = ldv2; a.iv = iv; a.O = O; a.ldo = ldo; a.LSE = LSE;
+  a.Mq = Mq; a.Hq = Hq; a.Hkv = Hkv; a.scale = scale; a.scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == UNOK_F32) {
+    hipLaunchKernelGGL(attn_fwd_f32_kernel, dim3((unsigned)(((int64_t)Mq * Hq + 3) / 4)), dim3(256), 0, st, a, D);
+  } else {
+    UNOK_REQUIRE(dtype == UNOK_BF16, UNOK_EINVAL, "attention: bad dtype %d", dtype);
+    UNOK_REQUIRE(al16(Q) && al16(K1) && al16(V1) && ldq % 8 == 0 && ldk1 % 8 == 0 && ldv1 % 8 == 0 && ldo % 8 == 0 &&
+                 (!K2 || (al16(K2) && al16(V2) && ldk2 % 8 == 0 && ldv2 % 8 == 0)),
+                 UNOK_EALIGN, "attention(bf16): operands must be 16-byte aligned with strides multiple of 8");
+    const unsigned blocks = (unsigned)(((Mq + 127) / 128) * Hq);
+    if (D == 128) hipLaunchKernelGGL(attn_fwd_bf16_kernel<128>, dim3(blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(attn_fwd_bf16_kernel<64>, dim3(blocks), dim3(256), 0, st, a);
+  }
+  return unok::check_launch("attn_fwd");
+}
+
+// Backward. Computes Dsum into the caller's [Mq,Hq] fp32 buffer, dQ for every query, and,
+// when dK/dV are non-null, dK/dV of the source-2 keys (rows [0, Mk2)).
+UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D, const void* Q, int64_t ldq,
+                              const void* K1, int64_t ldk1, const void* V1, int64_t ldv1, const void* K2, int64_t ldk2,
+                              const void* V2, int64_t ldv2, const int32_t* iv, const int32_t* ivk, const void* O,
+                              int64_t ldo, const float* LSE, const void* dO, int64_t lddo, float* Dsum, void* dQ,
+                              int64_t lddq, void* dK, int64_t lddk, void* dV, int64_t lddv, float scale,
+                              void* stream) {
+  if (Mq == 0) return 0;
+  int rc = check_geom(dtype, D, Hq, Hkv);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const unsigned items = (unsigned)(((int64_t)Mq * Hq + 3) / 4);
+  if (dtype == UNOK_BF16)
+    hipLaunchKernelGGL(attn_dsum_kernel<bf16_t>, dim3(items), dim3(256), 0, st, (const bf16_t*)dO, lddo,
+                       (const bf16_t*)O, ldo, Dsum, Mq, Hq, D);
+  else
+    hipLaunchKernelGGL(attn_dsum_kernel<float>, dim3(items), dim3(256), 0, st, (const float*)dO, lddo,
+                       (const float*)O, ldo, Dsum, Mq, Hq, D);
+  rc = unok::check_launch("attn_dsum");
+  if (rc) return rc;
+  AttnArgs a{};
+  a.Q = Q; a.ldq = ldq; a.K1 = K1; a.ldk1 = ldk1; a.V1 = V1; a.ldv1 = ldv1;
+  a.K2 = K2; a.ldk2 = ldk2; a.V2 = V2; a.ldv2 = ldv2; a.iv = iv; a.ivk = ivk; a.LSE = (float*)LSE;
+  a.dO = dO; a.lddo = lddo; a.Dsum = Dsum; a.dQ = dQ; a.lddq = lddq; a.dK = dK; a.lddk = lddk; a.dV = dV; a.lddv = lddv;
+  a.Mq = Mq; a.Mk2 = Mk2; a.Hq = Hq; a.Hkv = Hkv; a.scale = scale; a.scale_log2 = scale * 1.4426950408889634f;
+  const bool want_kv = dK != nullptr && dV != nullptr && K2 != nullptr && Mk2 > 0;
+  if (want_kv) UNOK_REQUIRE(ivk != nullptr, UNOK_EINVAL, "attn_bwd: key-side interval table required for dK/dV");
+  if (dtype == UNOK_F32) {
+    hipLaunchKernelGGL(attn_dq_f32_kernel, dim3(items), dim3(256), 0, st, a, D);
+    rc = unok::check_launch("attn_dq_f32");
+    if (rc || !want_kv) return rc;
+    hipLaunchKernelGGL(attn_dkv_f32_kernel, dim3((unsigned)(((int64_t)Mk2 * Hkv + 3) / 4)), dim3(256), 0, st, a, D);
+    return unok::check_launch("attn_dkv_f32");
+  }
+  UNOK_REQUIRE(al16(dO) && lddo % 8 == 0 && lddq % 8 == 0 && (!want_kv || (lddk % 8 == 0 && lddv % 8 == 0)),
+               UNOK_EALIGN, "attn_bwd(bf16): gradient strides must be multiples of 8");
+  const unsigned qblocks = (unsigned)(((Mq + 127) / 128) * Hq);
+  if (D == 128) hipLaunchKernelGGL(attn_dq_bf16_kernel<128>, dim3(qblocks), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(attn_dq_bf16_kernel<64>, dim3(qblocks), dim3(256), 0, st, a);
+  rc = unok::check_launch("attn_dq_bf16");
+  if (rc || !want_kv) return rc;
+  const unsigned kblocks = (unsigned)(((Mk2 + 127) / 128) * Hkv);
+  if (D == 128) hipLaunchKernelGGL(attn_dkv_bf16_kernel<128>, dim3(kblocks), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(attn_dkv_bf16_kernel<64>, dim3(kblocks), dim3(256), 0, st, a);
+  return unok::check_launch("attn_dkv_bf16");
+}

@@ -1,0 +1,323 @@
+// Objective kernels over LM-head logits.
+//
+// Cross-entropy (training/trainer.py:267-283): the LM head is evaluated in vocabulary chunks
+// (GEMM into a chunk buffer); row_lse_update merges each chunk into a running (max, sum-exp)
+// per row and captures the target logit, so the full [rows x vocab] logits never exist.
+// The backward recomputes each chunk and writes dz = g * w * (softmax - onehot) for the
+// data-gradient GEMM. Row weights w = 1 / p_mask; the 1 / max(token_count, 1) normaliser and
+// the upstream gradient come as device scalars (no host synchronisation).
+//
+// Total variation (training/losses.py:76-183) and reverse KL (losses.py:59-73) run over
+// materialised logits with fp32 per-row statistics, matching the reference's per-chunk fp32
+// math; TV's gradient is p * (sign(p - q) - sum sign * p) with sign(0) = 0.
+#include "common.h"
+
+// Floating-point contraction is off in this file: TV must see d = p - q == 0 exactly when
+// p == q (sign(0) = 0), which a fused multiply-add of p's scaling into the subtraction breaks.
+#pragma clang fp contract(off)
+
+template <typename T> __device__ __forceinline__ float ldf(const T* p) { return Elem<T>::load(p); }
+
+// Running softmax statistics of a logits chunk z[R, Vc] (columns c0..c0+Vc of the vocab).
+template <typename T>
+__global__ __launch_bounds__(256) void row_lse_update_kernel(const T* __restrict__ z, int64_t ldz, int Vc, int c0,
+                                                             const int64_t* __restrict__ tgt, float* run_max,
+                                                             float* run_sum, float* zt, int first) {
+  __shared__ float red[32];
+  const int row = blockIdx.x;
+  const T* zr = z + (int64_t)row * ldz;
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j < Vc; j += 256) m = fmaxf(m, ldf(zr + j));
+  m = block_max(m, red);
+  float s = 0.f;
+  for (int j = threadIdx.x; j < Vc; j += 256) s += expf(ldf(zr + j) - m);
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) {
+    float M0 = first ? -INFINITY : run_max[row];
+    float S0 = first ? 0.f : run_sum[row];
+    const float Mn = fmaxf(M0, m);
+    run_sum[row] = (S0 > 0.f ? S0 * expf(M0 - Mn) : 0.f) + s * expf(m - Mn);
+    run_max[row] = Mn;
+    if (tgt) {
+      const int64_t t = tgt[row];
+      if (t >= c0 && t < c0 + Vc) zt[row] = ldf(zr + (t - c0));
+    }
+  }
+}
+
+// First-index argmax merge over a chunk: best (value, index) per row.
+template <typename T>
+__global__ __launch_bounds__(256) void row_argmax_update_kernel(const T* __restrict__ z, int64_t ldz, int Vc, int c0,
+                                                                float* best_val, int64_t* best_idx, int first) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int row = blockIdx.x;
+  const T* zr = z + (int64_t)row * ldz;
+  float bv = -INFINITY;
+  int bi = INT_MAX;
+  for (int j = threadIdx.x; j < Vc; j += 256) {
+    const float v = ldf(zr + j);
+    if (v > bv) { bv = v; bi = j; }   // j increases per thread: strict > keeps the first index
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      const float v2 = sv[threadIdx.x + o];
+      const int i2 = si[threadIdx.x + o];
+      if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
+        sv[threadIdx.x] = v2;
+        si[threadIdx.x] = i2;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float v = sv[0];
+    const int64_t idx = (int64_t)si[0] + c0;
+    if (first || v > best_val[row]) { best_val[row] = v; best_idx[row] = idx; }
+  }
+}
+
+// loss = sum_r w[r] * (lse[r] - zt[r]) * inv_n ; also stores lse. Single workgroup, fixed order.
+__global__ __launch_bounds__(1024) void ce_finish_kernel(int R, const float* run_max, const float* run_sum,
+                                                         const float* zt, const float* w, const float* inv_n,
+                                                         float* lse, float* loss) {
+  __shared__ float red[32];
+  float acc = 0.f;
+  for (int r = threadIdx.x; r < R; r += 1024) {
+    const float l = run_max[r] + logf(run_sum[r]);
+    lse[r] = l;
+    acc += (w ? w[r] : 1.f) * (l - zt[r]);
+  }
+  acc = block_sum(acc, red);
+  if (threadIdx.x == 0) loss[0] = acc * (inv_n ? inv_n[0] : 1.f);
+}
+
+// dz[r, j] = g * inv_n * w[r] * (exp(z - lse[r]) - [c0 + j == tgt[r]])
+template <typename TO>
+__global__ __launch_bounds__(256) void ce_grad_chunk_kernel(const float* __restrict__ z, int64_t ldz, int Vc, int c0,
+                                                            const float* __restrict__ lse,
+                                                            const int64_t* __restrict__ tgt,
+                                                            const float* __restrict__ w, const float* gscale,
+                                                            const float* inv_n, TO* __restrict__ dz, int64_t lddz) {
+  const int row = blockIdx.x;
+  const float l = lse[row];
+  const float c = gscale[0] * (inv_n ? inv_n[0] : 1.f) * (w ? w[row] : 1.f);
+  const int64_t t = tgt[row] - c0;
+  const float* zr = z + (int64_t)row * ldz;
+  TO* dr = dz + (int64_t)row * lddz;
+  for (int j = threadIdx.x; j < Vc; j += 256) {
+    float p = expf(zr[j] - l);
+    if (j == t) p -= 1.f;
+    Elem<TO>::store(dr + j, c * p);
+  }
+}
+
+// Per-row max and sum-exp over full rows (fp32 statistics).
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_stats_kernel(const T* __restrict__ z, int64_t ldz, int V, float* mx,
+                                                            float* se) {
+  __shared__ float red[32];
+  const int row = blockIdx.x;
+  const T* zr = z + (int64_t)row * ldz;
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, ldf(zr + j));
+  m = block_max(m, red);
+  float s = 0.f;
+  for (int j = threadIdx.x; j < V; j += 256) s += expf(ldf(zr + j) - m);
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) { mx[row] = m; se[row] = fmaxf(s, 1.17549435e-38f); }
+}
+
+// TV forward: row_l1 = sum |ps - pt|, row_S = sum sign(ps - pt) * ps.
+template <typename T>
+__global__ __launch_bounds__(256) void tv_fwd_kernel(const T* __restrict__ zs, int64_t lds, const T* __restrict__ zt,
+                                                     int64_t ldt, int V, const float* ms, const float* ss,
+                                                     const float* mt, const float* st, float* row_l1, float* row_S) {
+  __shared__ float red[32];
+  const int row = blockIdx.x;
+  const float a = ms[row], ia = 1.f / ss[row], b = mt[row], ib = 1.f / st[row];
+  const T* s = zs + (int64_t)row * lds;
+  const T* t = zt + (int64_t)row * ldt;
+  float l1 = 0.f, S = 0.f;
+  for (int j = threadIdx.x; j < V; j += 256) {
+    const float ps = expf(ldf(s + j) - a) * ia, pt = expf(ldf(t + j) - b) * ib;
+    const float d = ps - pt;
+    l1 += fabsf(d);
+    S += (d > 0.f ? ps : (d < 0.f ? -ps : 0.f));
+  }
+  l1 = block_sum(l1, red);
+  S = block_sum(S, red);
+  if (threadIdx.x == 0) { row_l1[row] = l1; row_S[row] = S; }
+}
+
+// TV backward: grad[j] = ps_j * (sign_j - S) * g * inv_n; grad may alias zs.
+template <typename T>
+__global__ __launch_bounds__(256) void tv_bwd_kernel(const T* zs, int64_t lds, const T* __restrict__ zt, int64_t ldt,
+                                                     int V, const float* ms, const float* ss, const float* mt,
+                                                     const float* st, const float* row_S, const float* gscale,
+                                                     const float* inv_n, T* grad, int64_t ldg) {
+  const int row = blockIdx.x;
+  const float a = ms[row], ia = 1.f / ss[row], b = mt[row], ib = 1.f / st[row], S = row_S[row];
+  const float c = gscale[0] * inv_n[0];
+  const T* s = zs + (int64_t)row * lds;
+  const T* t = zt + (int64_t)row * ldt;
+  T* gr = grad + (int64_t)row * ldg;
+  for (int j = threadIdx.x; j < V; j += 256) {
+    const float ps = expf(ldf(s + j) - a) * ia, pt = expf(ldf(t + j) - b) * ib;
+    const float d = ps - pt;
+    const float sg = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
+    Elem<T>::store(gr + j, ps * (sg - S) * c);
+  }
+}
+
+// Reverse KL forward: row_kl = sum ps * (ls - lt).
+template <typename T>
+__global__ __launch_bounds__(256) void kl_fwd_kernel(const T* __restrict__ zs, int64_t lds, const T* __restrict__ zt,
+                                                     int64_t ldt, int V, const float* ms, const float* ss,
+                                                     const float* mt, const float* st, float* row_kl) {
+  __shared__ float red[32];
+  const int row = blockIdx.x;
+  const float la = ms[row] + logf(ss[row]), lb = mt[row] + logf(st[row]);
+  const T* s = zs + (int64_t)row * lds;
+  const T* t = zt + (int64_t)row * ldt;
+  float kl = 0.f;
+  for (int j = threadIdx.x; j < V; j += 256) {
+    const float ls = ldf(s + j) - la, lt = ldf(t + j) - lb;
+    kl += expf(ls) * (ls - lt);
+  }
+  kl = block_sum(kl, red);
+  if (threadIdx.x == 0) row_kl[row] = kl;
+}
+
+// Reverse KL backward: grad[j] = ps_j * ((ls_j - lt_j) - row_kl) * g * inv_n; grad may alias zs.
+template <typename T>
+__global__ __launch_bounds__(256) void kl_bwd_kernel(const T* zs, int64_t lds, const T* __restrict__ zt, int64_t ldt,
+                                                     int V, const float* ms, const float* ss, const float* mt,
+                                                     const float* st, const float* row_kl, const float* gscale,
+                                                     const float* inv_n, T* grad, int64_t ldg) {
+  const int row = blockIdx.x;
+  const float la = ms[row] + logf(ss[row]), lb = mt[row] + logf(st[row]), k = row_kl[row];
+  const float c = gscale[0] * inv_n[0];
+  const T* s = zs + (int64_t)row * lds;
+  const T* t = zt + (int64_t)row * ldt;
+  T* gr = grad + (int64_t)row * ldg;
+  for (int j = threadIdx.x; j < V; j += 256) {
+    const float ls = ldf(s + j) - la, lt = ldf(t + j) - lb;
+    Elem<T>::store(gr + j, expf(ls) * ((ls - lt) - k) * c);
+  }
+}
+
+// out[0] = scale * inv_n * sum x (single workgroup, fixed summation order).
+__global__ __launch_bounds__(1024) void sum_scaled_kernel(int64_t n, const float* __restrict__ x,
+                                                          const float* inv_n, float* out) {
+  __shared__ float red[32];
+  float acc = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) acc += x[i];
+  acc = block_sum(acc, red);
+  if (threadIdx.x == 0) out[0] = acc * (inv_n ? inv_n[0] : 1.f);
+}
+
+// ---------------------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------------------
+#define DISPATCH_T(dtype, ...)                                       \
+  do {                                                               \
+    if ((dtype) == UNOK_BF16) { using T = bf16_t; __VA_ARGS__; }     \
+    else if ((dtype) == UNOK_F32) { using T = float; __VA_ARGS__; }  \
+    else return unok::set_error(UNOK_EINVAL, "bad dtype %d", (dtype)); \
+  } while (0)
+
+UNOK_EXPORT int unok_row_lse_update(int dtype, int R, int Vc, const void* z, int64_t ldz, int c0, const int64_t* tgt,
+                                    float* run_max, float* run_sum, float* zt, int first, void* stream) {
+  if (R == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  DISPATCH_T(dtype, hipLaunchKernelGGL(row_lse_update_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)z, ldz, Vc, c0,
+                                       tgt, run_max, run_sum, zt, first));
+  return unok::check_launch("row_lse_update");
+}
+
+UNOK_EXPORT int unok_row_argmax_update(int dtype, int R, int Vc, const void* z, int64_t ldz, int c0, float* best_val,
+                                       int64_t* best_idx, int first, void* stream) {
+  if (R == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  DISPATCH_T(dtype, hipLaunchKernelGGL(row_argmax_update_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)z, ldz, Vc,
+                                       c0, best_val, best_idx, first));
+  return unok::check_launch("row_argmax_update");
+}
+
+UNOK_EXPORT int unok_ce_finish(int R, const float* run_max, const float* run_sum, const float* zt, const float* w,
+                               const float* inv_n, float* lse, float* loss, void* stream) {
+  hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, R, run_max, run_sum, zt, w, inv_n,
+                     lse, loss);
+  return unok::check_launch("ce_finish");
+}
+
+UNOK_EXPORT int unok_ce_grad_chunk(int out_dtype, int R, int Vc, const float* z, int64_t ldz, int c0, const float* lse,
+                                   const int64_t* tgt, const float* w, const float* gscale, const float* inv_n,
+                                   void* dz, int64_t lddz, void* stream) {
+  if (R == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  if (out_dtype == UNOK_BF16)
+    hipLaunchKernelGGL(ce_grad_chunk_kernel<bf16_t>, dim3(R), dim3(256), 0, st, z, ldz, Vc, c0, lse, tgt, w, gscale,
+                       inv_n, (bf16_t*)dz, lddz);
+  else
+    hipLaunchKernelGGL(ce_grad_chunk_kernel<float>, dim3(R), dim3(256), 0, st, z, ldz, Vc, c0, lse, tgt, w, gscale,
+                       inv_n, (float*)dz, lddz);
+  return unok::check_launch("ce_grad_chunk");
+}
+
+UNOK_EXPORT int unok_softmax_stats(int dtype, int R, int V, const void* z, int64_t ldz, float* mx, float* se,
+                                   void* stream) {
+  if (R == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  DISPATCH_T(dtype, hipLaunchKernelGGL(softmax_stats_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)z, ldz, V, mx, se));
+  return unok::check_launch("softmax_stats");
+}
+
+UNOK_EXPORT int unok_tv_fwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
+                            const float* ms, const float* ss, const float* mt, const float* st_, float* row_l1,
+                            float* row_S, void* stream) {
+  if (R == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  DISPATCH_T(dtype, hipLaunchKernelGGL(tv_fwd_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)zs, lds, (const T*)zt,
+                                       ldt, V, ms, ss, mt, st_, row_l1, row_S));
+  return unok::check_launch("tv_fwd");
+}
+
+UNOK_EXPORT int unok_tv_bwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
+                            const float* ms, const float* ss, const float* mt, const float* st_, const float* row_S,
+                            const float* gscale, const float* inv_n, void* grad, int64_t ldg, void* stream) {
+  if (R == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  DISPATCH_T(dtype, hipLaunchKernelGGL(tv_bwd_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)zs, lds, (const T*)zt,
+                                       ldt, V, ms, ss, mt, st_, row_S, gscale, inv_n, (T*)grad, ldg));
+  return unok::check_launch("tv_bwd");
+}
+
+UNOK_EXPORT int unok_kl_fwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
+                            const float* ms, const float* ss, const float* mt, const float* st_, float* row_kl,
+                            void* stream) {
+  if (R == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  DISPATCH_T(dtype, hipLaunchKernelGGL(kl_fwd_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)zs, lds, (const T*)zt,
+                                       ldt, V, ms, ss, mt, st_, row_kl));
+  return unok::check_launch("kl_fwd");
+}
+
+UNOK_EXPORT int unok_kl_bwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
+                            const float* ms, const float* ss, const float* mt, const float* st_, const float* row_kl,
+                            const float* gscale, const float* inv_n, void* grad, int64_t ldg, void* stream) {
+  if (R == 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  DISPATCH_T(dtype, hipLaunchKernelGGL(kl_bwd_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)zs, lds, (const T*)zt,
+                                       ldt, V, ms, ss, mt, st_, row_kl, gscale, inv_n, (T*)grad, ldg));
+  return unok::check_launch("kl_bwd");
+}
+
+UNOK_EXPORT int unok_sum_scaled(int64_t n, const float* x, const float* inv_n, float* out, void* stream) {
+  hipLaunchKernelGGL(sum_scaled_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, n, x, inv_n, out);
+  return unok::check_launch("sum_scaled");
+}

@@ -13,6 +13,38 @@ import torch
 from . import _native as N
 
 
+class LaunchRecorder:
+    """Brackets selected GEMM launches with HIP events (torch's current stream, which is the
+    stream the kernels run on) to measure their live duration inside a timed region."""
+
+    def __init__(self, predicate):
+        self.predicate = predicate
+        self.records = []   # (start_event, end_event, flops)
+
+    def elapsed(self):
+        torch.cuda.synchronize()
+        ms = [a.elapsed_time(b) for a, b, _ in self.records]
+        fl = [f for _, _, f in self.records]
+        return ms, fl
+
+
+_recorder: LaunchRecorder | None = None
+
+
+def set_recorder(rec: LaunchRecorder | None) -> None:
+    global _recorder
+    _recorder = rec
+
+
+def nt_uses_256_tiles(M: int, N: int, seg_end) -> bool:
+    """Mirror of the tile choice in unok_gemm_nt for bf16 (the 256x256 MFMA kernel)."""
+    if N <= 128:
+        return False
+    if any(e % 256 for e in list(seg_end)[:-1]):
+        return False
+    return ((M + 255) // 256) * ((N + 255) // 256) >= 512
+
+
 def _rowmajor(t: torch.Tensor, name: str) -> None:
     if t.dim() != 2:
         raise RuntimeError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
@@ -74,12 +106,21 @@ def gemm_nt(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
     if gate is not None:
         if gate.dtype not in (torch.bool, torch.uint8) or gate.numel() != M or not gate.is_contiguous():
             raise RuntimeError("gemm_nt: gate must be a contiguous bool/uint8 vector of length M")
+    rec = _recorder
+    if rec is not None and rec.predicate(a.dtype, M, Nn, K, K2, seg_end):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    else:
+        rec = None
     N.call("unok_gemm_nt", N.dtype_code(a.dtype), N.dtype_code(out_dtype), M, Nn, K,
            N.ptr(a), _ld(a), N.ptr(b), _ld(b),
            N.ptr(a2), _ld(a2) if a2 is not None else 0, N.ptr(b2), _ld(b2) if b2 is not None else 0, K2,
            len(seg_end), N.int_array(seg_end), N.int_array(seg_col),
            N.ptr(out), _ld(out), N.ptr(residual), _ld(residual) if residual is not None else 0,
            N.ptr(gate), float(alpha), N.stream())
+    if rec is not None:
+        ev1.record()
+        rec.records.append((ev0, ev1, 2.0 * M * Nn * (K + K2)))
     return out
 
 
@@ -103,3 +144,140 @@ def gemm_tn(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None
     N.call("unok_gemm_tn", N.dtype_code(a.dtype), Mr, P, Q, N.ptr(a), _ld(a), N.ptr(b), _ld(b),
            N.ptr(out), _ld(out), float(alpha), float(beta), N.ptr(ws), ws_bytes, N.stream())
     return out
+
+
+# ------------------------------------------------------------------------------------------
+# Row-wise kernels
+# ------------------------------------------------------------------------------------------
+def _contig(t: torch.Tensor, name: str) -> None:
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def rmsnorm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | None = None):
+    """y = w * round(x * rsqrt(mean(x^2) + eps)); returns (y, rstd[M] fp32)."""
+    _rowmajor(x, "x")
+    M, Hd = x.shape
+    if w.numel() != Hd or w.dtype != x.dtype:
+        raise RuntimeError("rmsnorm: weight must match the hidden size and dtype")
+    y = out if out is not None else torch.empty((M, Hd), device=x.device, dtype=x.dtype)
+    rstd = torch.empty(M, device=x.device, dtype=torch.float32)
+    N.call("unok_rmsnorm_fwd", N.dtype_code(x.dtype), M, Hd, N.ptr(x), _ld(x), N.ptr(w), N.ptr(y), _ld(y),
+           N.ptr(rstd), float(eps), N.stream())
+    return y, rstd
+
+
+def rmsnorm_bwd(dy, x, w, rstd, dres=None, out=None):
+    """dx = rmsnorm backward (+ dres); ``out`` may alias ``dres``."""
+    for t, n in ((dy, "dy"), (x, "x")):
+        _contig(t, n)
+    M, Hd = x.shape
+    dx = out if out is not None else torch.empty_like(x)
+    if dres is not None:
+        _contig(dres, "dres")
+    N.call("unok_rmsnorm_bwd", N.dtype_code(x.dtype), M, Hd, N.ptr(dy), N.ptr(x), N.ptr(w), N.ptr(rstd),
+           N.ptr(dres), N.ptr(dx), N.stream())
+    return dx
+
+
+def qknorm_rope_fwd(qkv, nq, nk, d, wq, wk, pos, inv_freq, eps):
+    """Per-head q/k RMSNorm (when wq/wk are given) then RoPE; returns (q, k, rstd)."""
+    _rowmajor(qkv, "qkv")
+    M = qkv.shape[0]
+    q = torch.empty((M, nq * d), device=qkv.device, dtype=qkv.dtype)
+    k = torch.empty((M, nk * d), device=qkv.device, dtype=qkv.dtype)
+    rstd = torch.empty((M, nq + nk), device=qkv.device, dtype=torch.float32)
+    if pos.dtype != torch.int64 or pos.numel() != M:
+        raise RuntimeError("qknorm_rope: pos must be int64 [M]")
+    N.call("unok_qknorm_rope_fwd", N.dtype_code(qkv.dtype), M, nq, nk, d, N.ptr(qkv), _ld(qkv), N.ptr(wq),
+           N.ptr(wk), N.ptr(pos), N.ptr(inv_freq), float(eps), N.ptr(q), N.ptr(k), N.ptr(rstd), N.stream())
+    return q, k, rstd
+
+
+def qknorm_rope_bwd(dq, dk, qkv, nq, nk, d, wq, wk, pos, inv_freq, rstd, dqkv):
+    """Writes the q and k column blocks of ``dqkv`` ([M, (nq+2nk)*d])."""
+    _contig(dq, "dq")
+    _contig(dk, "dk")
+    M = qkv.shape[0]
+    N.call("unok_qknorm_rope_bwd", N.dtype_code(qkv.dtype), M, nq, nk, d, N.ptr(dq), N.ptr(dk), N.ptr(qkv),
+           _ld(qkv), N.ptr(wq), N.ptr(wk), N.ptr(pos), N.ptr(inv_freq), N.ptr(rstd), N.ptr(dqkv), _ld(dqkv),
+           N.stream())
+    return dqkv
+
+
+def swiglu_fwd(gu, F, out=None):
+    _rowmajor(gu, "gu")
+    M = gu.shape[0]
+    out = out if out is not None else torch.empty((M, F), device=gu.device, dtype=gu.dtype)
+    N.call("unok_swiglu_fwd", N.dtype_code(gu.dtype), M, F, N.ptr(gu), _ld(gu), N.ptr(out), N.stream())
+    return out
+
+
+def swiglu_bwd(dout, gu, F, dgu=None):
+    _contig(dout, "dout")
+    M = gu.shape[0]
+    dgu = dgu if dgu is not None else torch.empty((M, 2 * F), device=gu.device, dtype=gu.dtype)
+    N.call("unok_swiglu_bwd", N.dtype_code(gu.dtype), M, F, N.ptr(dout), N.ptr(gu), _ld(gu), N.ptr(dgu),
+           _ld(dgu), N.stream())
+    return dgu
+
+
+def embedding(ids: torch.Tensor, table: torch.Tensor, out=None):
+    if ids.dtype != torch.int64 or not ids.is_contiguous():
+        raise RuntimeError("embedding: ids must be contiguous int64")
+    _contig(table, "table")
+    M = ids.numel()
+    out = out if out is not None else torch.empty((M, table.shape[1]), device=table.device, dtype=table.dtype)
+    N.call("unok_embedding", table.element_size(), M, table.shape[1], N.ptr(ids), N.ptr(table), table.shape[0],
+           N.ptr(out), N.stream())
+    return out
+
+
+def rows_copy(src: torch.Tensor, dst: torch.Tensor, M: int, smap=None, dmap=None):
+    """dst[dmap[r]] = src[smap[r]] for r < M (maps are int32; None = identity)."""
+    _rowmajor(src, "src")
+    _rowmajor(dst, "dst")
+    if src.dtype != dst.dtype or src.shape[1] != dst.shape[1]:
+        raise RuntimeError("rows_copy: src and dst rows differ")
+    for m in (smap, dmap):
+        if m is not None and (m.dtype != torch.int32 or m.numel() < M):
+            raise RuntimeError("rows_copy: maps must be int32 with >= M entries")
+    es = src.element_size()
+    N.call("unok_rows_copy", src.shape[1] * es, M, N.ptr(src), _ld(src) * es, N.ptr(smap), N.ptr(dst),
+           _ld(dst) * es, N.ptr(dmap), N.stream())
+    return dst
+
+
+# ------------------------------------------------------------------------------------------
+# Block-diffusion attention
+# ------------------------------------------------------------------------------------------
+def attn_fwd(q, k1, v1, iv, Hq, Hkv, D, *, k2=None, v2=None, scale=None):
+    """Returns (O [Mq, Hq*D], LSE2 [Mq, Hq] fp32 = log2-sum-exp2 of the scaled scores)."""
+    _rowmajor(q, "q")
+    Mq = q.shape[0]
+    scale = D ** -0.5 if scale is None else scale
+    if iv.dtype != torch.int32 or tuple(iv.shape) != (Mq, 8):
+        raise RuntimeError("attn_fwd: interval table must be int32 [Mq, 8]")
+    o = torch.empty((Mq, Hq * D), device=q.device, dtype=q.dtype)
+    lse = torch.empty((Mq, Hq), device=q.device, dtype=torch.float32)
+    N.call("unok_attn_fwd", N.dtype_code(q.dtype), Mq, Hq, Hkv, D, N.ptr(q), _ld(q), N.ptr(k1), _ld(k1),
+           N.ptr(v1), _ld(v1), N.ptr(k2), _ld(k2) if k2 is not None else 0, N.ptr(v2),
+           _ld(v2) if v2 is not None else 0, N.ptr(iv), N.ptr(o), _ld(o), N.ptr(lse), float(scale), N.stream())
+    return o, lse
+
+
+def attn_bwd(q, k1, v1, iv, o, lse, do, Hq, Hkv, D, *, k2=None, v2=None, ivk=None, dk=None, dv=None,
+             scale=None):
+    """Returns dQ; writes dK/dV of source-2 keys into ``dk``/``dv`` when given."""
+    Mq = q.shape[0]
+    scale = D ** -0.5 if scale is None else scale
+    _contig(do, "do")
+    dq = torch.empty((Mq, Hq * D), device=q.device, dtype=q.dtype)
+    dsum = torch.empty((Mq, Hq), device=q.device, dtype=torch.float32)
+    Mk2 = k2.shape[0] if k2 is not None else 0
+    N.call("unok_attn_bwd", N.dtype_code(q.dtype), Mq, Mk2, Hq, Hkv, D, N.ptr(q), _ld(q), N.ptr(k1), _ld(k1),
+           N.ptr(v1), _ld(v1), N.ptr(k2), _ld(k2) if k2 is not None else 0, N.ptr(v2),
+           _ld(v2) if v2 is not None else 0, N.ptr(iv), N.ptr(ivk), N.ptr(o), _ld(o), N.ptr(lse), N.ptr(do),
+           _ld(do), N.ptr(dsum), N.ptr(dq), _ld(dq), N.ptr(dk), _ld(dk) if dk is not None else 0, N.ptr(dv),
+           _ld(dv) if dv is not None else 0, float(scale), N.stream())
+    return dq

@@ -1,0 +1,227 @@
+"""Decoder-layer math of the conditional-LoRA block-diffusion step on the HIP kernels.
+
+The reference runs one transformer pass over 2L rows per sequence ([noisy | clean] per
+segment, training/modeling.py:65-81, 116-147) with LoRA gated to the noisy rows
+(training/lora.py:164-174) and back-propagates through all 2L rows. Here the two streams are
+computed separately, which is exact for this mask and gate:
+
+* the clean stream has LoRA off and attends only to clean keys (causal), so it does not
+  depend on the LoRA weights: it runs forward-only and keeps only its per-layer K/V;
+* the noisy stream (LoRA on) attends to the clean K/V of strictly earlier blocks plus its own
+  block; it is the only stream with a backward pass. Each noisy decoder layer is one
+  autograd Function whose backward drives the fused kernels and accumulates the LoRA
+  gradients straight into the flat gradient buffer of the adapter (see adapter.LoraState).
+
+Per layer (x = RMSNorm(h)):  q|k|v = x W_qkv^T + s B (x A)   -> q/k RMSNorm + RoPE
+                            h += attn(q, k, v) W_o^T + s B_o (attn A_o)
+                            h += down(silu(gate) * up) with gate|up one fused projection.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import kernels as K
+
+
+@dataclass
+class LayerWeights:
+    """Frozen weights of one decoder layer (fused projections plus transposed copies)."""
+    w_qkv: torch.Tensor      # [q+2kv, H]
+    w_qkv_t: torch.Tensor    # [H, q+2kv]
+    w_o: torch.Tensor        # [H, q]
+    w_o_t: torch.Tensor      # [q, H]
+    w_gu: torch.Tensor       # [2F, H]
+    w_gu_t: torch.Tensor     # [H, 2F]
+    w_d: torch.Tensor        # [H, F]
+    w_d_t: torch.Tensor      # [F, H]
+    ln_in: torch.Tensor
+    ln_post: torch.Tensor
+    q_norm: torch.Tensor | None
+    k_norm: torch.Tensor | None
+
+
+@dataclass
+class Geometry:
+    nq: int
+    nk: int
+    d: int
+    H: int
+    F: int
+    eps: float
+
+    @property
+    def q(self):
+        return self.nq * self.d
+
+    @property
+    def kv(self):
+        return self.nk * self.d
+
+
+@dataclass
+class StreamContext:
+    """Per-forward data shared by all layers: positions, interval tables, clean K/V."""
+    pos: torch.Tensor            # [M] int64 positions of stream rows
+    inv_freq: torch.Tensor       # [d/2] fp32
+    iv_noisy: torch.Tensor       # [M, 8] int32
+    iv_clean: torch.Tensor       # [M, 8] int32
+    clean_k: list                # per layer [M, kv]
+    clean_v: list
+
+
+def clean_layer(h: torch.Tensor, lw: LayerWeights, g: Geometry, sc: StreamContext):
+    """Forward-only clean-stream layer; returns (h_out, k, v) with k/v kept for the noisy stream."""
+    M = h.shape[0]
+    x1, _ = K.rmsnorm_fwd(h, lw.ln_in, g.eps)
+    qkv = K.gemm_nt(x1, lw.w_qkv)
+    q, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
+    v = torch.empty((M, g.kv), device=h.device, dtype=h.dtype)
+    K.rows_copy(qkv[:, g.q + g.kv:], v, M)
+    o, _ = K.attn_fwd(q, k, v, sc.iv_clean, g.nq, g.nk, g.d)
+    h1 = K.gemm_nt(o, lw.w_o, residual=h)
+    x2, _ = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
+    gu = K.gemm_nt(x2, lw.w_gu)
+    s = K.swiglu_fwd(gu, g.F)
+    h2 = K.gemm_nt(s, lw.w_d, residual=h1)
+    return h2, k, v
+
+
+class NoisyLayer(torch.autograd.Function):
+    """One noisy-stream decoder layer with fused gated LoRA (forward and backward)."""
+
+    @staticmethod
+    def forward(ctx, h0, anchor, lw: LayerWeights, lora, li: int, g: Geometry, sc: StreamContext):
+        del anchor
+        r = lora.rank
+        q_end, k_end = g.q, g.q + g.kv
+        x1, rstd1 = K.rmsnorm_fwd(h0, lw.ln_in, g.eps)
+        h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv"))
+        qkv = K.gemm_nt(x1, lw.w_qkv, a2=h_qkv, b2=lora.sb_c(li, "qkv"),
+                        segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)])
+        q, k, rstd_qk = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
+        v = qkv[:, k_end:]
+        o, lse = K.attn_fwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, g.nq, g.nk, g.d, k2=k, v2=v)
+        h_o = K.gemm_nt(o, lora.a_c(li, "o"))
+        h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o"), residual=h0)
+        x2, rstd2 = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
+        h_gu = K.gemm_nt(x2, lora.a_c(li, "gu"))
+        gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu"), segments=[(g.F, 0), (2 * g.F, r)])
+        s = K.swiglu_fwd(gu, g.F)
+        h_d = K.gemm_nt(s, lora.a_c(li, "d"))
+        h2 = K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d"), residual=h1)
+        ctx.lw, ctx.lora, ctx.li, ctx.g, ctx.sc = lw, lora, li, g, sc
+        ctx.bufs = (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d)
+        return h2
+
+    @staticmethod
+    def backward(ctx, dh2):
+        lw, lora, li, g, sc = ctx.lw, ctx.lora, ctx.li, ctx.g, ctx.sc
+        (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d) = ctx.bufs
+        ctx.bufs = None
+        dh2 = dh2.contiguous()
+        M = dh2.shape[0]
+        r, sc_l = lora.rank, lora.scale
+        q_end, k_end = g.q, g.q + g.kv
+        ga, gb = lora.grad_a, lora.grad_b
+        # ---- down projection ----------------------------------------------------------
+        g_d = K.gemm_nt(dh2, lora.sb_t(li, "d"))                              # [M, r]
+        K.gemm_tn(dh2, h_d, out=gb(li, "d"), alpha=sc_l, beta=1.0)            # dB_d
+        ds = K.gemm_nt(dh2, lw.w_d_t, a2=g_d, b2=lora.a_t(li, "d"))           # [M, F]
+        K.gemm_tn(g_d, s, out=ga(li, "d"), beta=1.0)                          # dA_d
+        dgu = K.swiglu_bwd(ds, gu, g.F)
+        del ds
+        # ---- gate | up -----------------------------------------------------------------
+        g_gu = torch.empty((M, 2 * r), device=dh2.device, dtype=dh2.dtype)
+        sbt = lora.sb_t(li, "gu")
+        gbgu = gb(li, "gu")
+        for j, (c0, c1) in enumerate(((0, g.F), (g.F, 2 * g.F))):
+            K.gemm_nt(dgu[:, c0:c1], sbt[:, c0:c1], out=g_gu[:, j * r:(j + 1) * r])
+            K.gemm_tn(dgu[:, c0:c1], h_gu[:, j * r:(j + 1) * r], out=gbgu[c0:c1], alpha=sc_l, beta=1.0)
+        dx2 = K.gemm_nt(dgu, lw.w_gu_t, a2=g_gu, b2=lora.a_t(li, "gu"))
+        K.gemm_tn(g_gu, x2, out=ga(li, "gu"), beta=1.0)
+        del dgu
+        dh1 = K.rmsnorm_bwd(dx2, h1, lw.ln_post, rstd2, dres=dh2)
+        del dx2
+        # ---- o projection --------------------------------------------------------------
+        g_o = K.gemm_nt(dh1, lora.sb_t(li, "o"))
+        K.gemm_tn(dh1, h_o, out=gb(li, "o"), alpha=sc_l, beta=1.0)
+        do = K.gemm_nt(dh1, lw.w_o_t, a2=g_o, b2=lora.a_t(li, "o"))
+        K.gemm_tn(g_o, o, out=ga(li, "o"), beta=1.0)
+        # ---- attention -----------------------------------------------------------------
+        dqkv = torch.empty_like(qkv)
+        dk = torch.empty((M, g.kv), device=dh2.device, dtype=dh2.dtype)
+        dq = K.attn_bwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, o, lse, do, g.nq, g.nk, g.d,
+                        k2=k, v2=qkv[:, k_end:], ivk=sc.iv_noisy, dk=dk, dv=dqkv[:, k_end:])
+        del do
+        K.qknorm_rope_bwd(dq, dk, qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, rstd_qk, dqkv)
+        del dq, dk
+        # ---- q | k | v -----------------------------------------------------------------
+        g_qkv = torch.empty((M, 3 * r), device=dh2.device, dtype=dh2.dtype)
+        sbt = lora.sb_t(li, "qkv")
+        gbqkv = gb(li, "qkv")
+        for j, (c0, c1) in enumerate(((0, q_end), (q_end, k_end), (k_end, k_end + g.kv))):
+            K.gemm_nt(dqkv[:, c0:c1], sbt[:, c0:c1], out=g_qkv[:, j * r:(j + 1) * r])
+            K.gemm_tn(dqkv[:, c0:c1], h_qkv[:, j * r:(j + 1) * r], out=gbqkv[c0:c1], alpha=sc_l, beta=1.0)
+        K.gemm_tn(g_qkv, x1, out=ga(li, "qkv"), beta=1.0)
+        dh0 = None
+        if ctx.needs_input_grad[0]:
+            dx1 = K.gemm_nt(dqkv, lw.w_qkv_t, a2=g_qkv, b2=lora.a_t(li, "qkv"))
+            dh0 = K.rmsnorm_bwd(dx1, h0, lw.ln_in, rstd1, dres=dh1)
+        return dh0, None, None, None, None, None, None
+
+
+class FinalNorm(torch.autograd.Function):
+    """Final RMSNorm of the noisy stream."""
+
+    @staticmethod
+    def forward(ctx, h, w, eps, anchor):
+        del anchor
+        y, rstd = K.rmsnorm_fwd(h, w, eps)
+        ctx.bufs = (h, w, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        h, w, rstd = ctx.bufs
+        ctx.bufs = None
+        return K.rmsnorm_bwd(dy.contiguous(), h, w, rstd), None, None, None
+
+
+class ScatterStreams(torch.autograd.Function):
+    """Writes the noisy and clean streams into the [B*2L, H] concatenated layout."""
+
+    @staticmethod
+    def forward(ctx, noisy, clean, noisy_src, clean_src):
+        M = noisy.shape[0]
+        out = torch.empty((2 * M, noisy.shape[1]), device=noisy.device, dtype=noisy.dtype)
+        K.rows_copy(noisy, out, M, dmap=noisy_src)
+        K.rows_copy(clean, out, M, dmap=clean_src)
+        ctx.noisy_src = noisy_src
+        ctx.M = M
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        dout = dout.contiguous()
+        dn = torch.empty((ctx.M, dout.shape[1]), device=dout.device, dtype=dout.dtype)
+        K.rows_copy(dout, dn, ctx.M, smap=ctx.noisy_src)
+        return dn, None, None, None
+
+
+class GatherRows(torch.autograd.Function):
+    """out[i] = x[idx[i]] (int32 idx); backward scatters into zeros."""
+
+    @staticmethod
+    def forward(ctx, x, idx):
+        out = torch.empty((idx.numel(), x.shape[1]), device=x.device, dtype=x.dtype)
+        K.rows_copy(x, out, idx.numel(), smap=idx)
+        ctx.idx, ctx.rows = idx, x.shape[0]
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        dx = torch.zeros((ctx.rows, dout.shape[1]), device=dout.device, dtype=dout.dtype)
+        K.rows_copy(dout.contiguous(), dx, ctx.idx.numel(), dmap=ctx.idx)
+        return dx, None

@@ -1,0 +1,203 @@
+"""LM-head objectives of the Uno step on the HIP kernels.
+
+* ``fused_weighted_ce``: CE with the diffusion 1/t weighting (training/trainer.py:267-283),
+  evaluated over vocabulary chunks: each chunk's logits are produced by the MFMA GEMM into a
+  chunk buffer and folded into a running per-row log-sum-exp; the backward recomputes each
+  chunk and feeds dz = g w (softmax - onehot) straight into the data-gradient GEMM. The full
+  [rows x vocab] logits are never materialised.
+* ``teacher_argmax``: first-index argmax of the clean-stream logits, chunked the same way
+  (training/losses.py:38-56, target source "clean_argmax").
+* ``distribution_losses``: reverse KL and total variation (training/losses.py:59-183) over
+  bf16 logits of the supervised rows, fp32 per-row statistics, with hand-written backward.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+from . import kernels as K
+
+DEFAULT_CE_CHUNK = 16384
+
+
+def lm_head_logits(lm_head, x: torch.Tensor) -> torch.Tensor:
+    """Plain logits (used by project_hidden_states); differentiable w.r.t. x."""
+    shape = x.shape
+    out = _Logits.apply(x.reshape(-1, shape[-1]), lm_head.weight, lm_head.weight_t)
+    return out.view(*shape[:-1], lm_head.weight.shape[0])
+
+
+class _Logits(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, w_t):
+        x = x.contiguous()
+        ctx.w_t = w_t
+        return K.gemm_nt(x, w)
+
+    @staticmethod
+    def backward(ctx, dz):
+        return K.gemm_nt(dz.contiguous(), ctx.w_t), None, None
+
+
+def _chunks(V: int, chunk: int):
+    for c0 in range(0, V, chunk):
+        yield c0, min(V, c0 + chunk)
+
+
+class ChunkedWeightedCE(torch.autograd.Function):
+    """loss = inv_n * sum_r w_r * CE(h_r W^T, y_r); inv_n is a device scalar."""
+
+    @staticmethod
+    def forward(ctx, h, w_lm, w_lm_t, targets, weights, inv_n, chunk):
+        h = h.contiguous()
+        R, V = h.shape[0], w_lm.shape[0]
+        dev = h.device
+        f32 = dict(device=dev, dtype=torch.float32)
+        run_max, run_sum, zt = torch.empty(R, **f32), torch.empty(R, **f32), torch.zeros(R, **f32)
+        lse = torch.empty(R, **f32)
+        loss = torch.empty((), **f32)
+        buf = torch.empty((R, min(chunk, V)), **f32)
+        for i, (c0, c1) in enumerate(_chunks(V, chunk)):
+            z = buf[:, :c1 - c0]
+            K.gemm_nt(h, w_lm[c0:c1], out=z)
+            N.call("unok_row_lse_update", N.F32, R, c1 - c0, N.ptr(z), buf.stride(0), c0, N.ptr(targets),
+                   N.ptr(run_max), N.ptr(run_sum), N.ptr(zt), int(i == 0), N.stream())
+        N.call("unok_ce_finish", R, N.ptr(run_max), N.ptr(run_sum), N.ptr(zt), N.ptr(weights), N.ptr(inv_n),
+               N.ptr(lse), N.ptr(loss), N.stream())
+        ctx.save = (h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk)
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk = ctx.save
+        ctx.save = None
+        R, V = h.shape[0], w_lm.shape[0]
+        g = g.reshape(1).float().contiguous()
+        f32 = dict(device=h.device, dtype=torch.float32)
+        buf = torch.empty((R, min(chunk, V)), **f32)
+        dz = torch.empty((R, min(chunk, V)), device=h.device, dtype=h.dtype)
+        dh = torch.zeros(h.shape, **f32)
+        for c0, c1 in _chunks(V, chunk):
+            z = buf[:, :c1 - c0]
+            K.gemm_nt(h, w_lm[c0:c1], out=z)
+            d = dz[:, :c1 - c0]
+            N.call("unok_ce_grad_chunk", N.dtype_code(h.dtype), R, c1 - c0, N.ptr(z), buf.stride(0), c0, N.ptr(lse),
+                   N.ptr(targets), N.ptr(weights), N.ptr(g), N.ptr(inv_n), N.ptr(d), dz.stride(0), N.stream())
+            K.gemm_nt(d, w_lm_t[:, c0:c1], out=dh, residual=dh)
+        return dh.to(h.dtype), None, None, None, None, None, None
+
+
+def fused_weighted_ce(lm_head, h_rows: torch.Tensor, targets: torch.Tensor, weights: torch.Tensor,
+                      inv_n: torch.Tensor, chunk: int = DEFAULT_CE_CHUNK) -> torch.Tensor:
+    if h_rows.shape[0] == 0:
+        return h_rows.sum() * 0.0
+    return ChunkedWeightedCE.apply(h_rows, lm_head.weight, lm_head.weight_t, targets.contiguous(),
+                                   weights.contiguous().float(), inv_n, chunk)
+
+
+@torch.no_grad()
+def teacher_argmax(lm_head, h_rows: torch.Tensor, chunk: int = DEFAULT_CE_CHUNK) -> torch.Tensor:
+    R, V = h_rows.shape[0], lm_head.weight.shape[0]
+    h_rows = h_rows.contiguous()
+    best_val = torch.empty(R, device=h_rows.device, dtype=torch.float32)
+    best_idx = torch.empty(R, device=h_rows.device, dtype=torch.int64)
+    if R == 0:
+        return best_idx
+    buf = torch.empty((R, min(chunk, V)), device=h_rows.device, dtype=h_rows.dtype)
+    for i, (c0, c1) in enumerate(_chunks(V, chunk)):
+        z = buf[:, :c1 - c0]
+        K.gemm_nt(h_rows, lm_head.weight[c0:c1], out=z)
+        N.call("unok_row_argmax_update", N.dtype_code(z.dtype), R, c1 - c0, N.ptr(z), buf.stride(0), c0,
+               N.ptr(best_val), N.ptr(best_idx), int(i == 0), N.stream())
+    return best_idx
+
+
+class DistributionLoss(torch.autograd.Function):
+    """kind 'tv': sum |p_s - p_t| * inv_n;  kind 'kl': sum p_s (log p_s - log p_t) * inv_n.
+    Student logits are computed from h_s (differentiable), teacher logits from h_t (detached)."""
+
+    @staticmethod
+    def forward(ctx, h_s, h_t, w_lm, w_lm_t, inv_n, kind):
+        h_s, h_t = h_s.contiguous(), h_t.contiguous()
+        R, V = h_s.shape[0], w_lm.shape[0]
+        zs = K.gemm_nt(h_s, w_lm)
+        zt = K.gemm_nt(h_t, w_lm)
+        f32 = dict(device=h_s.device, dtype=torch.float32)
+        ms, ss, mt, st = (torch.empty(R, **f32) for _ in range(4))
+        dt = N.dtype_code(zs.dtype)
+        N.call("unok_softmax_stats", dt, R, V, N.ptr(zs), V, N.ptr(ms), N.ptr(ss), N.stream())
+        N.call("unok_softmax_stats", dt, R, V, N.ptr(zt), V, N.ptr(mt), N.ptr(st), N.stream())
+        rows = torch.empty(R, **f32)
+        extra = torch.empty(R, **f32)
+        if kind == "tv":
+            N.call("unok_tv_fwd", dt, R, V, N.ptr(zs), V, N.ptr(zt), V, N.ptr(ms), N.ptr(ss), N.ptr(mt), N.ptr(st),
+                   N.ptr(rows), N.ptr(extra), N.stream())
+        elif kind == "kl":
+            N.call("unok_kl_fwd", dt, R, V, N.ptr(zs), V, N.ptr(zt), V, N.ptr(ms), N.ptr(ss), N.ptr(mt), N.ptr(st),
+                   N.ptr(rows), N.stream())
+            extra = rows
+        else:
+            raise ValueError(kind)
+        loss = torch.empty((), **f32)
+        N.call("unok_sum_scaled", R, N.ptr(rows), N.ptr(inv_n), N.ptr(loss), N.stream())
+        ctx.save = (zs, zt, ms, ss, mt, st, extra, inv_n, w_lm_t, kind)
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        zs, zt, ms, ss, mt, st, extra, inv_n, w_lm_t, kind = ctx.save
+        ctx.save = None
+        R, V = zs.shape
+        g = g.reshape(1).float().contiguous()
+        dt = N.dtype_code(zs.dtype)
+        fn = "unok_tv_bwd" if kind == "tv" else "unok_kl_bwd"
+        N.call(fn, dt, R, V, N.ptr(zs), V, N.ptr(zt), V, N.ptr(ms), N.ptr(ss), N.ptr(mt), N.ptr(st), N.ptr(extra),
+               N.ptr(g), N.ptr(inv_n), N.ptr(zs), V, N.stream())
+        dh = K.gemm_nt(zs, w_lm_t)
+        return dh, None, None, None, None, None
+
+
+def distribution_loss(lm_head, h_s, h_t, inv_n, kind: str) -> torch.Tensor:
+    if h_s.shape[0] == 0:
+        return h_s.sum() * 0.0
+    return DistributionLoss.apply(h_s, h_t.detach(), lm_head.weight, lm_head.weight_t, inv_n, kind)
+
+
+class LogitsDistributionLoss(torch.autograd.Function):
+    """TV / reverse KL over given logits (the losses.py call surface); gradient w.r.t. student."""
+
+    @staticmethod
+    def forward(ctx, zs, zt, inv_n, kind):
+        zs, zt = zs.contiguous(), zt.contiguous()
+        R, V = zs.shape
+        f32 = dict(device=zs.device, dtype=torch.float32)
+        ms, ss, mt, st = (torch.empty(R, **f32) for _ in range(4))
+        dt = N.dtype_code(zs.dtype)
+        if zt.dtype != zs.dtype:
+            raise RuntimeError("student and teacher logits must share a dtype")
+        N.call("unok_softmax_stats", dt, R, V, N.ptr(zs), V, N.ptr(ms), N.ptr(ss), N.stream())
+        N.call("unok_softmax_stats", dt, R, V, N.ptr(zt), V, N.ptr(mt), N.ptr(st), N.stream())
+        rows, extra = torch.empty(R, **f32), torch.empty(R, **f32)
+        if kind == "tv":
+            N.call("unok_tv_fwd", dt, R, V, N.ptr(zs), V, N.ptr(zt), V, N.ptr(ms), N.ptr(ss), N.ptr(mt), N.ptr(st),
+                   N.ptr(rows), N.ptr(extra), N.stream())
+        else:
+            N.call("unok_kl_fwd", dt, R, V, N.ptr(zs), V, N.ptr(zt), V, N.ptr(ms), N.ptr(ss), N.ptr(mt), N.ptr(st),
+                   N.ptr(rows), N.stream())
+            extra = rows
+        loss = torch.empty((), **f32)
+        N.call("unok_sum_scaled", R, N.ptr(rows), N.ptr(inv_n), N.ptr(loss), N.stream())
+        ctx.save = (zs, zt, ms, ss, mt, st, extra, inv_n, kind)
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        zs, zt, ms, ss, mt, st, extra, inv_n, kind = ctx.save
+        ctx.save = None
+        R, V = zs.shape
+        g = g.reshape(1).float().contiguous()
+        grad = torch.empty_like(zs)
+        fn = "unok_tv_bwd" if kind == "tv" else "unok_kl_bwd"
+        N.call(fn, N.dtype_code(zs.dtype), R, V, N.ptr(zs), V, N.ptr(zt), V, N.ptr(ms), N.ptr(ss), N.ptr(mt),
+               N.ptr(st), N.ptr(extra), N.ptr(g), N.ptr(inv_n), N.ptr(grad), V, N.stream())
+        return grad, None, None, None
