@@ -304,3 +304,28 @@ def test_fused_adamw_matches_torch(dev):
     assert (mine - theirs).abs().max().item() < 1e-6
     assert torch.equal(copy[:40_000], p[:40_000].bfloat16())
     assert torch.equal(copy[40_000:], (p[40_000:] * 2.0).bfloat16())
+
+
+def test_bf16_rounding_matches_torch(dev):
+    """The kernels' float->bf16 conversion is round-to-nearest-even like torch's, bit for bit."""
+    from uno_amd import _native as N
+    torch.manual_seed(8)
+    x = torch.randn(1 << 16, device=dev) * torch.exp2(torch.randint(-140, 120, (1 << 16,), device=dev).float())
+    specials = torch.tensor([0.0, -0.0, float("inf"), float("-inf"), 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8,
+                             -(1.0 + 2 ** -8), 3.4e38, 1e-45, -1e-40], device=dev)
+    # exact ties: mantissa ending in 0x8000 rounds to even
+    ties = (torch.randint(0, 1 << 15, (4096,), device=dev, dtype=torch.int32) * 65536 + 0x3F808000).view(torch.float32)
+    x = torch.cat([x, specials, ties]).contiguous()
+    out = torch.empty(x.numel(), device=dev, dtype=torch.bfloat16)
+    N.call("unok_cast_copy", N.BF16, x.numel(), x.numel(), 1.0, N.ptr(x), N.ptr(out), N.stream())
+    mine, ref = out.view(torch.int16), x.bfloat16().view(torch.int16)
+    # NaN payloads are not specified by either conversion: any NaN output counts as a match
+    diff = (mine != ref) & ~(torch.isnan(x) & torch.isnan(out.float()))
+    denormal = (x != 0) & (x.abs() < 2.0 ** -126)
+    bad = diff & ~denormal
+    print(f"[bf16 rounding] {int(diff.sum())} of {x.numel()} differ; {int(denormal.sum())} fp32-denormal inputs; "
+          f"non-denormal mismatches {int(bad.sum())}: {x[bad][:8].tolist()}")
+    assert not bad.any()
+    # fp32-denormal inputs may be flushed to a signed zero by the hardware conversion
+    flushed = diff & denormal
+    assert ((mine[flushed] & 0x7FFF) == 0).all()

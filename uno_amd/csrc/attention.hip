@@ -41,12 +41,13 @@ struct AttnArgs {
 __device__ __forceinline__ bf16x8_t ld_bf16x8(const bf16_t* p) { return *(const bf16x8_t*)p; }
 
 __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
-  uint4 u;
-  bf16_t* h = (bf16_t*)&u;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) h[i] = f32_to_bf16(v[i]);
+  uint4 u = make_uint4(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]), pack2_bf16(v[4], v[5]), pack2_bf16(v[6], v[7]));
   return __builtin_bit_cast(bf16x8_t, u);
 }
+
+// 2^x with the bare hardware instruction (inputs here are <= 8; results that would be
+// denormal flush towards zero, which is immaterial for softmax weights).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // A operand for a 16-key MFMA step read from a transposed [D][keys] LDS tile, with the key
 // permutation of the accumulator layout: lane group g supplies keys base+4g+{0..3} and
@@ -91,6 +92,56 @@ __device__ __forceinline__ void stage_tile(const bf16_t* src, int64_t ld, int co
   }
 }
 
+// Register staging of a [64 rows x D] tile: global loads into four flat uint4 registers
+// (issued early so they overlap the current tile's math), then row-major and/or transposed LDS
+// stores. Flat locals (rather than an array or struct) keep the staging in VGPRs under this
+// kernel's register pressure. D = 128 uses all four registers per thread, D = 64 the first two.
+__device__ __forceinline__ uint4 tile_ld(const bf16_t* __restrict__ src, int64_t ld, int col0, int r0, int rend, int i,
+                                         int cpr) {
+  const int c = threadIdx.x + 256 * i, r = c / cpr, dc = (c % cpr) * 8;
+  // Rows past rend re-read the last valid row: their scores are masked (p = 0) and the data is
+  // finite, so no zero fill (and no divergent branch) is needed.
+  const int row = min(r0 + r, rend - 1);
+  return *(const uint4*)(src + (int64_t)row * ld + col0 + dc);
+}
+
+__device__ __forceinline__ void tile_st_row(uint4 v, bf16_t* dst, int rs, int i, int cpr) {
+  const int c = threadIdx.x + 256 * i, r = c / cpr, dc = (c % cpr) * 8;
+  *(uint4*)&dst[r * rs + dc] = v;
+}
+
+__device__ __forceinline__ void tile_st_trans(uint4 v, bf16_t* dst, int ts, int i, int cpr) {
+  const int c = threadIdx.x + 256 * i, r = c / cpr, dc = (c % cpr) * 8;
+  bf16_t* col = dst + dc * ts + r;
+  col[0 * ts] = (bf16_t)(v.x & 0xffffu);
+  col[1 * ts] = (bf16_t)(v.x >> 16);
+  col[2 * ts] = (bf16_t)(v.y & 0xffffu);
+  col[3 * ts] = (bf16_t)(v.y >> 16);
+  col[4 * ts] = (bf16_t)(v.z & 0xffffu);
+  col[5 * ts] = (bf16_t)(v.z >> 16);
+  col[6 * ts] = (bf16_t)(v.w & 0xffffu);
+  col[7 * ts] = (bf16_t)(v.w >> 16);
+}
+
+#define UNOK_TILE_LOAD(pfx, src, ld, col0, r0, rend)                         \
+  do {                                                                       \
+    pfx##0 = tile_ld(src, ld, col0, r0, rend, 0, D / 8);                     \
+    pfx##1 = tile_ld(src, ld, col0, r0, rend, 1, D / 8);                     \
+    if constexpr (D == 128) {                                                \
+      pfx##2 = tile_ld(src, ld, col0, r0, rend, 2, D / 8);                   \
+      pfx##3 = tile_ld(src, ld, col0, r0, rend, 3, D / 8);                   \
+    }                                                                        \
+  } while (0)
+#define UNOK_TILE_STORE(fn, pfx, dst, stride)                                \
+  do {                                                                       \
+    fn(pfx##0, dst, stride, 0, D / 8);                                       \
+    fn(pfx##1, dst, stride, 1, D / 8);                                       \
+    if constexpr (D == 128) {                                                \
+      fn(pfx##2, dst, stride, 2, D / 8);                                     \
+      fn(pfx##3, dst, stride, 3, D / 8);                                     \
+    }                                                                        \
+  } while (0)
+
 // Interval bounds reduced over a workgroup's 4 waves. Empty intervals are ignored.
 struct Bounds { int lo, hi, maxlo, minhi; };
 
@@ -126,7 +177,9 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_kernel(const AttnArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
   const int nqt = (p.Mq + 127) / 128;
   const int lin = xcd_remap(blockIdx.x, nqt * p.Hq);
-  const int h = lin % p.Hq, qt = lin / p.Hq;
+  // q tiles are walked from the last to the first: with causal-like masks the late tiles carry
+  // the most key tiles, so the heaviest workgroups start first and the tail is light.
+  const int h = lin % p.Hq, qt = nqt - 1 - lin / p.Hq;
   const int kvh = h / (p.Hq / p.Hkv);
   const int qrow = qt * 128 + w * 32 + lq;
   const bool qvalid = qrow < p.Mq;
@@ -148,82 +201,111 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_kernel(const AttnArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
 
+  // Tile walk over both sources: tiles [0, n1) come from source 1, [n1, n1 + n2) from source 2.
+  const Bounds wb1 = wave_bounds(qvalid, ivq.x, ivq.y);
+  const Bounds wb2 = wave_bounds(qvalid && p.K2 != nullptr, ivq.z, ivq.w);
+  int kb1, ke1, kb2, ke2;
+  wg_bounds(wb1, sh, kb1, ke1);
+  wg_bounds(wb2, sh, kb2, ke2);
+  const int n1 = kb1 < ke1 ? (ke1 - (kb1 / BK) * BK + BK - 1) / BK : 0;
+  const int n2 = (p.K2 != nullptr && kb2 < ke2) ? (ke2 - (kb2 / BK) * BK + BK - 1) / BK : 0;
+  const int nt = n1 + n2;
+  const bf16_t* K1 = (const bf16_t*)p.K1;
+  const bf16_t* V1 = (const bf16_t*)p.V1;
+  const bf16_t* K2 = (const bf16_t*)p.K2;
+  const bf16_t* V2 = (const bf16_t*)p.V2;
+  // Next-tile prefetch: the source is selected with scalar selects (no branch writing the
+  // staging registers).
+  uint4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
+  kr2 = kr3 = vr2 = vr3 = make_uint4(0, 0, 0, 0);
+#define UNOK_FETCH(t_)                                                                     \
+  do {                                                                                     \
+    const bool f2 = (t_) >= n1;                                                            \
+    const int fkt = f2 ? (kb2 / BK) * BK + ((t_) - n1) * BK : (kb1 / BK) * BK + (t_) * BK;   \
+    const int fke = f2 ? ke2 : ke1;                                                        \
+    const bf16_t* fk = f2 ? K2 : K1;                                                       \
+    const bf16_t* fv = f2 ? V2 : V1;                                                       \
+    const int64_t fldk = f2 ? p.ldk2 : p.ldk1, fldv = f2 ? p.ldv2 : p.ldv1;               \
+    UNOK_TILE_LOAD(kr, fk, fldk, kvh * D, fkt, fke);                                       \
+    UNOK_TILE_LOAD(vr, fv, fldv, kvh * D, fkt, fke);                                       \
+  } while (0)
+  if (nt > 0) UNOK_FETCH(0);
 #pragma unroll 1
-  for (int src = 0; src < 2; ++src) {
-    const bf16_t* Kp = (const bf16_t*)(src ? p.K2 : p.K1);
-    const bf16_t* Vp = (const bf16_t*)(src ? p.V2 : p.V1);
-    const int64_t ldk = src ? p.ldk2 : p.ldk1, ldv = src ? p.ldv2 : p.ldv1;
-    if (Kp == nullptr) continue;
-    const int lo = src ? ivq.z : ivq.x, hi = src ? ivq.w : ivq.y;
-    const Bounds wb = wave_bounds(qvalid, lo, hi);
-    int kb, ke;
-    wg_bounds(wb, sh, kb, ke);
-    if (kb >= ke) continue;
-#pragma unroll 1
-    for (int kt = (kb / BK) * BK; kt < ke; kt += BK) {
-      __syncthreads();
-      stage_tile<D, true, false, KS, VS>(Kp, ldk, kvh * D, kt, ke, Ks, nullptr);
-      stage_tile<D, false, true, KS, VS>(Vp, ldv, kvh * D, kt, ke, nullptr, Vt);
-      __syncthreads();
-      if (kt >= wb.hi || kt + BK <= wb.lo) continue;
-      const bool full = kt >= wb.maxlo && kt + BK <= wb.minhi;
-      f32x16_t sacc[2];
+  for (int t = 0; t < nt; ++t) {
+    __syncthreads();
+    UNOK_TILE_STORE(tile_st_row, kr, Ks, KS);
+    UNOK_TILE_STORE(tile_st_trans, vr, Vt, VS);
+    __syncthreads();
+    if (t + 1 < nt) UNOK_FETCH(t + 1);
+    const bool s2 = t >= n1;
+    const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
+    const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
+    const int w_maxlo = s2 ? wb2.maxlo : wb1.maxlo, w_minhi = s2 ? wb2.minhi : wb1.minhi;
+    const int lo = s2 ? ivq.z : ivq.x, hi = s2 ? ivq.w : ivq.y;
+    if (kt >= w_hi || kt + BK <= w_lo) continue;
+    const bool full = kt >= w_maxlo && kt + BK <= w_minhi;
+    f32x16_t sacc[2];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kk][r] = 0.f;
+      for (int r = 0; r < 16; ++r) sacc[kk][r] = 0.f;
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-          sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Ks[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
-                                                              qreg[ks], sacc[kk], 0, 0, 0);
-      }
-      float tmax = -INFINITY;
+    for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
+        sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Ks[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
+                                                            qreg[ks], sacc[kk], 0, 0, 0);
+    float tmax = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          float v = sacc[kk][j] * p.scale_log2;
-          if (!full) {
-            const int key = kt + kk * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-            if (key < lo || key >= hi) v = -INFINITY;
-          }
-          sacc[kk][j] = v;
-          tmax = fmaxf(tmax, v);
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float v = sacc[kk][j] * p.scale_log2;
+        if (!full) {
+          const int key = kt + kk * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
+          if (key < lo || key >= hi) v = -INFINITY;
         }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run, tmax);
-      // Branch-free when nothing is visible yet (m_new = -inf): every lane must keep feeding
-      // the shared MFMAs, so exp2 is taken against 0 and yields p = 0, alpha = 0.
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
+        sacc[kk][j] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    // Lazy rescaling: the running max moves only when a row's tile max exceeds it by more than
+    // 8 (log2 units), so weights stay <= 2^8 and most tiles skip rescaling the accumulators.
+    const bool grow = tmax > m_run + 8.f;
+    if (__any(grow)) {
+      const float m_new = grow ? fmaxf(m_run, tmax) : m_run;
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
-      for (int t = 0; t < NDT; ++t)
+      for (int tt = 0; tt < NDT; ++tt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float e = exp2f(sacc[kk][j] - m_use);
-          sacc[kk][j] = e;
-          l_run += e;
-        }
+        for (int r = 0; r < 16; ++r) oacc[tt][r] *= alpha;
       m_run = m_new;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          float pv[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) pv[i] = sacc[kk][8 * hh + i];
-          const bf16x8_t b = pack_bf16x8(pv);
-#pragma unroll
-          for (int t = 0; t < NDT; ++t)
-            oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Vt[(t * 32 + lq) * VS], kk * 32 + 16 * hh, g),
-                                                               b, oacc[t], 0, 0, 0);
-        }
     }
+    // Branch-free when nothing is visible yet (m_run = -inf): every lane keeps feeding the
+    // shared MFMAs, with weights exp2(-inf) = 0.
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float e = fast_exp2(sacc[kk][j] - m_use);
+        sacc[kk][j] = e;
+        l_run += e;
+      }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        float pv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pv[i] = sacc[kk][8 * hh + i];
+        const bf16x8_t b = pack_bf16x8(pv);
+#pragma unroll
+        for (int tt = 0; tt < NDT; ++tt)
+          oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Vt[(tt * 32 + lq) * VS], kk * 32 + 16 * hh, g),
+                                                              b, oacc[tt], 0, 0, 0);
+      }
   }
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -272,7 +354,9 @@ __global__ __launch_bounds__(256) void attn_dq_bf16_kernel(const AttnArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
   const int nqt = (p.Mq + 127) / 128;
   const int lin = xcd_remap(blockIdx.x, nqt * p.Hq);
-  const int h = lin % p.Hq, qt = lin / p.Hq;
+  // q tiles are walked from the last to the first: with causal-like masks the late tiles carry
+  // the most key tiles, so the heaviest workgroups start first and the tail is light.
+  const int h = lin % p.Hq, qt = nqt - 1 - lin / p.Hq;
   const int kvh = h / (p.Hq / p.Hkv);
   const int qrow = qt * 128 + w * 32 + lq;
   const bool qvalid = qrow < p.Mq;
@@ -301,63 +385,87 @@ __global__ __launch_bounds__(256) void attn_dq_bf16_kernel(const AttnArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[t][r] = 0.f;
 
+  const Bounds wb1 = wave_bounds(qvalid, ivq.x, ivq.y);
+  const Bounds wb2 = wave_bounds(qvalid && p.K2 != nullptr, ivq.z, ivq.w);
+  int kb1, ke1, kb2, ke2;
+  wg_bounds(wb1, sh, kb1, ke1);
+  wg_bounds(wb2, sh, kb2, ke2);
+  const int n1 = kb1 < ke1 ? (ke1 - (kb1 / BK) * BK + BK - 1) / BK : 0;
+  const int n2 = (p.K2 != nullptr && kb2 < ke2) ? (ke2 - (kb2 / BK) * BK + BK - 1) / BK : 0;
+  const int nt = n1 + n2;
+  const bf16_t* K1 = (const bf16_t*)p.K1;
+  const bf16_t* V1 = (const bf16_t*)p.V1;
+  const bf16_t* K2 = (const bf16_t*)p.K2;
+  const bf16_t* V2 = (const bf16_t*)p.V2;
+  // Next-tile prefetch: the source is selected with scalar selects (no branch writing the
+  // staging registers).
+  uint4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
+  kr2 = kr3 = vr2 = vr3 = make_uint4(0, 0, 0, 0);
+#define UNOK_FETCH(t_)                                                                     \
+  do {                                                                                     \
+    const bool f2 = (t_) >= n1;                                                            \
+    const int fkt = f2 ? (kb2 / BK) * BK + ((t_) - n1) * BK : (kb1 / BK) * BK + (t_) * BK;   \
+    const int fke = f2 ? ke2 : ke1;                                                        \
+    const bf16_t* fk = f2 ? K2 : K1;                                                       \
+    const bf16_t* fv = f2 ? V2 : V1;                                                       \
+    const int64_t fldk = f2 ? p.ldk2 : p.ldk1, fldv = f2 ? p.ldv2 : p.ldv1;               \
+    UNOK_TILE_LOAD(kr, fk, fldk, kvh * D, fkt, fke);                                       \
+    UNOK_TILE_LOAD(vr, fv, fldv, kvh * D, fkt, fke);                                       \
+  } while (0)
+  if (nt > 0) UNOK_FETCH(0);
 #pragma unroll 1
-  for (int src = 0; src < 2; ++src) {
-    const bf16_t* Kp = (const bf16_t*)(src ? p.K2 : p.K1);
-    const bf16_t* Vp = (const bf16_t*)(src ? p.V2 : p.V1);
-    const int64_t ldk = src ? p.ldk2 : p.ldk1, ldv = src ? p.ldv2 : p.ldv1;
-    if (Kp == nullptr) continue;
-    const int lo = src ? ivq.z : ivq.x, hi = src ? ivq.w : ivq.y;
-    const Bounds wb = wave_bounds(qvalid, lo, hi);
-    int kb, ke;
-    wg_bounds(wb, sh, kb, ke);
-    if (kb >= ke) continue;
-#pragma unroll 1
-    for (int kt = (kb / BK) * BK; kt < ke; kt += BK) {
-      __syncthreads();
-      stage_tile<D, true, true, KS, TS>(Kp, ldk, kvh * D, kt, ke, Ks, Kt);
-      stage_tile<D, true, false, KS, TS>(Vp, ldv, kvh * D, kt, ke, Vs, nullptr);
-      __syncthreads();
-      if (kt >= wb.hi || kt + BK <= wb.lo) continue;
-      const bool full = kt >= wb.maxlo && kt + BK <= wb.minhi;
-      f32x16_t sacc[2], dpacc[2];
+  for (int t = 0; t < nt; ++t) {
+    __syncthreads();
+    UNOK_TILE_STORE(tile_st_row, kr, Ks, KS);
+    UNOK_TILE_STORE(tile_st_trans, kr, Kt, TS);
+    UNOK_TILE_STORE(tile_st_row, vr, Vs, KS);
+    __syncthreads();
+    if (t + 1 < nt) UNOK_FETCH(t + 1);
+    const bool s2 = t >= n1;
+    const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
+    const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
+    const int w_maxlo = s2 ? wb2.maxlo : wb1.maxlo, w_minhi = s2 ? wb2.minhi : wb1.minhi;
+    const int lo = s2 ? ivq.z : ivq.x, hi = s2 ? ivq.w : ivq.y;
+    if (kt >= w_hi || kt + BK <= w_lo) continue;
+    const bool full = kt >= w_maxlo && kt + BK <= w_minhi;
+    f32x16_t sacc[2], dpacc[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { sacc[kk][r] = 0.f; dpacc[kk][r] = 0.f; }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) { sacc[kk][r] = 0.f; dpacc[kk][r] = 0.f; }
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Ks[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
-                                                              qreg[ks], sacc[kk], 0, 0, 0);
-          dpacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Vs[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
-                                                               oreg[ks], dpacc[kk], 0, 0, 0);
-        }
+        sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Ks[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
+                                                            qreg[ks], sacc[kk], 0, 0, 0);
+        dpacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Vs[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
+                                                             oreg[ks], dpacc[kk], 0, 0, 0);
       }
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          float pr = exp2f(sacc[kk][j] * p.scale_log2 - lse);
-          if (!full) {
-            const int key = kt + kk * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-            if (key < lo || key >= hi) pr = 0.f;
-          }
-          sacc[kk][j] = pr * (dpacc[kk][j] - dsum);
+      for (int j = 0; j < 16; ++j) {
+        float pr = fast_exp2(sacc[kk][j] * p.scale_log2 - lse);
+        if (!full) {
+          const int key = kt + kk * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
+          if (key < lo || key >= hi) pr = 0.f;
         }
+        sacc[kk][j] = pr * (dpacc[kk][j] - dsum);
+      }
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          float dv[8];
+      for (int hh = 0; hh < 2; ++hh) {
+        float dv[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) dv[i] = sacc[kk][8 * hh + i];
-          const bf16x8_t b = pack_bf16x8(dv);
+        for (int i = 0; i < 8; ++i) dv[i] = sacc[kk][8 * hh + i];
+        const bf16x8_t b = pack_bf16x8(dv);
 #pragma unroll
-          for (int t = 0; t < NDT; ++t)
-            dq[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Kt[(t * 32 + lq) * TS], kk * 32 + 16 * hh, g), b,
-                                                             dq[t], 0, 0, 0);
-        }
-    }
+        for (int tt = 0; tt < NDT; ++tt)
+          dq[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Kt[(tt * 32 + lq) * TS], kk * 32 + 16 * hh, g), b,
+                                                            dq[tt], 0, 0, 0);
+      }
   }
   if (qvalid) {
     bf16_t* out = (bf16_t*)p.dQ + (int64_t)qrow * p.lddq + h * D;
@@ -460,7 +568,7 @@ __global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
           for (int j = 0; j < 16; ++j) {
             const int ql = qq * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
             float pr = 0.f;
-            if (kvalid && krow >= s_lo[ql] && krow < s_hi[ql]) pr = exp2f(sacc[qq][j] * p.scale_log2 - s_lse[ql]);
+            if (kvalid && krow >= s_lo[ql] && krow < s_hi[ql]) pr = fast_exp2(sacc[qq][j] * p.scale_log2 - s_lse[ql]);
             sacc[qq][j] = pr;
             dpacc[qq][j] = pr * (dpacc[qq][j] - s_dsum[ql]);
           }

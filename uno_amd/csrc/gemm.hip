@@ -17,6 +17,8 @@
 // token rows); gemm_tn computes them with split-K partials into a caller workspace.
 #include "common.h"
 
+#include <stdlib.h>
+
 struct GemmNT {
   const void* A; int64_t lda;
   const void* B; int64_t ldb;
@@ -157,6 +159,154 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_kernel(const GemmNT p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (row >= p.M) continue;
+      const bool on = (p.gate == nullptr) || (p.gate[row] != 0);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + lrow;
+        if (col >= p.N) continue;
+        float v = on ? acc[i][j][r] * p.alpha : 0.f;
+        if (R) v += ld_f(R + (int64_t)row * p.ldr + col);
+        Elem<OutT>::store(C + (int64_t)row * p.ldc + col, v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// bf16 MFMA NT kernel with direct global->LDS loads (gfx950 global_load_lds_dwordx4).
+// Each lane's 16-byte load lands at LDS base + 16*lane, so a wave instruction fills 8
+// consecutive 128-byte tile rows. Rows are stored unpadded and the 16-byte chunks of row r are
+// XOR-swizzled (slot = chunk ^ (r & 7)), which keeps the MFMA operand reads of each 16-lane
+// group on distinct banks. Two LDS stages: the loads of K tile kt+1 run in the background
+// while tile kt is multiplied; no VGPR staging and no LDS store instructions.
+// Requirements (checked on the host): K and K2 multiples of 64, 16-byte aligned operands.
+// Rows beyond M (N) are clamped to the last valid row; their results are never stored.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ void lds_dma16(const void* g, bf16_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
+
+template <int BM, int BN, int NW, typename OutT>
+__global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT p) {
+  constexpr int BK = 64;
+  constexpr int WAVES_N = 2, WAVES_M = NW / WAVES_N;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_INS = BM / (8 * NW), B_INS = BN / (8 * NW);   // load instructions per wave
+  static_assert(A_INS >= 1 && B_INS >= 1 && TM >= 1 && TN >= 1, "bad tile");
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  bf16_t* As = smem;                       // [2][BM*64]
+  bf16_t* Bs = smem + 2 * BM * BK;         // [2][BN*64]
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
+  const int lin = xcd_remap(blockIdx.x, nM * nN);
+  constexpr int GROUP = 8;
+  const int group = lin / (GROUP * nN);
+  const int first_m = group * GROUP;
+  const int gsz = min(nM - first_m, GROUP);
+  const int ing = lin % (GROUP * nN);
+  const int m0 = (first_m + ing % gsz) * BM;
+  const int n0 = (ing / gsz) * BN;
+
+  const bf16_t* A = (const bf16_t*)p.A;
+  const bf16_t* B = (const bf16_t*)p.B;
+  const bf16_t* A2 = nullptr;
+  if (p.A2 != nullptr && p.K2 > 0) A2 = (const bf16_t*)p.A2 + p.seg_col[find_seg(p, n0)];
+  const bf16_t* B2 = (const bf16_t*)p.B2;
+  const int nk1 = p.K / BK;
+  const int nk = nk1 + (A2 ? p.K2 / BK : 0);
+
+  // Per-lane source rows (clamped) and swizzled chunk, fixed for the whole K loop.
+  const int lrow8 = lane >> 3, slot = lane & 7;
+  int64_t a_off[A_INS], b_off[B_INS], a2_off[A_INS], b2_off[B_INS];
+#pragma unroll
+  for (int i = 0; i < A_INS; ++i) {
+    const int r = (i * NW + wid) * 8 + lrow8;
+    const int gm = min(m0 + r, p.M - 1);
+    const int chunk = slot ^ (r & 7);
+    a_off[i] = (int64_t)gm * p.lda + chunk * 8;
+    a2_off[i] = (int64_t)gm * p.lda2 + chunk * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < B_INS; ++i) {
+    const int r = (i * NW + wid) * 8 + lrow8;
+    const int gn = min(n0 + r, p.N - 1);
+    const int chunk = slot ^ (r & 7);
+    b_off[i] = (int64_t)gn * p.ldb + chunk * 8;
+    b2_off[i] = (int64_t)gn * p.ldb2 + chunk * 8;
+  }
+  auto issue = [&](int kt, int buf) {
+    bf16_t* as = As + buf * BM * BK;
+    bf16_t* bs = Bs + buf * BN * BK;
+    if (kt < nk1) {
+      const int kk = kt * BK;
+#pragma unroll
+      for (int i = 0; i < A_INS; ++i) lds_dma16(A + a_off[i] + kk, as + (i * NW + wid) * 8 * BK);
+#pragma unroll
+      for (int i = 0; i < B_INS; ++i) lds_dma16(B + b_off[i] + kk, bs + (i * NW + wid) * 8 * BK);
+    } else {
+      const int kk = (kt - nk1) * BK;
+#pragma unroll
+      for (int i = 0; i < A_INS; ++i) lds_dma16(A2 + a2_off[i] + kk, as + (i * NW + wid) * 8 * BK);
+#pragma unroll
+      for (int i = 0; i < B_INS; ++i) lds_dma16(B2 + b2_off[i] + kk, bs + (i * NW + wid) * 8 * BK);
+    }
+  };
+
+  const int wm = wid / WAVES_N, wn = wid % WAVES_N;
+  const int lrow = lane & 31, lg = lane >> 5;
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  auto compute = [&](int buf) {
+    const bf16_t* as = As + buf * BM * BK;
+    const bf16_t* bs = Bs + buf * BN * BK;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int chunk = ks * 2 + lg;
+      bf16x8_t a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WM + i * 32 + lrow;
+        a[i] = *(const bf16x8_t*)&as[r * BK + ((chunk ^ (r & 7)) << 3)];
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * WN + j * 32 + lrow;
+        b[j] = *(const bf16x8_t*)&bs[r * BK + ((chunk ^ (r & 7)) << 3)];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+    compute(kt & 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  OutT* C = (OutT*)p.C;
+  const OutT* R = (const OutT*)p.R;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
       if (row >= p.M) continue;
       const bool on = (p.gate == nullptr) || (p.gate[row] != 0);
 #pragma unroll
@@ -405,6 +555,38 @@ static void launch_nt_bf16(const GemmNT& p, int out_dtype, hipStream_t st) {
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// Waves per workgroup of the 256x256 direct-to-LDS kernel (UNOK_GEMM_WAVES = 4 or 8).
+static int dma_waves() {
+  static int w = [] {
+    const char* e = getenv("UNOK_GEMM_WAVES");
+    const int v = e ? atoi(e) : 8;
+    return (v == 4) ? 4 : 8;
+  }();
+  return w;
+}
+
+template <int BM, int BN, int NW, typename OutT>
+static void launch_nt_dma_t(const GemmNT& p, hipStream_t st) {
+  constexpr size_t lds = 2 * (BM + BN) * 64 * sizeof(bf16_t);
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_dma_kernel<BM, BN, NW, OutT>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    configured = true;
+  }
+  const int nb = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_nt_bf16_dma_kernel<BM, BN, NW, OutT>), dim3(nb), dim3(NW * 64), lds, st, p);
+}
+
+static void launch_nt_dma(const GemmNT& p, int out_dtype, hipStream_t st) {
+  const bool f32 = out_dtype == UNOK_F32;
+  if (dma_waves() == 4) {
+    if (f32) launch_nt_dma_t<256, 256, 4, float>(p, st); else launch_nt_dma_t<256, 256, 4, bf16_t>(p, st);
+  } else {
+    if (f32) launch_nt_dma_t<256, 256, 8, float>(p, st); else launch_nt_dma_t<256, 256, 8, bf16_t>(p, st);
+  }
+}
+
 // C = alpha * gate (.) (A B^T + A2[:, seg_col] B2^T) + R.
 // in_dtype: dtype of A, B, A2, B2; out_dtype: dtype of C and R.
 // seg_end/seg_col: `nseg` (<= 4) extension segments over N (ignored when A2 is null).
@@ -465,6 +647,8 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
   } else if (N <= 128 || !segs_ok(256) || big_tiles < 512) {
     if ((long long)((M + 127) / 128) * ((N + 127) / 128) < 256) launch_nt_bf16<64, 128>(p, out_dtype, st);
     else launch_nt_bf16<128, 128>(p, out_dtype, st);
+  } else if (K % 64 == 0 && (!p.A2 || p.K2 % 64 == 0)) {
+    launch_nt_dma(p, out_dtype, st);
   } else {
     launch_nt_bf16<256, 256>(p, out_dtype, st);
   }

@@ -28,9 +28,8 @@ template <typename T>
 __device__ __forceinline__ void store_vec(T* p, const float* in) {
   uint4 u;
   if constexpr (sizeof(T) == 2) {
-    bf16_t* h = (bf16_t*)&u;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16(in[e]);
+    u = make_uint4(pack2_bf16(in[0], in[1]), pack2_bf16(in[2], in[3]), pack2_bf16(in[4], in[5]),
+                   pack2_bf16(in[6], in[7]));
   } else {
     float* f = (float*)&u;
 #pragma unroll
