@@ -8,7 +8,7 @@ t ~ U(0.05, 1) per block, uniform token ids, objective CE with data targets and 
 
 Prints ONE JSON line. ``value`` = training tokens/s (B*L input tokens per step, the reference's
 accounting). ``roofline`` = the dominant kernel (256x256 bf16 MFMA GEMM of the fused LoRA
-linears): algorithmic FLOPs per launch / mean launch time, HIP events around every such launch
+linears and the LM head): algorithmic FLOPs per launch / mean launch time, HIP events around every such launch
 in the timed region. ``cpu_baseline`` = the CPU oracle of the same step timed on this host on a
 bounded sample (see cpu_baseline()).
 """
@@ -123,6 +123,22 @@ def cpu_baseline(threads: int) -> dict:
             "cpu_model": _cpu_model()}
 
 
+TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "hbm_traffic_gemm_nt_dma_256_qwen3_8b_step.md")
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the dominant GEMM kernel, from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the same counter over a 1 GiB copy)."""
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -142,6 +158,9 @@ def main() -> int:
                     help="decoder layers (the reported workload uses all 36)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run three plain 1 GiB device copies (the reference kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported in this build "
@@ -154,6 +173,13 @@ def main() -> int:
 
     cfg = dict(QWEN3_8B, num_hidden_layers=args.layers)
     dev = "cuda:0"
+    if args.calibrate_copy:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     model, lm, trainer, batch = build_step(cfg, WORKLOAD, dev)
     print(f"[bench] model built: {args.layers} layers; warmup {args.warmup} steps", file=sys.stderr, flush=True)
     for i in range(args.warmup):
@@ -198,9 +224,10 @@ def main() -> int:
                    "objective": "CE (data targets, 1/t weights)", "parallelism": "single GPU"},
         "mfu": round(mfu, 4), "algorithmic_tflop_per_step": round(flops["total"] / 1e12, 2),
         "flops_breakdown_tflop": {k: round(v / 1e12, 2) for k, v in flops.items() if k != "total"},
-        "roofline": {"kernel": "gemm_nt_bf16_kernel<256,256> (fused LoRA linears)", "bound": "mfma",
-                     "achieved": round(gemm_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+        "roofline": {"kernel": "gemm_nt_bf16_dma_kernel<256,256,8> (fused LoRA linears, LM head)",
+                     "bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic(),
                      "launches": len(ms), "mean_launch_ms": round(gemm_ms, 4)},
     }
     if not args.no_cpu_baseline:
