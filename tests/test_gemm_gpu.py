@@ -61,6 +61,40 @@ def test_gemm_tn(dev, Mr, P, Q, dtype):
     assert _rel(out, ref) < (1e-5 if dtype == torch.float32 else 1e-5)
 
 
+@pytest.mark.parametrize("Mr,P,Q", [(1000, 192, 4096), (16384, 4096, 64), (777, 1000, 96), (4100, 64, 12288),
+                                     (300, 1032, 256), (16384, 128, 4096)])
+def test_gemm_tn_skinny_bf16(dev, Mr, P, Q):
+    """LoRA weight-gradient shapes (rank side <= 256 columns): dA = g^T x and dB = dY^T h, with
+    ragged row counts and wide sides that are not a multiple of the 256-column strip."""
+    torch.manual_seed(Mr + Q)
+    a = torch.randn(Mr, P, device=dev).bfloat16()
+    b = torch.randn(Mr, Q, device=dev).bfloat16()
+    c0 = torch.randn(P, Q, device=dev)
+    out = K.gemm_tn(a, b, out=c0.clone(), alpha=0.5, beta=1.0)
+    ref = c0 + 0.5 * a.float().T @ b.float()
+    fresh = K.gemm_tn(a, b, alpha=1.0)
+    torch.cuda.synchronize()
+    assert _rel(out, ref) < 1e-5
+    assert _rel(fresh, a.float().T @ b.float()) < 1e-5
+
+
+def test_gemm_tn_skinny_column_slices(dev):
+    """Operands that are column slices of wider buffers (g_gu[:, r:2r], dgu[:, F:2F]) and an
+    output that is a row slice of the flat gradient buffer."""
+    torch.manual_seed(5)
+    Mr, F, r = 2048, 1536, 64
+    dgu = torch.randn(Mr, 2 * F, device=dev).bfloat16()
+    h = torch.randn(Mr, 2 * r, device=dev).bfloat16()
+    flat = torch.randn(3 * F * r, device=dev)
+    out = flat[F * r:2 * F * r].view(F, r)
+    before = flat.clone()
+    K.gemm_tn(dgu[:, F:], h[:, r:], out=out, alpha=2.0, beta=1.0)
+    torch.cuda.synchronize()
+    ref = before[F * r:2 * F * r].view(F, r) + 2.0 * dgu[:, F:].float().T @ h[:, r:].float()
+    assert _rel(out, ref) < 1e-5
+    assert torch.equal(flat[:F * r], before[:F * r]) and torch.equal(flat[2 * F * r:], before[2 * F * r:])
+
+
 def test_gemm_strided_views(dev):
     """Column-sliced operands (row stride > width), as used for fused projections."""
     torch.manual_seed(3)

@@ -528,6 +528,154 @@ __global__ __launch_bounds__(256) void gemm_tn_f32_kernel(const GemmTN p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Skinny TN product of the LoRA weight gradients:
+//   WS[z][s][x] = alpha * sum_{m in rows of split z} S[m, s] X[m, x]
+// S is the rank-side operand (NS <= 256 columns, a multiple of 32: g or h) and X the wide
+// activation or gradient (x, dY). The product is HBM-bound on X, so the kernel streams X once:
+// a workgroup owns a strip of 256 X columns and a contiguous range of rows. Every thread loads
+// one 8x8 block (8 rows x 16 bytes) of X or S, transposes it in registers and writes it to LDS
+// with the token index contiguous ([column][m], 72-element rows, 16-byte chunk c of row r at slot
+// c ^ ((r >> 4) & 7) so both the transposed writes and the MFMA operand reads spread over the
+// banks). Wave w then owns X columns [32w, 32w + 32) of the strip and all NS rows of the result
+// (32x32x16 bf16 MFMAs). The next 64-row tile is fetched into registers during the MFMAs.
+// ---------------------------------------------------------------------------------------
+struct GemmTNSkinny {
+  const bf16_t* S; int64_t lds;   // [Mrows, NS]
+  const bf16_t* X; int64_t ldx;   // [Mrows, NX]
+  float* WS;                       // [nsplit, NS, NX]
+  int Mrows, NS, NX, rows_per_split;
+  float alpha;
+};
+
+constexpr int TNS_QB = 256;   // X columns per workgroup
+constexpr int TNS_BK = 64;    // token rows per tile
+constexpr int TNS_LD = 72;    // LDS row pitch in elements
+
+// out[c] = column c of the 8x8 bf16 block whose rows are in[0..7].
+__device__ __forceinline__ void transpose8x8_bf16(const uint4 (&in)[8], uint4 (&out)[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint4 a = in[2 * k], b = in[2 * k + 1];
+      const uint32_t da = (c >> 1) == 0 ? a.x : (c >> 1) == 1 ? a.y : (c >> 1) == 2 ? a.z : a.w;
+      const uint32_t db = (c >> 1) == 0 ? b.x : (c >> 1) == 1 ? b.y : (c >> 1) == 2 ? b.z : b.w;
+      w[k] = (c & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
+    }
+    out[c] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+__device__ __forceinline__ int tns_slot(int row, int chunk) { return chunk ^ ((row >> 4) & 7); }
+
+// TOUT = false: WS[z][s][x] (the result is [rank, wide], e.g. dA = g^T x);
+// TOUT = true:  WS[z][x][s] (the result is [wide, rank], e.g. dB = dY^T h), computed as X^T S so
+// that both layouts are written and reduced with contiguous rows.
+template <int NS, bool TOUT>
+__global__ __launch_bounds__(512) void gemm_tn_skinny_kernel(const GemmTNSkinny p) {
+  constexpr int TM = NS / 32;
+  constexpr int XBLK = (TNS_BK / 8) * (TNS_QB / 8);   // 256 blocks of 8x8 in an X tile
+  constexpr int SCOLS = NS / 8;
+  constexpr int SBLK = (TNS_BK / 8) * SCOLS;
+  static_assert(NS % 32 == 0 && NS <= 256, "NS must be a multiple of 32, at most 256");
+  __shared__ __attribute__((aligned(16))) bf16_t Xs[TNS_QB * TNS_LD];
+  __shared__ __attribute__((aligned(16))) bf16_t Ss[NS * TNS_LD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int nstrip = (p.NX + TNS_QB - 1) / TNS_QB;
+  const int nz = gridDim.x / nstrip;
+  const int lin = xcd_remap(blockIdx.x, nstrip * nz);
+  const int x0 = (lin % nstrip) * TNS_QB;
+  const int z = lin / nstrip;
+  const int mbeg = z * p.rows_per_split;
+  const int mend = min(p.Mrows, mbeg + p.rows_per_split);
+
+  // This thread's 8x8 block: X block (tid < 256) or S block.
+  const bool isx = tid < XBLK;
+  const int sb = tid - XBLK;
+  const bool active = isx || sb < SBLK;
+  const int mg = isx ? tid / (TNS_QB / 8) : sb / SCOLS;          // row group (8 rows)
+  const int cl = isx ? (tid % (TNS_QB / 8)) * 8 : (sb % SCOLS) * 8;  // first column in the tile
+  const bool colok = active && (isx ? (x0 + cl < p.NX) : true);
+  const bf16_t* src = isx ? p.X + x0 + cl : p.S + cl;
+  const int64_t ld = isx ? p.ldx : p.lds;
+  bf16_t* dst = isx ? Xs : Ss;
+
+  uint4 st[8];
+  auto load = [&](int m0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int gm = m0 + mg * 8 + i;
+      st[i] = (colok && gm < mend) ? *(const uint4*)(src + (int64_t)gm * ld) : make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  f32x16_t acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+  const int lrow = lane & 31, lg = lane >> 5;
+  load(mbeg);
+  for (int m0 = mbeg; m0 < mend; m0 += TNS_BK) {
+    uint4 tr[8];
+    transpose8x8_bf16(st, tr);
+    __syncthreads();
+    if (active) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int r = cl + c;
+        *(uint4*)&dst[r * TNS_LD + tns_slot(r, mg) * 8] = tr[c];
+      }
+    }
+    __syncthreads();
+    if (m0 + TNS_BK < mend) load(m0 + TNS_BK);
+#pragma unroll
+    for (int ks = 0; ks < TNS_BK / 16; ++ks) {
+      const int chunk = ks * 2 + lg;
+      const int xr = wid * 32 + lrow;
+      const bf16x8_t b = *(const bf16x8_t*)&Xs[xr * TNS_LD + tns_slot(xr, chunk) * 8];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int sr = i * 32 + lrow;
+        const bf16x8_t a = *(const bf16x8_t*)&Ss[sr * TNS_LD + tns_slot(sr, chunk) * 8];
+        if (TOUT)
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, acc[i], 0, 0, 0);
+        else
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[i], 0, 0, 0);
+      }
+    }
+  }
+
+  if (TOUT) {
+    // acc[i][r] = result[x = x0 + 32 wid + 8 (r / 4) + 4 lg + r % 4][s = 32 i + lrow]
+    float* W = p.WS + (int64_t)z * p.NX * NS;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int x = x0 + wid * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
+      if (x < p.NX) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) W[(int64_t)x * NS + i * 32 + lrow] = acc[i][r] * p.alpha;
+      }
+    }
+  } else {
+    const int col = x0 + wid * 32 + lrow;
+    if (col < p.NX) {
+      float* W = p.WS + (int64_t)z * NS * p.NX + col;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = i * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
+          W[(int64_t)row * p.NX] = acc[i][r] * p.alpha;
+        }
+    }
+  }
+}
+
 // C[P,Q] (row stride ldc, fp32) = beta * C + sum_z WS[z]
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, float* C, int64_t ldc,
                                                              int P, int Q, int nsplit, float beta) {
@@ -656,13 +804,59 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
 }
 
 // Workspace bytes gemm_tn needs for a given problem (partials of the split-K reduction).
-UNOK_EXPORT int64_t unok_gemm_tn_workspace(int Mrows, int P, int Q) {
+// Split counts of the two TN kernels; the workspace is sized for the larger one.
+static int tn_general_splits(int Mrows, int P, int Q) {
   const int64_t tiles = (int64_t)((P + 63) / 64) * ((Q + 63) / 64);
   int64_t nsplit = (512 + tiles - 1) / tiles;
   const int64_t max_split = (Mrows + 255) / 256;
   if (nsplit > max_split) nsplit = max_split;
-  if (nsplit < 1) nsplit = 1;
-  return nsplit * (int64_t)P * Q * 4;
+  return nsplit < 1 ? 1 : (int)nsplit;
+}
+
+// Workgroups the skinny TN kernel aims for (UNOK_TN_WORKGROUPS overrides, for tuning).
+static int tn_skinny_target() {
+  static int t = [] {
+    const char* e = getenv("UNOK_TN_WORKGROUPS");
+    const int v = e ? atoi(e) : 256;
+    return v < 16 ? 16 : (v > 4096 ? 4096 : v);
+  }();
+  return t;
+}
+
+static int tn_skinny_splits(int Mrows, int NX) {
+  const int nstrip = (NX + TNS_QB - 1) / TNS_QB;
+  int nz = (tn_skinny_target() + nstrip - 1) / nstrip;
+  const int max_split = (Mrows + 255) / 256;
+  if (nz > max_split) nz = max_split;
+  return nz < 1 ? 1 : nz;
+}
+
+UNOK_EXPORT int64_t unok_gemm_tn_workspace(int Mrows, int P, int Q) {
+  const int a = tn_general_splits(Mrows, P, Q);
+  const int b = tn_skinny_splits(Mrows, P <= Q ? Q : P);
+  return (int64_t)(a > b ? a : b) * P * Q * 4;
+}
+
+template <int NS>
+static void launch_tn_skinny_t(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
+  const int nstrip = (p.NX + TNS_QB - 1) / TNS_QB;
+  if (tout)
+    hipLaunchKernelGGL((gemm_tn_skinny_kernel<NS, true>), dim3(nstrip * nz), dim3(512), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_tn_skinny_kernel<NS, false>), dim3(nstrip * nz), dim3(512), 0, st, p);
+}
+
+static void launch_tn_skinny(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
+  switch (p.NS) {
+    case 32: launch_tn_skinny_t<32>(p, nz, tout, st); break;
+    case 64: launch_tn_skinny_t<64>(p, nz, tout, st); break;
+    case 96: launch_tn_skinny_t<96>(p, nz, tout, st); break;
+    case 128: launch_tn_skinny_t<128>(p, nz, tout, st); break;
+    case 160: launch_tn_skinny_t<160>(p, nz, tout, st); break;
+    case 192: launch_tn_skinny_t<192>(p, nz, tout, st); break;
+    case 224: launch_tn_skinny_t<224>(p, nz, tout, st); break;
+    default: launch_tn_skinny_t<256>(p, nz, tout, st); break;
+  }
 }
 
 // C[P,Q] (fp32, row stride ldc) = beta * C + alpha * A[Mrows,P]^T B[Mrows,Q]
@@ -675,7 +869,31 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
   const int64_t need = unok_gemm_tn_workspace(Mrows, P, Q);
   UNOK_REQUIRE(workspace != nullptr && ws_bytes >= need, UNOK_EINVAL,
                "gemm_tn: workspace of %lld bytes needed, %lld given", (long long)need, (long long)ws_bytes);
-  const int nsplit = (int)(need / ((int64_t)P * Q * 4));
+  if (in_dtype == UNOK_BF16 && Mrows > 0) {
+    // Skinny path: the rank side (<= 256 columns, a multiple of 32) against a wide operand.
+    const bool a_small = P <= Q;
+    const int NS = a_small ? P : Q, NX = a_small ? Q : P;
+    const int64_t lds_ = a_small ? lda : ldb, ldx = a_small ? ldb : lda;
+    const void* S = a_small ? A : B;
+    const void* X = a_small ? B : A;
+    if (NS % 32 == 0 && NS <= 256 && NX >= TNS_QB && NX % 8 == 0 && lds_ % 8 == 0 && ldx % 8 == 0 &&
+        aligned16(S) && aligned16(X)) {
+      const int nz0 = tn_skinny_splits(Mrows, NX);
+      int rps = (Mrows + nz0 - 1) / nz0;
+      rps = ((rps + TNS_BK - 1) / TNS_BK) * TNS_BK;
+      const int nz = (Mrows + rps - 1) / rps;
+      GemmTNSkinny q{(const bf16_t*)S, lds_, (const bf16_t*)X, ldx, (float*)workspace, Mrows, NS, NX, rps, alpha};
+      launch_tn_skinny(q, nz, !a_small, st);
+      int rc = unok::check_launch("gemm_tn_skinny");
+      if (rc) return rc;
+      const int64_t total = (int64_t)NS * NX;
+      const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, (const float*)workspace, C, ldc,
+                         P, Q, nz, beta);
+      return unok::check_launch("gemm_tn_reduce");
+    }
+  }
+  const int nsplit = tn_general_splits(Mrows, P, Q);
   int rps = (Mrows + nsplit - 1) / nsplit;
   rps = ((rps + 63) / 64) * 64;
   if (rps == 0) rps = 64;
