@@ -48,6 +48,44 @@ def test_gemm_nt_lora_segments_gate_residual(dev, dtype):
     assert _rel(out, ref) < (1e-6 if dtype == torch.float32 else 8e-3)
 
 
+@pytest.mark.parametrize("M,N,Kd", [(8192, 8192, 512), (8200, 8448, 576), (16384, 4096, 320)])
+def test_gemm_nt_direct_to_lds_path(dev, M, N, Kd):
+    """Shapes large enough (>= 512 tiles of 256x256, K a multiple of 64) for the direct-to-LDS
+    kernel, including ragged M/N edges, with fp32 output."""
+    assert K.nt_uses_256_tiles(M, N, [N])
+    torch.manual_seed(M + N)
+    a = torch.randn(M, Kd, device=dev).bfloat16()
+    b = torch.randn(N, Kd, device=dev).bfloat16()
+    out = K.gemm_nt(a, b, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert _rel(out, a.float() @ b.float().T) < 1e-5
+
+
+def test_gemm_nt_direct_to_lds_lora_residual(dev):
+    """q|k|v-shaped fused product on the direct-to-LDS kernel: three 256-aligned segments with
+    their LoRA K-extension (K2 = 64), residual, alpha, bf16 output."""
+    torch.manual_seed(2)
+    M, Kd, r = 8192, 1024, 64
+    ends = [4096, 5120, 6144]
+    assert K.nt_uses_256_tiles(M, ends[-1], ends)
+    a = torch.randn(M, Kd, device=dev).bfloat16()
+    w = torch.randn(ends[-1], Kd, device=dev).bfloat16() * 0.05
+    h = torch.randn(M, 3 * r, device=dev).bfloat16()
+    bl = torch.randn(ends[-1], r, device=dev).bfloat16() * 0.05
+    res = torch.randn(M, ends[-1], device=dev).bfloat16()
+    out = K.gemm_nt(a, w, a2=h, b2=bl, segments=[(ends[0], 0), (ends[1], r), (ends[2], 2 * r)],
+                    residual=res, alpha=0.5)
+    ref = a.float() @ w.float().T
+    start = 0
+    for j, e in enumerate(ends):
+        ref[:, start:e] += h[:, j * r:(j + 1) * r].float() @ bl[start:e].float().T
+        start = e
+    ref = 0.5 * ref + res.float()
+    torch.cuda.synchronize()
+    # bf16 output: the only error beyond fp32 accumulation is the final rounding (2^-9 relative)
+    assert _rel(out, ref) < 4e-3
+
+
 @pytest.mark.parametrize("Mr,P,Q", [(4096, 64, 1024), (1000, 128, 64), (16384, 64, 4096), (64, 8, 16)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_gemm_tn(dev, Mr, P, Q, dtype):

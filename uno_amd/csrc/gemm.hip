@@ -18,6 +18,7 @@
 #include "common.h"
 
 #include <stdlib.h>
+#include <type_traits>
 
 struct GemmNT {
   const void* A; int64_t lda;
@@ -38,10 +39,14 @@ template <typename T> __device__ __forceinline__ float ld_f(const T* p);
 template <> __device__ __forceinline__ float ld_f<float>(const float* p) { return *p; }
 template <> __device__ __forceinline__ float ld_f<bf16_t>(const bf16_t* p) { return bf16_to_f32(*p); }
 
-__device__ __forceinline__ int find_seg(const GemmNT& p, int n0) {
-  int s = 0;
-  while (s + 1 < p.nseg && n0 >= p.seg_end[s]) ++s;
-  return s;
+// Column offset into A2 of the LoRA segment holding output column n0. Static indexing only, so
+// the kernel argument stays in SGPRs (a dynamic index would copy the struct to scratch).
+__device__ __forceinline__ int seg_col_of(const GemmNT& p, int n0) {
+  int col = p.seg_col[0];
+  if (p.nseg > 1 && n0 >= p.seg_end[0]) col = p.seg_col[1];
+  if (p.nseg > 2 && n0 >= p.seg_end[1]) col = p.seg_col[2];
+  if (p.nseg > 3 && n0 >= p.seg_end[2]) col = p.seg_col[3];
+  return col;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -77,7 +82,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_kernel(const GemmNT p) {
   const bf16_t* B = (const bf16_t*)p.B;
   const bf16_t* A2 = nullptr;
   const bf16_t* B2 = (const bf16_t*)p.B2;
-  if (p.A2 != nullptr && p.K2 > 0) A2 = (const bf16_t*)p.A2 + p.seg_col[find_seg(p, n0)];
+  if (p.A2 != nullptr && p.K2 > 0) A2 = (const bf16_t*)p.A2 + seg_col_of(p, n0);
   const int nk1 = (p.K + BK - 1) / BK;
   const int nk2 = A2 ? (p.K2 + BK - 1) / BK : 0;
   const int nk = nk1 + nk2;
@@ -175,29 +180,46 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_kernel(const GemmNT p) {
 
 // ---------------------------------------------------------------------------------------
 // bf16 MFMA NT kernel with direct global->LDS loads (gfx950 global_load_lds_dwordx4).
-// Each lane's 16-byte load lands at LDS base + 16*lane, so a wave instruction fills 8
-// consecutive 128-byte tile rows. Rows are stored unpadded and the 16-byte chunks of row r are
-// XOR-swizzled (slot = chunk ^ (r & 7)), which keeps the MFMA operand reads of each 16-lane
-// group on distinct banks. Two LDS stages: the loads of K tile kt+1 run in the background
-// while tile kt is multiplied; no VGPR staging and no LDS store instructions.
-// Requirements (checked on the host): K and K2 multiples of 64, 16-byte aligned operands.
+// Each lane's 16-byte load lands at LDS base + 16*lane, so one wave instruction fills
+// 64*16/(2*BK) consecutive tile rows of BK elements. Rows are stored unpadded; the 16-byte
+// chunk c of row r sits at slot c ^ swz(r), chosen so that the 16 lanes one LDS cycle serves
+// (rows r0..r0+15 of one chunk column) hit 16 distinct 4-bank groups.
+// STAGES LDS buffers form a ring: the loads of K tile kt+STAGES-1 are issued while tile kt is
+// multiplied, so STAGES-1 tiles are in flight to cover HBM latency; no VGPR staging and no LDS
+// store instructions. One barrier per K tile.
+// Requirements (checked on the host): K and K2 multiples of BK, 16-byte aligned operands.
 // Rows beyond M (N) are clamped to the last valid row; their results are never stored.
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ void lds_dma16(const void* g, bf16_t* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
 }
 
-template <int BM, int BN, int NW, typename OutT>
+template <int BK>
+__device__ __forceinline__ int dma_swz(int r) {
+  // BK = 64: a row is 32 banks, (r & 1) picks the bank half, the slot picks 4 of its 32 banks.
+  // BK = 32: a row is 16 banks, (r & 3) picks the quarter, the slot picks 4 of its 16 banks.
+  return BK == 64 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+}
+
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int NW, int BK, int STAGES, typename OutT>
 __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT p) {
-  constexpr int BK = 64;
+  constexpr int CPR = BK / 8;                     // 16-byte chunks per tile row
+  constexpr int RPI = 64 / CPR;                   // tile rows per wave load instruction
   constexpr int WAVES_N = 2, WAVES_M = NW / WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_INS = BM / (8 * NW), B_INS = BN / (8 * NW);   // load instructions per wave
+  constexpr int A_INS = BM / (RPI * NW), B_INS = BN / (RPI * NW);   // load instructions per wave
+  constexpr int LPT = A_INS + B_INS;              // loads per wave per K tile
   static_assert(A_INS >= 1 && B_INS >= 1 && TM >= 1 && TN >= 1, "bad tile");
+  static_assert(STAGES >= 2 && (STAGES - 2) * LPT < 64, "bad stage count");
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
-  bf16_t* As = smem;                       // [2][BM*64]
-  bf16_t* Bs = smem + 2 * BM * BK;         // [2][BN*64]
+  bf16_t* As = smem;                              // [STAGES][BM*BK]
+  bf16_t* Bs = smem + STAGES * BM * BK;           // [STAGES][BN*BK]
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
@@ -213,27 +235,27 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT 
   const bf16_t* A = (const bf16_t*)p.A;
   const bf16_t* B = (const bf16_t*)p.B;
   const bf16_t* A2 = nullptr;
-  if (p.A2 != nullptr && p.K2 > 0) A2 = (const bf16_t*)p.A2 + p.seg_col[find_seg(p, n0)];
+  if (p.A2 != nullptr && p.K2 > 0) A2 = (const bf16_t*)p.A2 + seg_col_of(p, n0);
   const bf16_t* B2 = (const bf16_t*)p.B2;
   const int nk1 = p.K / BK;
   const int nk = nk1 + (A2 ? p.K2 / BK : 0);
 
   // Per-lane source rows (clamped) and swizzled chunk, fixed for the whole K loop.
-  const int lrow8 = lane >> 3, slot = lane & 7;
+  const int lrowi = lane / CPR, slot = lane % CPR;
   int64_t a_off[A_INS], b_off[B_INS], a2_off[A_INS], b2_off[B_INS];
 #pragma unroll
   for (int i = 0; i < A_INS; ++i) {
-    const int r = (i * NW + wid) * 8 + lrow8;
+    const int r = (i * NW + wid) * RPI + lrowi;
     const int gm = min(m0 + r, p.M - 1);
-    const int chunk = slot ^ (r & 7);
+    const int chunk = slot ^ dma_swz<BK>(r);
     a_off[i] = (int64_t)gm * p.lda + chunk * 8;
     a2_off[i] = (int64_t)gm * p.lda2 + chunk * 8;
   }
 #pragma unroll
   for (int i = 0; i < B_INS; ++i) {
-    const int r = (i * NW + wid) * 8 + lrow8;
+    const int r = (i * NW + wid) * RPI + lrowi;
     const int gn = min(n0 + r, p.N - 1);
-    const int chunk = slot ^ (r & 7);
+    const int chunk = slot ^ dma_swz<BK>(r);
     b_off[i] = (int64_t)gn * p.ldb + chunk * 8;
     b2_off[i] = (int64_t)gn * p.ldb2 + chunk * 8;
   }
@@ -243,15 +265,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT 
     if (kt < nk1) {
       const int kk = kt * BK;
 #pragma unroll
-      for (int i = 0; i < A_INS; ++i) lds_dma16(A + a_off[i] + kk, as + (i * NW + wid) * 8 * BK);
+      for (int i = 0; i < A_INS; ++i) lds_dma16(A + a_off[i] + kk, as + (i * NW + wid) * RPI * BK);
 #pragma unroll
-      for (int i = 0; i < B_INS; ++i) lds_dma16(B + b_off[i] + kk, bs + (i * NW + wid) * 8 * BK);
+      for (int i = 0; i < B_INS; ++i) lds_dma16(B + b_off[i] + kk, bs + (i * NW + wid) * RPI * BK);
     } else {
       const int kk = (kt - nk1) * BK;
 #pragma unroll
-      for (int i = 0; i < A_INS; ++i) lds_dma16(A2 + a2_off[i] + kk, as + (i * NW + wid) * 8 * BK);
+      for (int i = 0; i < A_INS; ++i) lds_dma16(A2 + a2_off[i] + kk, as + (i * NW + wid) * RPI * BK);
 #pragma unroll
-      for (int i = 0; i < B_INS; ++i) lds_dma16(B2 + b2_off[i] + kk, bs + (i * NW + wid) * 8 * BK);
+      for (int i = 0; i < B_INS; ++i) lds_dma16(B2 + b2_off[i] + kk, bs + (i * NW + wid) * RPI * BK);
     }
   };
 
@@ -275,12 +297,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT 
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = wm * WM + i * 32 + lrow;
-        a[i] = *(const bf16x8_t*)&as[r * BK + ((chunk ^ (r & 7)) << 3)];
+        a[i] = *(const bf16x8_t*)&as[r * BK + ((chunk ^ dma_swz<BK>(r)) << 3)];
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int r = wn * WN + j * 32 + lrow;
-        b[j] = *(const bf16x8_t*)&bs[r * BK + ((chunk ^ (r & 7)) << 3)];
+        b[j] = *(const bf16x8_t*)&bs[r * BK + ((chunk ^ dma_swz<BK>(r)) << 3)];
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -290,14 +312,22 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT 
     }
   };
 
-  issue(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nk) issue(s, s);
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
-    compute(kt & 1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // Tile kt has landed once at most (tiles issued after it) * LPT loads are outstanding.
+    const int later = min(nk - 1 - kt, STAGES - 2);
+    if (later >= STAGES - 2) wait_vm<(STAGES - 2) * LPT>();
+    else if (STAGES > 3 && later == 2) wait_vm<(STAGES > 3 ? 2 * LPT : 0)>();
+    else if (STAGES > 2 && later == 1) wait_vm<(STAGES > 2 ? LPT : 0)>();
+    else wait_vm<0>();
+    // Plain s_barrier: a __syncthreads() fence would also wait for the tiles still in flight.
+    // Each wave has waited for its own loads of tile kt above, so after the barrier the whole
+    // tile is in LDS; the "memory" clobber keeps the compiler from moving LDS reads across it.
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+    compute(kt % STAGES);
   }
 
   OutT* C = (OutT*)p.C;
@@ -322,6 +352,232 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT 
 }
 
 // ---------------------------------------------------------------------------------------
+// 256x256 bf16 NT kernel with four waves, each owning a 128x128 block of C (16 accumulator
+// tiles of 32x32 in AGPRs). Per MFMA this halves the LDS operand traffic of the 8-wave layout
+// (8 fragment reads per 16 MFMAs instead of 6 per 8), which is what bounds the 8-wave kernel:
+// LDS reads + direct-to-LDS writes of a K tile equal its MFMA time there. Operand fragments are
+// double-buffered in VGPRs: the reads for step ks+1 are issued before the MFMAs of step ks, and
+// the first fragments of the next K tile are read right after the per-tile barrier, so the MFMA
+// pipe is never waiting on LDS latency. K tiles stream in through two direct-to-LDS stages.
+// ---------------------------------------------------------------------------------------
+// Buffer resource over `bytes` bytes from `base` (raw buffer: stride 0, dword 3 = data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, bf16_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// dst[0..3] = v[0..3] (+ res[0..3]) as one vector store (8 bytes for bf16, 16 for fp32).
+__device__ __forceinline__ void store4(bf16_t* dst, const bf16_t* res, const float (&v)[4]) {
+  float a0 = v[0], a1 = v[1], a2 = v[2], a3 = v[3];
+  if (res) {
+    const uint2 r = *(const uint2*)res;
+    a0 += __uint_as_float(r.x << 16); a1 += __uint_as_float(r.x & 0xffff0000u);
+    a2 += __uint_as_float(r.y << 16); a3 += __uint_as_float(r.y & 0xffff0000u);
+  }
+  *(uint2*)dst = make_uint2(pack2_bf16(a0, a1), pack2_bf16(a2, a3));
+}
+__device__ __forceinline__ void store4(float* dst, const float* res, const float (&v)[4]) {
+  float4 o = make_float4(v[0], v[1], v[2], v[3]);
+  if (res) {
+    const float4 r = *(const float4*)res;
+    o.x += r.x; o.y += r.y; o.z += r.z; o.w += r.w;
+  }
+  *(float4*)dst = o;
+}
+
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int SG_MFMA = 0x008, SG_DS_READ = 0x100;
+
+template <int BK, int STAGES, typename OutT>
+__global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
+  constexpr int BM = 256, BN = 256, NW = 4;
+  constexpr int TM = 4, TN = 4;
+  constexpr int KS = BK / 16;                   // MFMA K steps per tile
+  constexpr int CPR = BK / 8;                   // 16-byte chunks per tile row
+  constexpr int RPI = 64 / CPR;                 // tile rows per load instruction
+  constexpr int INS = BM / (RPI * NW);          // load instructions per wave per operand
+  constexpr int LPT = 2 * INS;                  // loads per wave per tile
+  static_assert(KS % 2 == 0 && STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * LPT < 64, "bad config");
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  bf16_t* As = smem;                            // [STAGES][BM*BK]
+  bf16_t* Bs = smem + STAGES * BM * BK;         // [STAGES][BN*BK]
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
+  const int lin = xcd_remap(blockIdx.x, nM * nN);
+  constexpr int GROUP = 8;
+  const int group = lin / (GROUP * nN);
+  const int first_m = group * GROUP;
+  const int gsz = min(nM - first_m, GROUP);
+  const int ing = lin % (GROUP * nN);
+  const int m0 = (first_m + ing % gsz) * BM;
+  const int n0 = (ing / gsz) * BN;
+
+  const bool ext = p.A2 != nullptr && p.K2 > 0;
+  const int nk1 = p.K / BK;
+  const int nk = nk1 + (ext ? p.K2 / BK : 0);
+
+  // Direct-to-LDS sources: lane -> (row lane/CPR of an RPI-row group, 16-byte slot lane%CPR);
+  // the byte offsets of the rows this lane loads (clamped to the last row) are fixed per
+  // operand pair. Byte ranges were checked on the host to fit 32 bits.
+  const int lrowi = lane / CPR, slot = lane % CPR;
+  __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(((int64_t)(p.M - 1) * p.lda + p.K) * 2));
+  __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)(((int64_t)(p.N - 1) * p.ldb + p.K) * 2));
+  uint32_t a_vo[INS], b_vo[INS];
+  auto set_offsets = [&](int64_t lda, int64_t ldb) {
+#pragma unroll
+    for (int i = 0; i < INS; ++i) {
+      const int r = (i * NW + wid) * RPI + lrowi;
+      const int chunk = slot ^ dma_swz<BK>(r);
+      a_vo[i] = (uint32_t)(((int64_t)min(m0 + r, p.M - 1) * lda + chunk * 8) * 2);
+      b_vo[i] = (uint32_t)(((int64_t)min(n0 + r, p.N - 1) * ldb + chunk * 8) * 2);
+    }
+  };
+  set_offsets(p.lda, p.ldb);
+  int kbase = 0;
+  // Tiles are issued in order; tile nk1 switches to the LoRA operand pair (A2, B2).
+  auto issue = [&](int kt, int buf) {
+    if (kt == nk1) {
+      ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0), (uint32_t)(((int64_t)(p.M - 1) * p.lda2 + p.K2) * 2));
+      rb = make_rsrc(p.B2, (uint32_t)(((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2));
+      set_offsets(p.lda2, p.ldb2);
+      kbase = nk1;
+    }
+    bf16_t* as = As + buf * BM * BK + wid * RPI * BK;
+    bf16_t* bs = Bs + buf * BN * BK + wid * RPI * BK;
+    const uint32_t kb = (uint32_t)(kt - kbase) * BK * 2;
+#pragma unroll
+    for (int i = 0; i < INS; ++i) buf_lds16(ra, a_vo[i], kb, as + i * NW * RPI * BK);
+#pragma unroll
+    for (int i = 0; i < INS; ++i) buf_lds16(rb, b_vo[i], kb, bs + i * NW * RPI * BK);
+  };
+  // Wait until this wave's LDS reads have returned (unconditionally, so the compiler's wait
+  // tracking knows it) and its loads of tile t have landed, `later` tiles having been issued
+  // after tile t.
+  auto wait_tile = [&](int later) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
+    if (STAGES > 4 && later >= 3) wait_vm<(STAGES > 4 ? 3 * LPT : 0)>();
+    else if (STAGES > 3 && later >= 2) wait_vm<(STAGES > 3 ? 2 * LPT : 0)>();
+    else if (STAGES > 2 && later >= 1) wait_vm<(STAGES > 2 ? LPT : 0)>();
+    else wait_vm<0>();
+  };
+
+  // Fragment reads: rows wm*128 + 32i + lrow (A) / wn*128 + 32j + lrow (B); every such row has
+  // the same swizzle dma_swz(lrow), so only the chunk term varies with ks.
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lrow = lane & 31, lg = lane >> 5;
+  const int sw = dma_swz<BK>(lrow);
+  const int a_row0 = (wm * 128 + lrow) * BK, b_row0 = (wn * 128 + lrow) * BK;
+  bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  auto load_frags = [&](bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN], int buf, int ks) {
+    const bf16_t* as = As + buf * BM * BK + a_row0;
+    const bf16_t* bs = Bs + buf * BN * BK + b_row0;
+    const int co = ((ks * 2 + lg) ^ sw) << 3;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[i] = *(const bf16x8_t*)&as[i * 32 * BK + co];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[j] = *(const bf16x8_t*)&bs[j * 32 * BK + co];
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // The product is formed transposed (B fragment as the MFMA's first operand), so that each lane
+  // ends up holding 4 consecutive output columns of one row: acc[i][j][4k + q] =
+  // C[wm*128 + 32i + lrow][wn*128 + 32j + 8k + 4lg + q], stored as one 8/16-byte vector.
+  auto mfmas = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+  };
+  // 8 fragment reads spread over the first 8 of 16 MFMAs, then the remaining 8 MFMAs.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
+  };
+
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < nk) issue(t, t);
+  wait_tile(min(nk - 1, STAGES - 2));
+  asm volatile("s_barrier" ::: "memory");
+  load_frags(fa0, fb0, 0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt % STAGES;
+    const int ahead = kt + STAGES - 1;
+    const bool more = kt + 1 < nk;
+    // The stage of tile `ahead` held tile kt-1, whose reads ended before the last barrier.
+    if (ahead < nk) issue(ahead, ahead % STAGES);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      if (ks % 2 == 0) { load_frags(fa1, fb1, cur, ks + 1); mfmas(fa0, fb0); }
+      else { load_frags(fa0, fb0, cur, ks + 1); mfmas(fa1, fb1); }
+      interleave();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Every read of stage `cur` by this wave has been issued and has returned; once each wave is
+    // here with its loads of tile kt+1 landed, tile kt+1 is complete in LDS.
+    wait_tile(min(nk - 1, ahead) - (kt + 1));
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) load_frags(fa0, fb0, (kt + 1) % STAGES, 0);
+    mfmas(fa1, fb1);
+    if (more) interleave();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Epilogue: 4 consecutive columns per lane and row -> one 8-byte (bf16) / 16-byte (fp32)
+  // store, residual read the same way. Columns come in groups of 4 (N % 4 == 0 on the host).
+  // Interior tiles without a gate take a branch-free path.
+  OutT* C = (OutT*)p.C;
+  const OutT* R = (const OutT*)p.R;
+  auto epilogue = [&](auto has_res, auto checked) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm * 128 + i * 32 + lrow;
+      if (checked && row >= p.M) continue;
+      const float sc = (!checked || p.gate == nullptr || p.gate[row] != 0) ? p.alpha : 0.f;
+      OutT* crow = C + (int64_t)row * p.ldc;
+      const OutT* rrow = has_res ? R + (int64_t)row * p.ldr : nullptr;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int col = n0 + wn * 128 + j * 32 + k * 8 + lg * 4;
+          if (checked && col >= p.N) continue;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * k + q] * sc;
+          store4(crow + col, has_res ? rrow + col : nullptr, v);
+        }
+      }
+    }
+  };
+  const bool interior = m0 + BM <= p.M && n0 + BN <= p.N && p.gate == nullptr;
+  if (R) {
+    if (interior) epilogue(std::true_type{}, std::false_type{}); else epilogue(std::true_type{}, std::true_type{});
+  } else {
+    if (interior) epilogue(std::false_type{}, std::false_type{}); else epilogue(std::false_type{}, std::true_type{});
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // fp32 NT kernel (fp32 parity mode): 64x64 tiles, 16-deep K slices, 4x4 outputs per thread.
 // ---------------------------------------------------------------------------------------
 template <typename OutT>
@@ -332,7 +588,7 @@ __global__ __launch_bounds__(256) void gemm_nt_f32_kernel(const GemmNT p) {
   const float* A = (const float*)p.A;
   const float* B = (const float*)p.B;
   const float* A2 = nullptr;
-  if (p.A2 != nullptr && p.K2 > 0) A2 = (const float*)p.A2 + p.seg_col[find_seg(p, n0)];
+  if (p.A2 != nullptr && p.K2 > 0) A2 = (const float*)p.A2 + seg_col_of(p, n0);
   const float* B2 = (const float*)p.B2;
   float acc[4][4] = {};
   for (int part = 0; part < 2; ++part) {
@@ -703,36 +959,77 @@ static void launch_nt_bf16(const GemmNT& p, int out_dtype, hipStream_t st) {
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
-// Waves per workgroup of the 256x256 direct-to-LDS kernel (UNOK_GEMM_WAVES = 4 or 8).
-static int dma_waves() {
-  static int w = [] {
-    const char* e = getenv("UNOK_GEMM_WAVES");
-    const int v = e ? atoi(e) : 8;
-    return (v == 4) ? 4 : 8;
+// Configuration of the 256x256 direct-to-LDS kernel (UNOK_GEMM_CFG selects one, for tuning):
+//   0: 8 waves, BK 64, 2 stages   1: 8 waves, BK 32, 4 stages   2: 8 waves, BK 32, 5 stages
+//   3: 4 waves, BK 32, 4 stages   4: 4 waves, BK 64, 2 stages
+//   5/6/7: 4 waves of 128x128, VGPR double-buffered fragments; BK 64 x 2 stages / BK 32 x 4 / BK 32 x 5
+static int dma_cfg() {
+  static int c = [] {
+    const char* e = getenv("UNOK_GEMM_CFG");
+    const int v = e ? atoi(e) : 5;
+    return (v >= 0 && v <= 7) ? v : 5;
   }();
-  return w;
+  return c;
 }
 
-template <int BM, int BN, int NW, typename OutT>
-static void launch_nt_dma_t(const GemmNT& p, hipStream_t st) {
-  constexpr size_t lds = 2 * (BM + BN) * 64 * sizeof(bf16_t);
+// The 4-wave kernel addresses operands through buffer resources with 32-bit byte offsets and
+// stores 4 output columns per vector (C and R rows aligned to 16 bytes, N a multiple of 4).
+static bool buffer_ranges_ok(const GemmNT& p) {
+  const int64_t lim = 0xFFFFFFFFll;
+  if (p.N % 4 || p.ldc % 4 || ((uintptr_t)p.C & 15) || (p.R && (p.ldr % 4 || ((uintptr_t)p.R & 15)))) return false;
+  if (((int64_t)(p.M - 1) * p.lda + p.K) * 2 > lim || ((int64_t)(p.N - 1) * p.ldb + p.K) * 2 > lim) return false;
+  if (p.A2 && (((int64_t)(p.M - 1) * p.lda2 + p.K2 + 4096) * 2 > lim || ((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2 > lim))
+    return false;
+  return true;
+}
+
+template <int BK, int STAGES, typename OutT>
+static void launch_nt_w4(const GemmNT& p, hipStream_t st) {
+  constexpr size_t lds = (size_t)STAGES * (256 + 256) * BK * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_dma_kernel<BM, BN, NW, OutT>,
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4_kernel<BK, STAGES, OutT>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    configured = true;
+  }
+  const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
+  hipLaunchKernelGGL((gemm_nt_bf16_w4_kernel<BK, STAGES, OutT>), dim3(nb), dim3(256), lds, st, p);
+}
+
+template <int BM, int BN, int NW, int BK, int STAGES, typename OutT>
+static void launch_nt_dma_t(const GemmNT& p, hipStream_t st) {
+  constexpr size_t lds = (size_t)STAGES * (BM + BN) * BK * sizeof(bf16_t);
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT>,
                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
   const int nb = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_nt_bf16_dma_kernel<BM, BN, NW, OutT>), dim3(nb), dim3(NW * 64), lds, st, p);
+  hipLaunchKernelGGL((gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT>), dim3(nb), dim3(NW * 64), lds, st, p);
+}
+
+template <typename OutT>
+static void launch_nt_dma_o(const GemmNT& p, hipStream_t st) {
+  switch (dma_cfg()) {
+    case 1: launch_nt_dma_t<256, 256, 8, 32, 4, OutT>(p, st); break;
+    case 2: launch_nt_dma_t<256, 256, 8, 32, 5, OutT>(p, st); break;
+    case 3: launch_nt_dma_t<256, 256, 4, 32, 4, OutT>(p, st); break;
+    case 4: launch_nt_dma_t<256, 256, 4, 64, 2, OutT>(p, st); break;
+    case 5:
+    case 6:
+    case 7:
+      if (!buffer_ranges_ok(p)) { launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break; }
+      if (dma_cfg() == 5) launch_nt_w4<64, 2, OutT>(p, st);
+      else if (dma_cfg() == 6) launch_nt_w4<32, 4, OutT>(p, st);
+      else launch_nt_w4<32, 5, OutT>(p, st);
+      break;
+    default: launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break;
+  }
 }
 
 static void launch_nt_dma(const GemmNT& p, int out_dtype, hipStream_t st) {
-  const bool f32 = out_dtype == UNOK_F32;
-  if (dma_waves() == 4) {
-    if (f32) launch_nt_dma_t<256, 256, 4, float>(p, st); else launch_nt_dma_t<256, 256, 4, bf16_t>(p, st);
-  } else {
-    if (f32) launch_nt_dma_t<256, 256, 8, float>(p, st); else launch_nt_dma_t<256, 256, 8, bf16_t>(p, st);
-  }
+  if (out_dtype == UNOK_F32) launch_nt_dma_o<float>(p, st); else launch_nt_dma_o<bf16_t>(p, st);
 }
 
 // C = alpha * gate (.) (A B^T + A2[:, seg_col] B2^T) + R.
