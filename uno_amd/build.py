@@ -37,9 +37,16 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; the uno_amd kernel library cannot be built")
 
 
+# Per-file additions. attention.hip: MFMA accumulators in VGPRs, so the softmax and the
+# accumulator rescale run on them directly instead of shuttling through AGPRs.
+FILE_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr[-6000:]}")

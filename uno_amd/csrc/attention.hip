@@ -156,172 +156,346 @@ __device__ __forceinline__ Bounds wave_bounds(bool valid, int lo, int hi) {
   return b;
 }
 
-__device__ __forceinline__ void wg_bounds(const Bounds& w, int* sh, int& lo, int& hi) {
+// Workgroup-wide (lo, hi) of the 4 waves' bounds, returned by value (x = lo, y = hi).
+__device__ __forceinline__ int2 wg_bounds(const Bounds& w, int* sh) {
   const int wid = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { sh[wid * 2] = w.lo; sh[wid * 2 + 1] = w.hi; }
   __syncthreads();
-  lo = min(min(sh[0], sh[2]), min(sh[4], sh[6]));
-  hi = max(max(sh[1], sh[3]), max(sh[5], sh[7]));
+  const int lo = min(min(sh[0], sh[2]), min(sh[4], sh[6]));
+  const int hi = max(max(sh[1], sh[3]), max(sh[5], sh[7]));
   __syncthreads();
+  return make_int2(__builtin_amdgcn_readfirstlane(lo), __builtin_amdgcn_readfirstlane(hi));
 }
 
 // ---------------------------------------------------------------------------------------
-// Forward, bf16: one workgroup = 128 queries (4 waves x 32) of one q-head.
+// K/V tile staging for the 64-query-per-wave kernels. A 64-key tile is loaded into registers
+// one tile ahead; threads [0, 128) own V (or K for the dQ transposed copy) as 8-key x 8-dim
+// blocks, which they transpose in registers and store as 16-byte rows of a [D][keys] LDS tile;
+// threads [128, 256) own row-major 16-byte chunks. The transposed tile has 72-element rows and
+// its 16-byte key group kg of dim row d sits at slot kg ^ ((d >> 4) & 7), which keeps both the
+// transposed stores and the P.V operand reads on distinct banks.
+// ---------------------------------------------------------------------------------------
+constexpr int ATT_BK = 64;     // keys per tile
+constexpr int ATT_TS = 72;     // transposed tile row pitch (elements)
+
+__device__ __forceinline__ int tslot(int d, int kg) { return kg ^ ((d >> 4) & 7); }
+
+template <int D>
+struct TileStage {
+  static constexpr int CPR = D / 8;            // 16-byte chunks per key row
+  static constexpr int TBLK = 8 * CPR;         // 8x8 blocks of the transposed operand (<= 128)
+  static constexpr int RPT = 64 * CPR / 128;   // row-major chunks per thread of [128, 256)
+  uint4 st[8];
+  // Transposed role (tid < TBLK): block (key group tid / CPR, dim group tid % CPR).
+  __device__ __forceinline__ void load_t(const bf16_t* src, int64_t ld, int col0, int k0, int kend, int tid) {
+    const int kg = tid / CPR, dg = tid % CPR;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = min(k0 + kg * 8 + i, kend - 1);
+      st[i] = *(const uint4*)(src + (int64_t)row * ld + col0 + dg * 8);
+    }
+  }
+  __device__ __forceinline__ void store_t(bf16_t* dst, int tid) const {
+    const int kg = tid / CPR, dg = tid % CPR;
+    // column e of the block = element e of every row; each column is stored as soon as it is
+    // formed, so only the 8 staged rows are live.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint4 a = st[2 * k], b = st[2 * k + 1];
+        const uint32_t da = (e >> 1) == 0 ? a.x : (e >> 1) == 1 ? a.y : (e >> 1) == 2 ? a.z : a.w;
+        const uint32_t db = (e >> 1) == 0 ? b.x : (e >> 1) == 1 ? b.y : (e >> 1) == 2 ? b.z : b.w;
+        w[k] = (e & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
+      }
+      const int d = dg * 8 + e;
+      *(uint4*)&dst[d * ATT_TS + tslot(d, kg) * 8] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  // Row-major role (128 <= tid < 256).
+  __device__ __forceinline__ void load_r(const bf16_t* src, int64_t ld, int col0, int k0, int kend, int tid) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int c = (tid - 128) + 128 * i, r = c / CPR, dc = (c % CPR) * 8;
+      const int row = min(k0 + r, kend - 1);
+      st[i] = *(const uint4*)(src + (int64_t)row * ld + col0 + dc);
+    }
+  }
+  __device__ __forceinline__ void store_r(bf16_t* dst, int rs, int tid) const {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int c = (tid - 128) + 128 * i, r = c / CPR, dc = (c % CPR) * 8;
+      *(uint4*)&dst[r * rs + dc] = st[i];
+    }
+  }
+};
+
+// A operand of a 16-key MFMA step from a transposed tile (dim row d), in the accumulator's key
+// order: lane group g supplies keys 8*kg0 + 4g + {0..3} and 8*(kg0 + 1) + 4g + {0..3}.
+__device__ __forceinline__ bf16x8_t ld_perm_t(const bf16_t* t, int d, int kg0, int g) {
+  const bf16_t* row = t + d * ATT_TS + 4 * g;
+  const uint2 lo = *(const uint2*)(row + tslot(d, kg0) * 8);
+  const uint2 hi = *(const uint2*)(row + tslot(d, kg0 + 1) * 8);
+  return __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
+// Row-major [64 keys x D] tiles filled by direct global->LDS loads (16 bytes per lane). The
+// 16-byte chunk c of row r sits at slot c ^ kswz(r), which spreads the 16 rows one LDS cycle
+// serves over all banks for both the MFMA fragment reads and the transposition reads.
+template <int D> __device__ __forceinline__ int kswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+
+// One 64-row tile of a row-major [rows, ld] bf16 matrix (columns [col0, col0 + D)) via buffer
+// loads straight into LDS. The buffer resource starts at row k0 and covers rows [k0, kend), so
+// rows past kend read as zeros without any clamping arithmetic (their keys are masked).
+template <int D>
+__device__ __forceinline__ void dma_tile(const bf16_t* src, int64_t ld, int col0, int k0, int kend, bf16_t* dst,
+                                         int wid, int lane) {
+  constexpr int CPR = D / 8, RPI = 64 / CPR, INS = 64 / (RPI * 4);
+  const int rl = lane / CPR, slot = lane % CPR;
+  const int nrows = max(0, min(kend - k0, 64));
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t*>(src + (int64_t)k0 * ld), (short)0, (int)((int64_t)nrows * ld * 2), 0x00020000);
+  const uint32_t ldb = (uint32_t)ld * 2;
+#pragma unroll
+  for (int i = 0; i < INS; ++i) {
+    const int r = (i * 4 + wid) * RPI + rl;
+    const uint32_t voff = (uint32_t)r * ldb + (uint32_t)(col0 + ((slot ^ kswz<D>(r)) << 3)) * 2;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + (i * 4 + wid) * RPI * D),
+                                             16, voff, 0, 0, 0);
+  }
+}
+
+// MFMA fragment (row r, 16-byte chunk c) of a swizzled row-major tile.
+template <int D>
+__device__ __forceinline__ bf16x8_t ld_frag(const bf16_t* tile, int r, int c) {
+  return *(const bf16x8_t*)&tile[r * D + ((c ^ kswz<D>(r)) << 3)];
+}
+
+// LDS -> LDS transposition of a swizzled row-major V tile into the [D][keys] layout read by
+// ld_perm_t: thread tid < 8*D/8 handles the 8-key x 8-dim block (tid / CPR, tid % CPR).
+template <int D>
+__device__ __forceinline__ void transpose_tile(const bf16_t* vr, bf16_t* vt, int tid) {
+  constexpr int CPR = D / 8;
+  if (tid >= 8 * CPR) return;
+  const int kg = tid / CPR, dg = tid % CPR;
+  uint4 st[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = kg * 8 + i;
+    st[i] = *(const uint4*)&vr[r * D + ((dg ^ kswz<D>(r)) << 3)];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint4 a = st[2 * k], b = st[2 * k + 1];
+      const uint32_t da = (e >> 1) == 0 ? a.x : (e >> 1) == 1 ? a.y : (e >> 1) == 2 ? a.z : a.w;
+      const uint32_t db = (e >> 1) == 0 ? b.x : (e >> 1) == 1 ? b.y : (e >> 1) == 2 ? b.z : b.w;
+      w[k] = (e & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
+    }
+    const int d = dg * 8 + e;
+    *(uint4*)&vt[d * ATT_TS + tslot(d, kg) * 8] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+__device__ __forceinline__ Bounds merge_bounds(const Bounds& a, const Bounds& b) {
+  Bounds r;
+  r.lo = min(a.lo, b.lo); r.hi = max(a.hi, b.hi);
+  r.maxlo = max(a.maxlo, b.maxlo); r.minhi = min(a.minhi, b.minhi);
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------
+// Forward, bf16: one workgroup = 256 queries of one q-head; each wave owns 64 queries as two
+// groups of 32 (one per MFMA column block), so every K/V fragment read from LDS feeds two MFMAs.
 // ---------------------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void attn_fwd_bf16_kernel(const AttnArgs p) {
-  constexpr int BK = 64, KS = D + 8, VS = BK + 4, NKS = D / 16, NDT = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[BK * KS];
-  __shared__ __attribute__((aligned(16))) bf16_t Vt[D * VS];
+  constexpr int BK = ATT_BK, NKS = D / 16, NDT = D / 32, QG = 2, BQ = 256;
+  // Dynamic LDS: K tiles [2][64*D] (direct-to-LDS double buffer), V rows [64*D], V^T [D][72].
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  bf16_t* Ks = smem;
+  bf16_t* Vr = smem + 2 * BK * D;
+  bf16_t* Vt = Vr + BK * D;
   __shared__ int sh[8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
-  const int nqt = (p.Mq + 127) / 128;
+  const int nqt = (p.Mq + BQ - 1) / BQ;
   const int lin = xcd_remap(blockIdx.x, nqt * p.Hq);
   // q tiles are walked from the last to the first: with causal-like masks the late tiles carry
   // the most key tiles, so the heaviest workgroups start first and the tail is light.
   const int h = lin % p.Hq, qt = nqt - 1 - lin / p.Hq;
   const int kvh = h / (p.Hq / p.Hkv);
-  const int qrow = qt * 128 + w * 32 + lq;
-  const bool qvalid = qrow < p.Mq;
-  int4 ivq = make_int4(0, 0, 0, 0);
-  if (qvalid) ivq = *(const int4*)(p.iv + (int64_t)qrow * 8);
-
+  int qrow[QG];
+  bool qvalid[QG];
+  int4 ivq[QG];
   const bf16_t* Q = (const bf16_t*)p.Q;
-  bf16x8_t qreg[NKS];
+  bf16x8_t qreg[QG][NKS];
 #pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) {
-    if (qvalid) qreg[ks] = ld_bf16x8(Q + (int64_t)qrow * p.ldq + h * D + ks * 16 + g * 8);
-    else qreg[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+  for (int qg = 0; qg < QG; ++qg) {
+    qrow[qg] = qt * BQ + w * 64 + qg * 32 + lq;
+    qvalid[qg] = qrow[qg] < p.Mq;
+    ivq[qg] = qvalid[qg] ? *(const int4*)(p.iv + (int64_t)qrow[qg] * 8) : make_int4(0, 0, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      qreg[qg][ks] = qvalid[qg] ? ld_bf16x8(Q + (int64_t)qrow[qg] * p.ldq + h * D + ks * 16 + g * 8)
+                                : __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
   }
 
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x16_t oacc[NDT];
+  float m_run[QG], l_run[QG];
+  f32x16_t oacc[QG][NDT];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t)
+  for (int qg = 0; qg < QG; ++qg) {
+    m_run[qg] = -INFINITY;
+    l_run[qg] = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[qg][t][r] = 0.f;
+  }
 
   // Tile walk over both sources: tiles [0, n1) come from source 1, [n1, n1 + n2) from source 2.
-  const Bounds wb1 = wave_bounds(qvalid, ivq.x, ivq.y);
-  const Bounds wb2 = wave_bounds(qvalid && p.K2 != nullptr, ivq.z, ivq.w);
-  int kb1, ke1, kb2, ke2;
-  wg_bounds(wb1, sh, kb1, ke1);
-  wg_bounds(wb2, sh, kb2, ke2);
+  const Bounds wb1 = merge_bounds(wave_bounds(qvalid[0], ivq[0].x, ivq[0].y), wave_bounds(qvalid[1], ivq[1].x, ivq[1].y));
+  const bool has2 = p.K2 != nullptr;
+  const Bounds wb2 = merge_bounds(wave_bounds(has2 && qvalid[0], ivq[0].z, ivq[0].w),
+                                  wave_bounds(has2 && qvalid[1], ivq[1].z, ivq[1].w));
+  const int2 r1 = wg_bounds(wb1, sh), r2 = wg_bounds(wb2, sh);
+  const int kb1 = r1.x, ke1 = r1.y, kb2 = r2.x, ke2 = r2.y;
   const int n1 = kb1 < ke1 ? (ke1 - (kb1 / BK) * BK + BK - 1) / BK : 0;
-  const int n2 = (p.K2 != nullptr && kb2 < ke2) ? (ke2 - (kb2 / BK) * BK + BK - 1) / BK : 0;
+  const int n2 = (has2 && kb2 < ke2) ? (ke2 - (kb2 / BK) * BK + BK - 1) / BK : 0;
   const int nt = n1 + n2;
   const bf16_t* K1 = (const bf16_t*)p.K1;
   const bf16_t* V1 = (const bf16_t*)p.V1;
   const bf16_t* K2 = (const bf16_t*)p.K2;
   const bf16_t* V2 = (const bf16_t*)p.V2;
-  // Next-tile prefetch: the source is selected with scalar selects (no branch writing the
-  // staging registers).
-  uint4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
-  kr2 = kr3 = vr2 = vr3 = make_uint4(0, 0, 0, 0);
-#define UNOK_FETCH(t_)                                                                     \
-  do {                                                                                     \
-    const bool f2 = (t_) >= n1;                                                            \
-    const int fkt = f2 ? (kb2 / BK) * BK + ((t_) - n1) * BK : (kb1 / BK) * BK + (t_) * BK;   \
-    const int fke = f2 ? ke2 : ke1;                                                        \
-    const bf16_t* fk = f2 ? K2 : K1;                                                       \
-    const bf16_t* fv = f2 ? V2 : V1;                                                       \
-    const int64_t fldk = f2 ? p.ldk2 : p.ldk1, fldv = f2 ? p.ldv2 : p.ldv1;               \
-    UNOK_TILE_LOAD(kr, fk, fldk, kvh * D, fkt, fke);                                       \
-    UNOK_TILE_LOAD(vr, fv, fldv, kvh * D, fkt, fke);                                       \
-  } while (0)
-  if (nt > 0) UNOK_FETCH(0);
+  const int wid = __builtin_amdgcn_readfirstlane(w);
+  // Tile t streams into K stage t&1 and the V row buffer; every thread issues its loads of tile
+  // t+1 right after V(t) has been transposed, so they fly during tile t's math.
+  // The source is chosen arithmetically (f2 in {0, 1}), not with selects between variables:
+  // the compiler would otherwise turn those into selected addresses of stack/kernarg memory.
+  const uintptr_t k1a = (uintptr_t)K1, v1a = (uintptr_t)V1;
+  const uintptr_t kd = (uintptr_t)K2 - k1a, vd = (uintptr_t)V2 - v1a;
+  const int64_t ldkd = p.ldk2 - p.ldk1, ldvd = p.ldv2 - p.ldv1;
+  const int kt1 = (kb1 / BK) * BK, kt2 = (kb2 / BK) * BK - n1 * BK;
+  auto fetch = [&](int t, int stage) {
+    const int f2 = t >= n1 ? 1 : 0;
+    const int fkt = (f2 ? kt2 : kt1) + t * BK;
+    const int fke = ke1 + f2 * (ke2 - ke1);
+    dma_tile<D>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, kvh * D, fkt, fke, Ks + stage * BK * D, wid, lane);
+    dma_tile<D>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, kvh * D, fkt, fke, Vr, wid, lane);
+  };
+  if (nt > 0) fetch(0, 0);
 #pragma unroll 1
   for (int t = 0; t < nt; ++t) {
-    __syncthreads();
-    UNOK_TILE_STORE(tile_st_row, kr, Ks, KS);
-    UNOK_TILE_STORE(tile_st_trans, vr, Vt, VS);
-    __syncthreads();
-    if (t + 1 < nt) UNOK_FETCH(t + 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();                       // K(t) and V rows(t) are in LDS
+    transpose_tile<D>(Vr, Vt, tid);
+    __syncthreads();                       // V^T(t) complete; V rows free for tile t+1
+    if (t + 1 < nt) fetch(t + 1, (t + 1) & 1);
+    const bf16_t* Kc = Ks + (t & 1) * BK * D;
     const bool s2 = t >= n1;
     const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
     const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
     const int w_maxlo = s2 ? wb2.maxlo : wb1.maxlo, w_minhi = s2 ? wb2.minhi : wb1.minhi;
-    const int lo = s2 ? ivq.z : ivq.x, hi = s2 ? ivq.w : ivq.y;
     if (kt >= w_hi || kt + BK <= w_lo) continue;
     const bool full = kt >= w_maxlo && kt + BK <= w_minhi;
-    f32x16_t sacc[2];
+    // Scores of both 32-key halves (kk) are issued first; the softmax of one half then runs on
+    // the VALU while the MFMA pipe works through the other half's products.
+    f32x16_t sacc[2][QG];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kk][r] = 0.f;
+      for (int qg = 0; qg < QG; ++qg)
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
+        for (int r = 0; r < 16; ++r) sacc[kk][qg][r] = 0.f;
+      bf16x8_t kf[NKS];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Ks[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
-                                                            qreg[ks], sacc[kk], 0, 0, 0);
-    float tmax = -INFINITY;
+      for (int ks = 0; ks < NKS; ++ks) kf[ks] = ld_frag<D>(Kc, kk * 32 + lq, ks * 2 + g);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+      for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float v = sacc[kk][j] * p.scale_log2;
-        if (!full) {
-          const int key = kt + kk * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-          if (key < lo || key >= hi) v = -INFINITY;
-        }
-        sacc[kk][j] = v;
-        tmax = fmaxf(tmax, v);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    // Lazy rescaling: the running max moves only when a row's tile max exceeds it by more than
-    // 8 (log2 units), so weights stay <= 2^8 and most tiles skip rescaling the accumulators.
-    const bool grow = tmax > m_run + 8.f;
-    if (__any(grow)) {
-      const float m_new = grow ? fmaxf(m_run, tmax) : m_run;
-      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int tt = 0; tt < NDT; ++tt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[tt][r] *= alpha;
-      m_run = m_new;
+        for (int qg = 0; qg < QG; ++qg)
+          sacc[kk][qg] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qreg[qg][ks], sacc[kk][qg], 0, 0, 0);
     }
-    // Branch-free when nothing is visible yet (m_run = -inf): every lane keeps feeding the
-    // shared MFMAs, with weights exp2(-inf) = 0.
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float e = fast_exp2(sacc[kk][j] - m_use);
-        sacc[kk][j] = e;
-        l_run += e;
+      for (int qg = 0; qg < QG; ++qg) {
+        f32x16_t& sv = sacc[kk][qg];
+        if (!full) {   // wave-uniform: only tiles that cut through some query's interval
+          const int lo = s2 ? ivq[qg].z : ivq[qg].x, hi = s2 ? ivq[qg].w : ivq[qg].y;
+          const int kbase = kt + kk * 32 + 4 * g;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int key = kbase + 8 * (j >> 2) + (j & 3);
+            sv[j] = (key >= lo && key < hi) ? sv[j] : -INFINITY;
+          }
+        }
+        // Raw scores; the scale (> 0) is applied inside the exponent: p = 2^(s*scale_log2 - m).
+        float tmax = sv[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) tmax = fmaxf(tmax, sv[j]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
+        // Lazy rescaling: the running max moves only when a row's max exceeds it by more than
+        // 8 (log2 units), so weights stay <= 2^8 and most steps skip rescaling the accumulators.
+        const bool grow = tmax > m_run[qg] + 8.f;
+        if (__any(grow)) {
+          const float m_new = grow ? fmaxf(m_run[qg], tmax) : m_run[qg];
+          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[qg] - m_new);
+          l_run[qg] *= alpha;
+#pragma unroll
+          for (int tt = 0; tt < NDT; ++tt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[qg][tt][r] *= alpha;
+          m_run[qg] = m_new;
+        }
+        // Branch-free when nothing is visible yet (m_run = -inf): every lane keeps feeding the
+        // shared MFMAs, with weights 2^-inf = 0.
+        const float neg_m = m_run[qg] == -INFINITY ? 0.f : -m_run[qg];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float e = fast_exp2(fmaf(sv[j], p.scale_log2, neg_m));
+          sv[j] = e;
+          l_run[qg] += e;
+        }
       }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        float pv[8];
+        bf16x8_t pb[QG];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pv[i] = sacc[kk][8 * hh + i];
-        const bf16x8_t b = pack_bf16x8(pv);
+        for (int qg = 0; qg < QG; ++qg) {
+          float pv[8];
 #pragma unroll
-        for (int tt = 0; tt < NDT; ++tt)
-          oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Vt[(tt * 32 + lq) * VS], kk * 32 + 16 * hh, g),
-                                                              b, oacc[tt], 0, 0, 0);
+          for (int i = 0; i < 8; ++i) pv[i] = sacc[kk][qg][8 * hh + i];
+          pb[qg] = pack_bf16x8(pv);
+        }
+#pragma unroll
+        for (int tt = 0; tt < NDT; ++tt) {
+          const bf16x8_t vf = ld_perm_t(Vt, tt * 32 + lq, kk * 4 + 2 * hh, g);
+#pragma unroll
+          for (int qg = 0; qg < QG; ++qg)
+            oacc[qg][tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[qg], oacc[qg][tt], 0, 0, 0);
+        }
       }
+    }
   }
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (qvalid) {
-    bf16_t* O = (bf16_t*)p.O + (int64_t)qrow * p.ldo + h * D;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+  for (int qg = 0; qg < QG; ++qg) {
+    const float l_tot = l_run[qg] + __shfl_xor(l_run[qg], 32, 64);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (qvalid[qg]) {
+      bf16_t* O = (bf16_t*)p.O + (int64_t)qrow[qg] * p.ldo + h * D;
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        uint2 u;
-        bf16_t* hv = (bf16_t*)&u;
+      for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hv[e] = f32_to_bf16(oacc[t][j4 * 4 + e] * inv);
-        *(uint2*)(O + t * 32 + 8 * j4 + 4 * g) = u;
-      }
-    if (g == 0) p.LSE[(int64_t)qrow * p.Hq + h] = l_tot > 0.f ? m_run + log2f(l_tot) : -INFINITY;
+        for (int j4 = 0; j4 < 4; ++j4) {
+          const f32x16_t& a = oacc[qg][t];
+          *(uint2*)(O + t * 32 + 8 * j4 + 4 * g) = make_uint2(pack2_bf16(a[j4 * 4] * inv, a[j4 * 4 + 1] * inv),
+                                                              pack2_bf16(a[j4 * 4 + 2] * inv, a[j4 * 4 + 3] * inv));
+        }
+      if (g == 0) p.LSE[(int64_t)qrow[qg] * p.Hq + h] = l_tot > 0.f ? m_run[qg] + log2f(l_tot) : -INFINITY;
+    }
   }
 }
 
@@ -387,9 +561,8 @@ __global__ __launch_bounds__(256) void attn_dq_bf16_kernel(const AttnArgs p) {
 
   const Bounds wb1 = wave_bounds(qvalid, ivq.x, ivq.y);
   const Bounds wb2 = wave_bounds(qvalid && p.K2 != nullptr, ivq.z, ivq.w);
-  int kb1, ke1, kb2, ke2;
-  wg_bounds(wb1, sh, kb1, ke1);
-  wg_bounds(wb2, sh, kb2, ke2);
+  const int2 r1 = wg_bounds(wb1, sh), r2 = wg_bounds(wb2, sh);
+  const int kb1 = r1.x, ke1 = r1.y, kb2 = r2.x, ke2 = r2.y;
   const int n1 = kb1 < ke1 ? (ke1 - (kb1 / BK) * BK + BK - 1) / BK : 0;
   const int n2 = (p.K2 != nullptr && kb2 < ke2) ? (ke2 - (kb2 / BK) * BK + BK - 1) / BK : 0;
   const int nt = n1 + n2;
@@ -520,8 +693,8 @@ __global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
     }
   }
   const Bounds wb = wave_bounds(kvalid, qlo, qhi);
-  int qb, qe;
-  wg_bounds(wb, sh, qb, qe);
+  const int2 rq = wg_bounds(wb, sh);
+  const int qb = rq.x, qe = rq.y;
   f32x16_t dk[NDT], dv[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t)
@@ -735,6 +908,17 @@ static int check_geom(int dtype, int D, int Hq, int Hkv) {
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+template <int D>
+static void launch_fwd(unsigned blocks, hipStream_t st, const AttnArgs& a) {
+  constexpr size_t lds = (3 * ATT_BK * D + D * ATT_TS) * sizeof(bf16_t);
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    configured = true;
+  }
+  hipLaunchKernelGGL(attn_fwd_bf16_kernel<D>, dim3(blocks), dim3(256), lds, st, a);
+}
+
 // Forward. K2/V2 may be null (single source). Strides in elements.
 UNOK_EXPORT int unok_attn_fwd(int dtype, int Mq, int Hq, int Hkv, int D, const void* Q, int64_t ldq, const void* K1,
                               int64_t ldk1, const void* V1, int64_t ldv1, const void* K2, int64_t ldk2, const void* V2,
@@ -755,9 +939,9 @@ UNOK_EXPORT int unok_attn_fwd(int dtype, int Mq, int Hq, int Hkv, int D, const v
     UNOK_REQUIRE(al16(Q) && al16(K1) && al16(V1) && ldq % 8 == 0 && ldk1 % 8 == 0 && ldv1 % 8 == 0 && ldo % 8 == 0 &&
                  (!K2 || (al16(K2) && al16(V2) && ldk2 % 8 == 0 && ldv2 % 8 == 0)),
                  UNOK_EALIGN, "attention(bf16): operands must be 16-byte aligned with strides multiple of 8");
-    const unsigned blocks = (unsigned)(((Mq + 127) / 128) * Hq);
-    if (D == 128) hipLaunchKernelGGL(attn_fwd_bf16_kernel<128>, dim3(blocks), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(attn_fwd_bf16_kernel<64>, dim3(blocks), dim3(256), 0, st, a);
+    const unsigned blocks = (unsigned)(((Mq + 255) / 256) * Hq);
+    if (D == 128) launch_fwd<128>(blocks, st, a);
+    else launch_fwd<64>(blocks, st, a);
   }
   return unok::check_launch("attn_fwd");
 }
