@@ -17,6 +17,8 @@
 // log2-sum-exp2 of the scaled scores (lse2) for the backward pass.
 #include "common.h"
 
+#include <stdlib.h>
+
 struct AttnArgs {
   const void* Q; int64_t ldq;          // [Mq, Hq*D]
   const void* K1; int64_t ldk1;        // source 1 keys  [Mk1, Hkv*D]
@@ -311,9 +313,9 @@ __device__ __forceinline__ Bounds merge_bounds(const Bounds& a, const Bounds& b)
 // Forward, bf16: one workgroup = 256 queries of one q-head; each wave owns 64 queries as two
 // groups of 32 (one per MFMA column block), so every K/V fragment read from LDS feeds two MFMAs.
 // ---------------------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(256) void attn_fwd_bf16_kernel(const AttnArgs p) {
-  constexpr int BK = ATT_BK, NKS = D / 16, NDT = D / 32, QG = 2, BQ = 256;
+template <int D, int QG>
+__global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(const AttnArgs p) {
+  constexpr int BK = ATT_BK, NKS = D / 16, NDT = D / 32, BQ = 128 * QG;
   // Dynamic LDS: K tiles [2][64*D] (direct-to-LDS double buffer), V rows [64*D], V^T [D][72].
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   bf16_t* Ks = smem;
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_kernel(const AttnArgs p) {
   bf16x8_t qreg[QG][NKS];
 #pragma unroll
   for (int qg = 0; qg < QG; ++qg) {
-    qrow[qg] = qt * BQ + w * 64 + qg * 32 + lq;
+    qrow[qg] = qt * BQ + w * (32 * QG) + qg * 32 + lq;
     qvalid[qg] = qrow[qg] < p.Mq;
     ivq[qg] = qvalid[qg] ? *(const int4*)(p.iv + (int64_t)qrow[qg] * 8) : make_int4(0, 0, 0, 0);
 #pragma unroll
@@ -356,10 +358,14 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_kernel(const AttnArgs p) {
   }
 
   // Tile walk over both sources: tiles [0, n1) come from source 1, [n1, n1 + n2) from source 2.
-  const Bounds wb1 = merge_bounds(wave_bounds(qvalid[0], ivq[0].x, ivq[0].y), wave_bounds(qvalid[1], ivq[1].x, ivq[1].y));
   const bool has2 = p.K2 != nullptr;
-  const Bounds wb2 = merge_bounds(wave_bounds(has2 && qvalid[0], ivq[0].z, ivq[0].w),
-                                  wave_bounds(has2 && qvalid[1], ivq[1].z, ivq[1].w));
+  Bounds wb1 = wave_bounds(qvalid[0], ivq[0].x, ivq[0].y);
+  Bounds wb2 = wave_bounds(has2 && qvalid[0], ivq[0].z, ivq[0].w);
+#pragma unroll
+  for (int qg = 1; qg < QG; ++qg) {
+    wb1 = merge_bounds(wb1, wave_bounds(qvalid[qg], ivq[qg].x, ivq[qg].y));
+    wb2 = merge_bounds(wb2, wave_bounds(has2 && qvalid[qg], ivq[qg].z, ivq[qg].w));
+  }
   const int2 r1 = wg_bounds(wb1, sh), r2 = wg_bounds(wb2, sh);
   const int kb1 = r1.x, ke1 = r1.y, kb2 = r2.x, ke2 = r2.y;
   const int n1 = kb1 < ke1 ? (ke1 - (kb1 / BK) * BK + BK - 1) / BK : 0;
@@ -908,15 +914,32 @@ static int check_geom(int dtype, int D, int Hq, int Hkv) {
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-template <int D>
-static void launch_fwd(unsigned blocks, hipStream_t st, const AttnArgs& a) {
+// Queries per wave in the forward: 32 (QG = 1, two workgroups per CU) or 64 (QG = 2, one).
+// UNOK_ATTN_QG selects, for tuning.
+static int attn_qg() {
+  static int q = [] {
+    const char* e = getenv("UNOK_ATTN_QG");
+    return (e && atoi(e) == 2) ? 2 : 1;
+  }();
+  return q;
+}
+
+template <int D, int QG>
+static void launch_fwd_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
   constexpr size_t lds = (3 * ATT_BK * D + D * ATT_TS) * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<D, QG>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
-  hipLaunchKernelGGL(attn_fwd_bf16_kernel<D>, dim3(blocks), dim3(256), lds, st, a);
+  const unsigned blocks = (unsigned)(((Mq + 128 * QG - 1) / (128 * QG)) * Hq);
+  hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, QG>), dim3(blocks), dim3(256), lds, st, a);
+}
+
+template <int D>
+static void launch_fwd(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
+  if (attn_qg() == 2) launch_fwd_t<D, 2>(Mq, Hq, st, a);
+  else launch_fwd_t<D, 1>(Mq, Hq, st, a);
 }
 
 // Forward. K2/V2 may be null (single source). Strides in elements.
@@ -939,9 +962,8 @@ UNOK_EXPORT int unok_attn_fwd(int dtype, int Mq, int Hq, int Hkv, int D, const v
     UNOK_REQUIRE(al16(Q) && al16(K1) && al16(V1) && ldq % 8 == 0 && ldk1 % 8 == 0 && ldv1 % 8 == 0 && ldo % 8 == 0 &&
                  (!K2 || (al16(K2) && al16(V2) && ldk2 % 8 == 0 && ldv2 % 8 == 0)),
                  UNOK_EALIGN, "attention(bf16): operands must be 16-byte aligned with strides multiple of 8");
-    const unsigned blocks = (unsigned)(((Mq + 255) / 256) * Hq);
-    if (D == 128) launch_fwd<128>(blocks, st, a);
-    else launch_fwd<64>(blocks, st, a);
+    if (D == 128) launch_fwd<128>(Mq, Hq, st, a);
+    else launch_fwd<64>(Mq, Hq, st, a);
   }
   return unok::check_launch("attn_fwd");
 }
