@@ -250,10 +250,11 @@ template <int D> __device__ __forceinline__ int kswz(int r) { return D == 128 ? 
 // One 64-row tile of a row-major [rows, ld] bf16 matrix (columns [col0, col0 + D)) via buffer
 // loads straight into LDS. The buffer resource starts at row k0 and covers rows [k0, kend), so
 // rows past kend read as zeros without any clamping arithmetic (their keys are masked).
-template <int D>
+template <int D, int NW = 4>
 __device__ __forceinline__ void dma_tile(const bf16_t* src, int64_t ld, int col0, int k0, int kend, bf16_t* dst,
                                          int wid, int lane) {
-  constexpr int CPR = D / 8, RPI = 64 / CPR, INS = 64 / (RPI * 4);
+  constexpr int CPR = D / 8, RPI = 64 / CPR, INS = 64 / (RPI * NW);
+  static_assert(INS >= 1, "tile too small for the wave count");
   const int rl = lane / CPR, slot = lane % CPR;
   const int nrows = max(0, min(kend - k0, 64));
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -261,9 +262,9 @@ __device__ __forceinline__ void dma_tile(const bf16_t* src, int64_t ld, int col0
   const uint32_t ldb = (uint32_t)ld * 2;
 #pragma unroll
   for (int i = 0; i < INS; ++i) {
-    const int r = (i * 4 + wid) * RPI + rl;
+    const int r = (i * NW + wid) * RPI + rl;
     const uint32_t voff = (uint32_t)r * ldb + (uint32_t)(col0 + ((slot ^ kswz<D>(r)) << 3)) * 2;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + (i * 4 + wid) * RPI * D),
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + (i * NW + wid) * RPI * D),
                                              16, voff, 0, 0, 0);
   }
 }
@@ -523,22 +524,25 @@ __global__ __launch_bounds__(256) void attn_dsum_kernel(const T* __restrict__ dO
   if (lane == 0) Dsum[item] = s;
 }
 
-// dQ, bf16: per workgroup 128 queries of one head; same tile walk as the forward.
+// dQ, bf16: per workgroup 256 queries (8 waves x 32) of one head; same tile walk as the forward.
+// K and V tiles stream into LDS by buffer loads (two stages); the transposed K used by the dQ
+// product is built LDS -> LDS at the start of each tile. Per 32-key half: S = K Q^T and
+// dP = V dO^T, then dS = P (dP - Dsum), then dQ += dS K.
 template <int D>
-__global__ __launch_bounds__(256) void attn_dq_bf16_kernel(const AttnArgs p) {
-  constexpr int BK = 64, KS = D + 8, TS = BK + 4, NKS = D / 16, NDT = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[BK * KS];
-  __shared__ __attribute__((aligned(16))) bf16_t Kt[D * TS];
-  __shared__ __attribute__((aligned(16))) bf16_t Vs[BK * KS];
-  __shared__ int sh[8];
+__global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
+  constexpr int BK = ATT_BK, NKS = D / 16, NDT = D / 32, NW = 8, BQ = 32 * NW;
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  bf16_t* Ks = smem;                      // [2][64*D]
+  bf16_t* Vs = smem + 2 * BK * D;         // [2][64*D]
+  bf16_t* Kt = Vs + 2 * BK * D;           // [D][ATT_TS]
+  __shared__ int sh[16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
-  const int nqt = (p.Mq + 127) / 128;
+  const int wid = __builtin_amdgcn_readfirstlane(w);
+  const int nqt = (p.Mq + BQ - 1) / BQ;
   const int lin = xcd_remap(blockIdx.x, nqt * p.Hq);
-  // q tiles are walked from the last to the first: with causal-like masks the late tiles carry
-  // the most key tiles, so the heaviest workgroups start first and the tail is light.
   const int h = lin % p.Hq, qt = nqt - 1 - lin / p.Hq;
   const int kvh = h / (p.Hq / p.Hkv);
-  const int qrow = qt * 128 + w * 32 + lq;
+  const int qrow = qt * BQ + w * 32 + lq;
   const bool qvalid = qrow < p.Mq;
   int4 ivq = make_int4(0, 0, 0, 0);
   float lse = 0.f, dsum = 0.f;
@@ -552,12 +556,9 @@ __global__ __launch_bounds__(256) void attn_dq_bf16_kernel(const AttnArgs p) {
   bf16x8_t qreg[NKS], oreg[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) {
-    if (qvalid) {
-      qreg[ks] = ld_bf16x8(Q + (int64_t)qrow * p.ldq + h * D + ks * 16 + g * 8);
-      oreg[ks] = ld_bf16x8(dO + (int64_t)qrow * p.lddo + h * D + ks * 16 + g * 8);
-    } else {
-      qreg[ks] = oreg[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
-    }
+    const bf16x8_t z = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+    qreg[ks] = qvalid ? ld_bf16x8(Q + (int64_t)qrow * p.ldq + h * D + ks * 16 + g * 8) : z;
+    oreg[ks] = qvalid ? ld_bf16x8(dO + (int64_t)qrow * p.lddo + h * D + ks * 16 + g * 8) : z;
   }
   f32x16_t dq[NDT];
 #pragma unroll
@@ -565,99 +566,109 @@ __global__ __launch_bounds__(256) void attn_dq_bf16_kernel(const AttnArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[t][r] = 0.f;
 
-  const Bounds wb1 = wave_bounds(qvalid, ivq.x, ivq.y);
-  const Bounds wb2 = wave_bounds(qvalid && p.K2 != nullptr, ivq.z, ivq.w);
-  const int2 r1 = wg_bounds(wb1, sh), r2 = wg_bounds(wb2, sh);
-  const int kb1 = r1.x, ke1 = r1.y, kb2 = r2.x, ke2 = r2.y;
+  const bool has2 = p.K2 != nullptr;
+  Bounds wb1 = wave_bounds(qvalid, ivq.x, ivq.y);
+  Bounds wb2 = wave_bounds(has2 && qvalid, ivq.z, ivq.w);
+  wb1.lo = __builtin_amdgcn_readfirstlane(wb1.lo); wb1.hi = __builtin_amdgcn_readfirstlane(wb1.hi);
+  wb1.maxlo = __builtin_amdgcn_readfirstlane(wb1.maxlo); wb1.minhi = __builtin_amdgcn_readfirstlane(wb1.minhi);
+  wb2.lo = __builtin_amdgcn_readfirstlane(wb2.lo); wb2.hi = __builtin_amdgcn_readfirstlane(wb2.hi);
+  wb2.maxlo = __builtin_amdgcn_readfirstlane(wb2.maxlo); wb2.minhi = __builtin_amdgcn_readfirstlane(wb2.minhi);
+  // workgroup bounds over 8 waves
+  if (lane == 0) { sh[w * 2] = wb1.lo; sh[w * 2 + 1] = wb1.hi; }
+  __syncthreads();
+  int kb1 = INT_MAX, ke1 = INT_MIN;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) { kb1 = min(kb1, sh[2 * i]); ke1 = max(ke1, sh[2 * i + 1]); }
+  __syncthreads();
+  if (lane == 0) { sh[w * 2] = wb2.lo; sh[w * 2 + 1] = wb2.hi; }
+  __syncthreads();
+  int kb2 = INT_MAX, ke2 = INT_MIN;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) { kb2 = min(kb2, sh[2 * i]); ke2 = max(ke2, sh[2 * i + 1]); }
+  kb1 = __builtin_amdgcn_readfirstlane(kb1); ke1 = __builtin_amdgcn_readfirstlane(ke1);
+  kb2 = __builtin_amdgcn_readfirstlane(kb2); ke2 = __builtin_amdgcn_readfirstlane(ke2);
   const int n1 = kb1 < ke1 ? (ke1 - (kb1 / BK) * BK + BK - 1) / BK : 0;
-  const int n2 = (p.K2 != nullptr && kb2 < ke2) ? (ke2 - (kb2 / BK) * BK + BK - 1) / BK : 0;
+  const int n2 = (has2 && kb2 < ke2) ? (ke2 - (kb2 / BK) * BK + BK - 1) / BK : 0;
   const int nt = n1 + n2;
-  const bf16_t* K1 = (const bf16_t*)p.K1;
-  const bf16_t* V1 = (const bf16_t*)p.V1;
-  const bf16_t* K2 = (const bf16_t*)p.K2;
-  const bf16_t* V2 = (const bf16_t*)p.V2;
-  // Next-tile prefetch: the source is selected with scalar selects (no branch writing the
-  // staging registers).
-  uint4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
-  kr2 = kr3 = vr2 = vr3 = make_uint4(0, 0, 0, 0);
-#define UNOK_FETCH(t_)                                                                     \
-  do {                                                                                     \
-    const bool f2 = (t_) >= n1;                                                            \
-    const int fkt = f2 ? (kb2 / BK) * BK + ((t_) - n1) * BK : (kb1 / BK) * BK + (t_) * BK;   \
-    const int fke = f2 ? ke2 : ke1;                                                        \
-    const bf16_t* fk = f2 ? K2 : K1;                                                       \
-    const bf16_t* fv = f2 ? V2 : V1;                                                       \
-    const int64_t fldk = f2 ? p.ldk2 : p.ldk1, fldv = f2 ? p.ldv2 : p.ldv1;               \
-    UNOK_TILE_LOAD(kr, fk, fldk, kvh * D, fkt, fke);                                       \
-    UNOK_TILE_LOAD(vr, fv, fldv, kvh * D, fkt, fke);                                       \
-  } while (0)
-  if (nt > 0) UNOK_FETCH(0);
+
+  // Source selection is arithmetic (see the forward kernel).
+  const uintptr_t k1a = (uintptr_t)p.K1, v1a = (uintptr_t)p.V1;
+  const uintptr_t kd = (uintptr_t)p.K2 - k1a, vd = (uintptr_t)p.V2 - v1a;
+  const int64_t ldkd = p.ldk2 - p.ldk1, ldvd = p.ldv2 - p.ldv1;
+  const int kt1 = (kb1 / BK) * BK, kt2 = (kb2 / BK) * BK - n1 * BK;
+  auto fetch = [&](int t, int stage) {
+    const int f2 = t >= n1 ? 1 : 0;
+    const int fkt = (f2 ? kt2 : kt1) + t * BK;
+    const int fke = ke1 + f2 * (ke2 - ke1);
+    dma_tile<D, NW>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, kvh * D, fkt, fke, Ks + stage * BK * D, wid, lane);
+    dma_tile<D, NW>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, kvh * D, fkt, fke, Vs + stage * BK * D, wid, lane);
+  };
+  if (nt > 0) fetch(0, 0);
 #pragma unroll 1
   for (int t = 0; t < nt; ++t) {
-    __syncthreads();
-    UNOK_TILE_STORE(tile_st_row, kr, Ks, KS);
-    UNOK_TILE_STORE(tile_st_trans, kr, Kt, TS);
-    UNOK_TILE_STORE(tile_st_row, vr, Vs, KS);
-    __syncthreads();
-    if (t + 1 < nt) UNOK_FETCH(t + 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();                       // K(t), V(t) in LDS; previous tile's reads are done
+    const bf16_t* Kc = Ks + (t & 1) * BK * D;
+    const bf16_t* Vc = Vs + (t & 1) * BK * D;
+    transpose_tile<D>(Kc, Kt, tid);
+    if (t + 1 < nt) fetch(t + 1, (t + 1) & 1);
+    __syncthreads();                       // K^T(t) complete
     const bool s2 = t >= n1;
     const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
     const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
     const int w_maxlo = s2 ? wb2.maxlo : wb1.maxlo, w_minhi = s2 ? wb2.minhi : wb1.minhi;
-    const int lo = s2 ? ivq.z : ivq.x, hi = s2 ? ivq.w : ivq.y;
     if (kt >= w_hi || kt + BK <= w_lo) continue;
     const bool full = kt >= w_maxlo && kt + BK <= w_minhi;
-    f32x16_t sacc[2], dpacc[2];
+    const int lo = full ? INT_MIN / 2 : (s2 ? ivq.z : ivq.x);
+    const int hi = full ? INT_MAX / 2 : (s2 ? ivq.w : ivq.y);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < 2; ++kk) {
+      f32x16_t sacc, dpacc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) { sacc[kk][r] = 0.f; dpacc[kk][r] = 0.f; }
+      for (int r = 0; r < 16; ++r) { sacc[r] = 0.f; dpacc[r] = 0.f; }
+      // fragments in groups of 4 (16 registers) to stay within two waves per SIMD
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
+      for (int k0 = 0; k0 < NKS; k0 += 4) {
+        bf16x8_t f[4], v[4];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Ks[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
-                                                            qreg[ks], sacc[kk], 0, 0, 0);
-        dpacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Vs[(kk * 32 + lq) * KS + ks * 16 + g * 8]),
-                                                             oreg[ks], dpacc[kk], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) f[i] = ld_frag<D>(Kc, kk * 32 + lq, (k0 + i) * 2 + g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = ld_frag<D>(Vc, kk * 32 + lq, (k0 + i) * 2 + g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], qreg[k0 + i], sacc, 0, 0, 0);
+          dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[i], oreg[k0 + i], dpacc, 0, 0, 0);
+        }
       }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+      const int kbase = kt + kk * 32 + 4 * g;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float pr = fast_exp2(sacc[kk][j] * p.scale_log2 - lse);
-        if (!full) {
-          const int key = kt + kk * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-          if (key < lo || key >= hi) pr = 0.f;
-        }
-        sacc[kk][j] = pr * (dpacc[kk][j] - dsum);
+        const int key = kbase + 8 * (j >> 2) + (j & 3);
+        const float pr = (key >= lo && key < hi) ? fast_exp2(fmaf(sacc[j], p.scale_log2, -lse)) : 0.f;
+        sacc[j] = pr * (dpacc[j] - dsum);
       }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         float dv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dv[i] = sacc[kk][8 * hh + i];
+        for (int i = 0; i < 8; ++i) dv[i] = sacc[8 * hh + i];
         const bf16x8_t b = pack_bf16x8(dv);
 #pragma unroll
         for (int tt = 0; tt < NDT; ++tt)
-          dq[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Kt[(tt * 32 + lq) * TS], kk * 32 + 16 * hh, g), b,
-                                                            dq[tt], 0, 0, 0);
+          dq[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm_t(Kt, tt * 32 + lq, kk * 4 + 2 * hh, g), b, dq[tt],
+                                                            0, 0, 0);
       }
+    }
   }
   if (qvalid) {
     bf16_t* out = (bf16_t*)p.dQ + (int64_t)qrow * p.lddq + h * D;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        uint2 u;
-        bf16_t* hv = (bf16_t*)&u;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) hv[e] = f32_to_bf16(dq[t][j4 * 4 + e] * p.scale);
-        *(uint2*)(out + t * 32 + 8 * j4 + 4 * g) = u;
-      }
+      for (int j4 = 0; j4 < 4; ++j4)
+        *(uint2*)(out + t * 32 + 8 * j4 + 4 * g) =
+            make_uint2(pack2_bf16(dq[t][j4 * 4] * p.scale, dq[t][j4 * 4 + 1] * p.scale),
+                       pack2_bf16(dq[t][j4 * 4 + 2] * p.scale, dq[t][j4 * 4 + 3] * p.scale));
   }
 }
 
@@ -937,6 +948,18 @@ static void launch_fwd_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
 }
 
 template <int D>
+static void launch_dq(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
+  constexpr size_t lds = (4 * ATT_BK * D + D * ATT_TS) * sizeof(bf16_t);
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)attn_dq_bf16_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    configured = true;
+  }
+  const unsigned blocks = (unsigned)(((Mq + 255) / 256) * Hq);
+  hipLaunchKernelGGL(attn_dq_bf16_kernel<D>, dim3(blocks), dim3(512), lds, st, a);
+}
+
+template <int D>
 static void launch_fwd(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
   if (attn_qg() == 2) launch_fwd_t<D, 2>(Mq, Hq, st, a);
   else launch_fwd_t<D, 1>(Mq, Hq, st, a);
@@ -1005,9 +1028,8 @@ UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D
   }
   UNOK_REQUIRE(al16(dO) && lddo % 8 == 0 && lddq % 8 == 0 && (!want_kv || (lddk % 8 == 0 && lddv % 8 == 0)),
                UNOK_EALIGN, "attn_bwd(bf16): gradient strides must be multiples of 8");
-  const unsigned qblocks = (unsigned)(((Mq + 127) / 128) * Hq);
-  if (D == 128) hipLaunchKernelGGL(attn_dq_bf16_kernel<128>, dim3(qblocks), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(attn_dq_bf16_kernel<64>, dim3(qblocks), dim3(256), 0, st, a);
+  if (D == 128) launch_dq<128>(Mq, Hq, st, a);
+  else launch_dq<64>(Mq, Hq, st, a);
   rc = unok::check_launch("attn_dq_bf16");
   if (rc || !want_kv) return rc;
   const unsigned kblocks = (unsigned)(((Mk2 + 127) / 128) * Hkv);
