@@ -30,7 +30,7 @@ struct AttnArgs {
   float* LSE;                          // [Mq, Hq]
   // backward
   const void* dO; int64_t lddo;
-  const float* Dsum;                   // [Mq, Hq] rowsum(dO * O)
+  float* Dsum;                         // [Mq, Hq] rowsum(dO * O), written by the dQ kernel
   void* dQ; int64_t lddq;
   const int32_t* ivk;                  // [Mk2, 8] key-side table (qlo2, qhi2 at 4, 5)
   void* dK; int64_t lddk;              // [Mk2, Hkv*D]
@@ -70,28 +70,6 @@ __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
   return v;
-}
-
-// Loads a [64 rows x D] tile of a row-major [rows, *] bf16 matrix (column offset col0) into
-// LDS, row-major with stride RS and/or transposed ([D][64] with stride TS). Rows >= rend are 0.
-template <int D, bool ROW, bool TRN, int RS, int TS>
-__device__ __forceinline__ void stage_tile(const bf16_t* src, int64_t ld, int col0, int r0, int rend, bf16_t* rowdst,
-                                           bf16_t* trndst) {
-  constexpr int CPR = D / 8;               // 16-byte chunks per row
-  constexpr int ITER = 64 * CPR / 256;
-#pragma unroll
-  for (int i = 0; i < ITER; ++i) {
-    const int c = threadIdx.x + 256 * i, r = c / CPR, dc = (c % CPR) * 8;
-    const int row = r0 + r;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (row < rend) v = *(const uint4*)(src + (int64_t)row * ld + col0 + dc);
-    if (ROW) *(uint4*)&rowdst[r * RS + dc] = v;
-    if (TRN) {
-      const bf16_t* h = (const bf16_t*)&v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) trndst[(dc + e) * TS + r] = h[e];
-    }
-  }
 }
 
 // Register staging of a [64 rows x D] tile: global loads into four flat uint4 registers
@@ -545,21 +523,28 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
   const int qrow = qt * BQ + w * 32 + lq;
   const bool qvalid = qrow < p.Mq;
   int4 ivq = make_int4(0, 0, 0, 0);
-  float lse = 0.f, dsum = 0.f;
+  float lse = 0.f;
   if (qvalid) {
     ivq = *(const int4*)(p.iv + (int64_t)qrow * 8);
     lse = p.LSE[(int64_t)qrow * p.Hq + h];
-    dsum = p.Dsum[(int64_t)qrow * p.Hq + h];
   }
   const bf16_t* Q = (const bf16_t*)p.Q;
   const bf16_t* dO = (const bf16_t*)p.dO;
+  const bf16_t* Ob = (const bf16_t*)p.O;
   bf16x8_t qreg[NKS], oreg[NKS];
+  // Dsum = rowsum(dO * O) of this (query, head): each lane holds half of the head's dims.
+  float dpart = 0.f;
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) {
     const bf16x8_t z = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
     qreg[ks] = qvalid ? ld_bf16x8(Q + (int64_t)qrow * p.ldq + h * D + ks * 16 + g * 8) : z;
     oreg[ks] = qvalid ? ld_bf16x8(dO + (int64_t)qrow * p.lddo + h * D + ks * 16 + g * 8) : z;
+    const bf16x8_t ov = qvalid ? ld_bf16x8(Ob + (int64_t)qrow * p.ldo + h * D + ks * 16 + g * 8) : z;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dpart = fmaf((float)oreg[ks][e], (float)ov[e], dpart);
   }
+  const float dsum = dpart + __shfl_xor(dpart, 32, 64);
+  if (qvalid && g == 0) p.Dsum[(int64_t)qrow * p.Hq + h] = dsum;
   f32x16_t dq[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t)
@@ -672,15 +657,47 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
   }
 }
 
+// Stages a [64 rows x D] tile of Q or dO for the dK/dV kernel: row-major (pitch RS) and
+// transposed ([D][ATT_TS] with the tslot swizzle), from 8x8 register blocks so both copies are
+// written with 16-byte stores. `half` selects the thread group (threads [128 * half, +128)).
+template <int D, int RS>
+__device__ __forceinline__ void stage_rows_and_t(const bf16_t* src, int64_t ld, int col0, int r0, int rend,
+                                                 bf16_t* rowdst, bf16_t* trndst, int t) {
+  constexpr int CPR = D / 8;
+  if (t >= 8 * CPR) return;
+  const int kg = t / CPR, dg = t % CPR;
+  uint4 st[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = kg * 8 + i;
+    const int row = r0 + r;
+    st[i] = row < rend ? *(const uint4*)(src + (int64_t)row * ld + col0 + dg * 8) : make_uint4(0, 0, 0, 0);
+    *(uint4*)&rowdst[r * RS + dg * 8] = st[i];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint4 a = st[2 * k], b = st[2 * k + 1];
+      const uint32_t da = (e >> 1) == 0 ? a.x : (e >> 1) == 1 ? a.y : (e >> 1) == 2 ? a.z : a.w;
+      const uint32_t db = (e >> 1) == 0 ? b.x : (e >> 1) == 1 ? b.y : (e >> 1) == 2 ? b.z : b.w;
+      w[k] = (e & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
+    }
+    const int d = dg * 8 + e;
+    *(uint4*)&trndst[d * ATT_TS + tslot(d, kg) * 8] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // dK, dV of source-2 keys, bf16: per workgroup 128 keys (4 waves x 32) of one kv-head; walks
 // the query rows [qlo2, qhi2) of those keys for every q-head of the GQA group.
 template <int D>
 __global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
-  constexpr int BQ = 64, RS = D + 8, TS = BQ + 4, NKS = D / 16, NDT = D / 32;
+  constexpr int BQ = 64, RS = D + 8, NKS = D / 16, NDT = D / 32;
   __shared__ __attribute__((aligned(16))) bf16_t Qs[BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Qt[D * TS];
+  __shared__ __attribute__((aligned(16))) bf16_t Qt[D * ATT_TS];
   __shared__ __attribute__((aligned(16))) bf16_t Os[BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Ot[D * TS];
+  __shared__ __attribute__((aligned(16))) bf16_t Ot[D * ATT_TS];
   __shared__ float s_lse[BQ], s_dsum[BQ];
   __shared__ int s_lo[BQ], s_hi[BQ];
   __shared__ int sh[8];
@@ -726,8 +743,8 @@ __global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
 #pragma unroll 1
       for (int q0 = (qb / BQ) * BQ; q0 < qe; q0 += BQ) {
         __syncthreads();
-        stage_tile<D, true, true, RS, TS>(Q, p.ldq, h * D, q0, qe, Qs, Qt);
-        stage_tile<D, true, true, RS, TS>(dO, p.lddo, h * D, q0, qe, Os, Ot);
+        if (tid < 128) stage_rows_and_t<D, RS>(Q, p.ldq, h * D, q0, qe, Qs, Qt, tid);
+        else stage_rows_and_t<D, RS>(dO, p.lddo, h * D, q0, qe, Os, Ot, tid - 128);
         if (tid < BQ) {
           const int qr = q0 + tid;
           const bool ok = qr < qe;
@@ -772,9 +789,9 @@ __global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
             const bf16x8_t bp = pack_bf16x8(pv), bds = pack_bf16x8(dsv);
 #pragma unroll
             for (int t = 0; t < NDT; ++t) {
-              dv[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Ot[(t * 32 + lq) * TS], qq * 32 + 16 * hh, g), bp,
+              dv[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm_t(Ot, t * 32 + lq, qq * 4 + 2 * hh, g), bp,
                                                                dv[t], 0, 0, 0);
-              dk[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm(&Qt[(t * 32 + lq) * TS], qq * 32 + 16 * hh, g), bds,
+              dk[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm_t(Qt, t * 32 + lq, qq * 4 + 2 * hh, g), bds,
                                                                dk[t], 0, 0, 0);
             }
           }
@@ -1004,15 +1021,15 @@ UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   const unsigned items = (unsigned)(((int64_t)Mq * Hq + 3) / 4);
-  if (dtype == UNOK_BF16)
-    hipLaunchKernelGGL(attn_dsum_kernel<bf16_t>, dim3(items), dim3(256), 0, st, (const bf16_t*)dO, lddo,
-                       (const bf16_t*)O, ldo, Dsum, Mq, Hq, D);
-  else
+  if (dtype == UNOK_F32) {
+    // The fp32 path forms Dsum in its own pass; the bf16 dQ kernel forms it on the fly.
     hipLaunchKernelGGL(attn_dsum_kernel<float>, dim3(items), dim3(256), 0, st, (const float*)dO, lddo,
                        (const float*)O, ldo, Dsum, Mq, Hq, D);
-  rc = unok::check_launch("attn_dsum");
-  if (rc) return rc;
+    rc = unok::check_launch("attn_dsum");
+    if (rc) return rc;
+  }
   AttnArgs a{};
+  a.O = const_cast<void*>(O); a.ldo = ldo;
   a.Q = Q; a.ldq = ldq; a.K1 = K1; a.ldk1 = ldk1; a.V1 = V1; a.ldv1 = ldv1;
   a.K2 = K2; a.ldk2 = ldk2; a.V2 = V2; a.ldv2 = ldv2; a.iv = iv; a.ivk = ivk; a.LSE = (float*)LSE;
   a.dO = dO; a.lddo = lddo; a.Dsum = Dsum; a.dQ = dQ; a.lddq = lddq; a.dK = dK; a.lddk = lddk; a.dV = dV; a.lddv = lddv;
@@ -1026,7 +1043,8 @@ UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D
     hipLaunchKernelGGL(attn_dkv_f32_kernel, dim3((unsigned)(((int64_t)Mk2 * Hkv + 3) / 4)), dim3(256), 0, st, a, D);
     return unok::check_launch("attn_dkv_f32");
   }
-  UNOK_REQUIRE(al16(dO) && lddo % 8 == 0 && lddq % 8 == 0 && (!want_kv || (lddk % 8 == 0 && lddv % 8 == 0)),
+  UNOK_REQUIRE(al16(dO) && al16(O) && lddo % 8 == 0 && ldo % 8 == 0 && lddq % 8 == 0 &&
+                   (!want_kv || (lddk % 8 == 0 && lddv % 8 == 0)),
                UNOK_EALIGN, "attn_bwd(bf16): gradient strides must be multiples of 8");
   if (D == 128) launch_dq<128>(Mq, Hq, st, a);
   else launch_dq<64>(Mq, Hq, st, a);

@@ -121,118 +121,167 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------
-// q/k RMSNorm (optional) + RoPE. One wavefront per (row, head); lane i handles the RoPE pair
-// (i, i + d/2). Reads the fused qkv projection output, writes contiguous q and k.
+// q/k RMSNorm (optional) + RoPE. One wavefront per row covers all q and k heads of the row,
+// HPW heads per pass: each lane owns 16 contiguous bytes (EPL elements) of a head and the RoPE
+// partner elements (i +- d/2) sit LPH/2 lanes away, fetched with a lane shuffle. The row's
+// angles fl32(pos * inv_freq[j]) are evaluated once per row (one sincosf per lane) into LDS.
+// Reads the fused qkv projection output, writes contiguous q and k.
 // ---------------------------------------------------------------------------------------
-template <typename T>
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void load(const bf16_t* p, float (&v)[8]) {
+    const uint4 u = *(const uint4*)p;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[2 * i] = __uint_as_float(w[i] << 16); v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u); }
+  }
+  __device__ __forceinline__ static void store(bf16_t* p, const float (&v)[8]) {
+    *(uint4*)p = make_uint4(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]), pack2_bf16(v[4], v[5]), pack2_bf16(v[6], v[7]));
+  }
+};
+template <> struct Vec16<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void load(const float* p, float (&v)[4]) {
+    const float4 u = *(const float4*)p;
+    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+  }
+  __device__ __forceinline__ static void store(float* p, const float (&v)[4]) { *(float4*)p = make_float4(v[0], v[1], v[2], v[3]); }
+};
+
+// Angles of one row into LDS (cs, sn: d/2 floats each, one wavefront).
+__device__ __forceinline__ void rope_angles(float p, const float* __restrict__ inv_freq, int half, float* cs,
+                                            float* sn, int lane) {
+  for (int j = lane; j < half; j += 64) {
+    float sv, cv;
+    sincosf(p * inv_freq[j], &sv, &cv);
+    cs[j] = cv;
+    sn[j] = sv;
+  }
+}
+
+template <typename T, int D>
 __global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const T* __restrict__ qkv, int64_t ld, const T* wq,
                                                               const T* wk, const int64_t* __restrict__ pos,
                                                               const float* __restrict__ inv_freq, T* __restrict__ qo,
                                                               T* __restrict__ ko, float* __restrict__ rstd, int M,
-                                                              int nq, int nk, int d, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+                                                              int nq, int nk, float eps) {
+  constexpr int EPL = Vec16<T>::N, LPH = D / EPL, HPW = 64 / LPH, HALF = D / 2;
+  static_assert(LPH >= 2 && LPH <= 64 && 64 % LPH == 0, "head geometry");
+  __shared__ float s_cs[4][HALF], s_sn[4][HALF];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = blockIdx.x * 4 + w;
+  if (row < M) rope_angles((float)pos[row], inv_freq, HALF, s_cs[w], s_sn[w], lane);
+  __syncthreads();
+  if (row >= M) return;
+  const int hh = lane / LPH, c0 = (lane % LPH) * EPL;
+  const int j0 = c0 % HALF;
+  const float sgn = c0 < HALF ? -1.f : 1.f;
+  float cv[EPL], sv[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) { cv[e] = s_cs[w][j0 + e]; sv[e] = s_sn[w][j0 + e]; }
   const int nh = nq + nk;
-  if (item >= (int64_t)M * nh) return;
-  const int row = (int)(item / nh), hd = (int)(item % nh);
-  const bool isq = hd < nq;
-  const T* src = qkv + (int64_t)row * ld + (int64_t)hd * d;
-  T* dst = isq ? qo + ((int64_t)row * nq + hd) * d : ko + ((int64_t)row * nk + (hd - nq)) * d;
-  const T* w = isq ? wq : wk;
-  const int half = d >> 1;
-  float x0[2], x1[2];
-  float ss = 0.f;
+  const bool norm = wq != nullptr;
+  for (int hb = 0; hb < nh; hb += HPW) {
+    const int head = hb + hh;
+    const bool valid = head < nh;
+    const bool isq = head < nq;
+    float x[EPL];
+    if (valid) Vec16<T>::load(qkv + (int64_t)row * ld + (int64_t)head * D + c0, x);
+    else {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int i = lane + 64 * t;
-    x0[t] = x1[t] = 0.f;
-    if (i < half) {
-      x0[t] = Elem<T>::load(src + i);
-      x1[t] = Elem<T>::load(src + i + half);
-      ss += x0[t] * x0[t] + x1[t] * x1[t];
+      for (int e = 0; e < EPL; ++e) x[e] = 0.f;
     }
-  }
-  float r = 1.f;
-  if (w) {
-    ss = wave_sum(ss);
-    r = rsqrtf(ss / (float)d + eps);
-    if (lane == 0) rstd[(int64_t)row * nh + hd] = r;
-  }
-  const float p = (float)pos[row];
+    if (norm) {
+      float ss = 0.f;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int i = lane + 64 * t;
-    if (i < half) {
-      float n0 = x0[t], n1 = x1[t];
-      if (w) {
-        n0 = Elem<T>::round(Elem<T>::round(n0 * r) * Elem<T>::load(w + i));
-        n1 = Elem<T>::round(Elem<T>::round(n1 * r) * Elem<T>::load(w + i + half));
-      }
-      float s, c;
-      sincosf(p * inv_freq[i], &s, &c);
-      Elem<T>::store(dst + i, n0 * c - n1 * s);
-      Elem<T>::store(dst + i + half, n1 * c + n0 * s);
+      for (int e = 0; e < EPL; ++e) ss += x[e] * x[e];
+#pragma unroll
+      for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      const float r = rsqrtf(ss / (float)D + eps);
+      if (valid && lane % LPH == 0) rstd[(int64_t)row * nh + head] = r;
+      float wv[EPL];
+      if (valid) Vec16<T>::load((isq ? wq : wk) + c0, wv);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) x[e] = valid ? Elem<T>::round(Elem<T>::round(x[e] * r) * wv[e]) : 0.f;
+    }
+    float out[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const float y = __shfl_xor(x[e], LPH / 2, 64);   // partner element i +- d/2
+      out[e] = x[e] * cv[e] + sgn * y * sv[e];
+    }
+    if (valid) {
+      T* dst = isq ? qo + ((int64_t)row * nq + head) * D : ko + ((int64_t)row * nk + (head - nq)) * D;
+      Vec16<T>::store(dst + c0, out);
     }
   }
 }
 
-template <typename T>
+template <typename T, int D>
 __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk,
                                                               const T* __restrict__ qkv, int64_t ld, const T* wq,
                                                               const T* wk, const int64_t* __restrict__ pos,
                                                               const float* __restrict__ inv_freq,
                                                               const float* __restrict__ rstd, T* __restrict__ dqkv,
-                                                              int64_t ldd, int M, int nq, int nk, int d) {
-  const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+                                                              int64_t ldd, int M, int nq, int nk) {
+  constexpr int EPL = Vec16<T>::N, LPH = D / EPL, HPW = 64 / LPH, HALF = D / 2;
+  static_assert(LPH >= 2 && LPH <= 64 && 64 % LPH == 0, "head geometry");
+  __shared__ float s_cs[4][HALF], s_sn[4][HALF];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = blockIdx.x * 4 + w;
+  if (row < M) rope_angles((float)pos[row], inv_freq, HALF, s_cs[w], s_sn[w], lane);
+  __syncthreads();
+  if (row >= M) return;
+  const int hh = lane / LPH, c0 = (lane % LPH) * EPL;
+  const int j0 = c0 % HALF;
+  // inverse rotation: dn_i = dy_i c + dy_{i+h} s (first half), dn_i = dy_i c - dy_{i-h} s (second)
+  const float sgn = c0 < HALF ? 1.f : -1.f;
+  float cv[EPL], sv[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) { cv[e] = s_cs[w][j0 + e]; sv[e] = s_sn[w][j0 + e]; }
   const int nh = nq + nk;
-  if (item >= (int64_t)M * nh) return;
-  const int row = (int)(item / nh), hd = (int)(item % nh);
-  const bool isq = hd < nq;
-  const T* dy = isq ? dq + ((int64_t)row * nq + hd) * d : dk + ((int64_t)row * nk + (hd - nq)) * d;
-  const T* src = qkv + (int64_t)row * ld + (int64_t)hd * d;
-  T* out = dqkv + (int64_t)row * ldd + (int64_t)hd * d;
-  const T* w = isq ? wq : wk;
-  const int half = d >> 1;
-  const float p = (float)pos[row];
-  const float r = w ? rstd[(int64_t)row * nh + hd] : 1.f;
-  float g0[2], g1[2], xh0[2], xh1[2];
-  float dot = 0.f;
+  const bool norm = wq != nullptr;
+  for (int hb = 0; hb < nh; hb += HPW) {
+    const int head = hb + hh;
+    const bool valid = head < nh;
+    const bool isq = head < nq;
+    float dy[EPL];
+    if (valid) Vec16<T>::load(isq ? dq + ((int64_t)row * nq + head) * D + c0 : dk + ((int64_t)row * nk + (head - nq)) * D + c0, dy);
+    else {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int i = lane + 64 * t;
-    g0[t] = g1[t] = xh0[t] = xh1[t] = 0.f;
-    if (i < half) {
-      const float dy0 = Elem<T>::load(dy + i), dy1 = Elem<T>::load(dy + i + half);
-      float s, c;
-      sincosf(p * inv_freq[i], &s, &c);
-      const float dn0 = dy0 * c + dy1 * s;
-      const float dn1 = dy1 * c - dy0 * s;
-      if (w) {
-        xh0[t] = Elem<T>::load(src + i) * r;
-        xh1[t] = Elem<T>::load(src + i + half) * r;
-        g0[t] = dn0 * Elem<T>::load(w + i);
-        g1[t] = dn1 * Elem<T>::load(w + i + half);
-        dot += g0[t] * xh0[t] + g1[t] * xh1[t];
-      } else {
-        g0[t] = dn0;
-        g1[t] = dn1;
-      }
+      for (int e = 0; e < EPL; ++e) dy[e] = 0.f;
     }
-  }
-  if (w) dot = wave_sum(dot) / (float)d;
+    float g[EPL];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int i = lane + 64 * t;
-    if (i < half) {
-      if (w) {
-        Elem<T>::store(out + i, r * (g0[t] - xh0[t] * dot));
-        Elem<T>::store(out + i + half, r * (g1[t] - xh1[t] * dot));
-      } else {
-        Elem<T>::store(out + i, g0[t]);
-        Elem<T>::store(out + i + half, g1[t]);
-      }
+    for (int e = 0; e < EPL; ++e) {
+      const float y = __shfl_xor(dy[e], LPH / 2, 64);
+      g[e] = dy[e] * cv[e] + sgn * y * sv[e];
     }
+    if (norm) {
+      const float r = valid ? rstd[(int64_t)row * nh + head] : 0.f;
+      float x[EPL], wv[EPL];
+      if (valid) {
+        Vec16<T>::load(qkv + (int64_t)row * ld + (int64_t)head * D + c0, x);
+        Vec16<T>::load((isq ? wq : wk) + c0, wv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) { x[e] = 0.f; wv[e] = 0.f; }
+      }
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        x[e] *= r;            // x-hat
+        g[e] *= wv[e];
+        dot += g[e] * x[e];
+      }
+#pragma unroll
+      for (int o = LPH / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+      dot /= (float)D;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) g[e] = r * (g[e] - x[e] * dot);
+    }
+    if (valid) Vec16<T>::store(dqkv + (int64_t)row * ldd + (int64_t)head * D + c0, g);
   }
 }
 
@@ -377,14 +426,20 @@ UNOK_EXPORT int unok_qknorm_rope_fwd(int dtype, int M, int nq, int nk, int d, co
                                      const void* wq, const void* wk, const int64_t* pos, const float* inv_freq,
                                      float eps, void* q_out, void* k_out, float* rstd, void* stream) {
   if (M == 0) return 0;
-  UNOK_REQUIRE(d % 2 == 0 && d <= 256 && nq > 0 && nk >= 0, UNOK_EINVAL, "qknorm_rope: bad head geometry d=%d", d);
+  UNOK_REQUIRE((d == 64 || d == 128) && nq > 0 && nk >= 0, UNOK_EINVAL, "qknorm_rope: head dim %d not in {64,128}", d);
   UNOK_REQUIRE((wq == nullptr) == (wk == nullptr), UNOK_EINVAL, "qknorm_rope: q and k norms must both be given");
-  const int64_t items = (int64_t)M * (nq + nk);
-  const int blocks = (int)((items + 3) / 4);
+  UNOK_REQUIRE(ld % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)q_out & 15) == 0 && ((uintptr_t)k_out & 15) == 0,
+               UNOK_EALIGN, "qknorm_rope: rows must be 16-byte aligned");
+  const int blocks = (M + 3) / 4;
   hipStream_t st = (hipStream_t)stream;
-  DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_fwd_kernel<T>), dim3(blocks), dim3(256), 0, st, (const T*)qkv, ld,
-                                       (const T*)wq, (const T*)wk, pos, inv_freq, (T*)q_out, (T*)k_out, rstd, M, nq,
-                                       nk, d, eps));
+  if (d == 128)
+    DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_fwd_kernel<T, 128>), dim3(blocks), dim3(256), 0, st, (const T*)qkv,
+                                         ld, (const T*)wq, (const T*)wk, pos, inv_freq, (T*)q_out, (T*)k_out, rstd, M,
+                                         nq, nk, eps));
+  else
+    DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_fwd_kernel<T, 64>), dim3(blocks), dim3(256), 0, st, (const T*)qkv,
+                                         ld, (const T*)wq, (const T*)wk, pos, inv_freq, (T*)q_out, (T*)k_out, rstd, M,
+                                         nq, nk, eps));
   return unok::check_launch("qknorm_rope_fwd");
 }
 
@@ -393,13 +448,20 @@ UNOK_EXPORT int unok_qknorm_rope_bwd(int dtype, int M, int nq, int nk, int d, co
                                      const float* inv_freq, const float* rstd, void* dqkv, int64_t ldd,
                                      void* stream) {
   if (M == 0) return 0;
-  UNOK_REQUIRE(d % 2 == 0 && d <= 256, UNOK_EINVAL, "qknorm_rope_bwd: bad head dim %d", d);
-  const int64_t items = (int64_t)M * (nq + nk);
-  const int blocks = (int)((items + 3) / 4);
+  UNOK_REQUIRE(d == 64 || d == 128, UNOK_EINVAL, "qknorm_rope_bwd: head dim %d not in {64,128}", d);
+  UNOK_REQUIRE(ld % 8 == 0 && ldd % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)dqkv & 15) == 0 &&
+                   ((uintptr_t)dq & 15) == 0 && ((uintptr_t)dk & 15) == 0,
+               UNOK_EALIGN, "qknorm_rope_bwd: rows must be 16-byte aligned");
+  const int blocks = (M + 3) / 4;
   hipStream_t st = (hipStream_t)stream;
-  DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<T>), dim3(blocks), dim3(256), 0, st, (const T*)dq,
-                                       (const T*)dk, (const T*)qkv, ld, (const T*)wq, (const T*)wk, pos, inv_freq, rstd,
-                                       (T*)dqkv, ldd, M, nq, nk, d));
+  if (d == 128)
+    DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<T, 128>), dim3(blocks), dim3(256), 0, st, (const T*)dq,
+                                         (const T*)dk, (const T*)qkv, ld, (const T*)wq, (const T*)wk, pos, inv_freq, rstd,
+                                         (T*)dqkv, ldd, M, nq, nk));
+  else
+    DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<T, 64>), dim3(blocks), dim3(256), 0, st, (const T*)dq,
+                                         (const T*)dk, (const T*)qkv, ld, (const T*)wq, (const T*)wk, pos, inv_freq, rstd,
+                                         (T*)dqkv, ldd, M, nq, nk));
   return unok::check_launch("qknorm_rope_bwd");
 }
 

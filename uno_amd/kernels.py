@@ -42,7 +42,7 @@ def nt_uses_256_tiles(M: int, N: int, seg_end) -> bool:
         return False
     if any(e % 256 for e in list(seg_end)[:-1]):
         return False
-    return ((M + 255) // 256) * ((N + 255) // 256) >= 512
+    return ((M + 255) // 256) * ((N + 255) // 256) >= 256
 
 
 def _rowmajor(t: torch.Tensor, name: str) -> None:
