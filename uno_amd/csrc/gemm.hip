@@ -389,9 +389,9 @@ __device__ __forceinline__ void store4(float* dst, const float* res, const float
 }
 
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int SG_MFMA = 0x008, SG_DS_READ = 0x100;
+constexpr int SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
 
-template <int BK, int STAGES, typename OutT>
+template <int BK, int STAGES, typename OutT, bool SPREAD>
 __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
   constexpr int BM = 256, BN = 256, NW = 4;
   constexpr int TM = 4, TN = 4;
@@ -401,6 +401,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
   constexpr int INS = BM / (RPI * NW);          // load instructions per wave per operand
   constexpr int LPT = 2 * INS;                  // loads per wave per tile
   static_assert(KS % 2 == 0 && STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * LPT < 64, "bad config");
+  static_assert(!SPREAD || (STAGES == 2 && BK == 64), "the spread schedule is written for 2 stages of BK 64");
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   bf16_t* As = smem;                            // [STAGES][BM*BK]
   bf16_t* Bs = smem + STAGES * BM * BK;         // [STAGES][BN*BK]
@@ -477,10 +478,12 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
     const bf16_t* as = As + buf * BM * BK + a_row0;
     const bf16_t* bs = Bs + buf * BN * BK + b_row0;
     const int co = ((ks * 2 + lg) ^ sw) << 3;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[i] = *(const bf16x8_t*)&as[i * 32 * BK + co];
+    // Read in the order the next step's MFMAs consume them: fa[0], all of fb, then fa[1..3].
+    fa[0] = *(const bf16x8_t*)&as[co];
 #pragma unroll
     for (int j = 0; j < TN; ++j) fb[j] = *(const bf16x8_t*)&bs[j * 32 * BK + co];
+#pragma unroll
+    for (int i = 1; i < TM; ++i) fa[i] = *(const bf16x8_t*)&as[i * 32 * BK + co];
   };
 
   f32x16_t acc[TM][TN];
@@ -501,28 +504,39 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
       for (int j = 0; j < TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
   };
-  // 8 fragment reads spread over the first 8 of 16 MFMAs, then the remaining 8 MFMAs.
+  // 8 fragment reads spread evenly over the 16 MFMAs (one per two), so the four waves' reads
+  // keep the LDS at about half its bandwidth instead of saturating it for half of each step (a
+  // read stalled in a full LDS queue blocks the in-order issue of the MFMAs behind it).
   auto interleave = [&]() {
+    if constexpr (SPREAD) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      for (int k = 0; k < 8; ++k) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
   };
 
+  // All STAGES stages are filled up front; afterwards the stage of tile kt is refilled with tile
+  // kt + STAGES right after the barrier that ends its reads, so every load has a full tile of
+  // MFMA work per stage ahead of it to land.
 #pragma unroll
-  for (int t = 0; t < STAGES - 1; ++t)
+  for (int t = 0; t < STAGES; ++t)
     if (t < nk) issue(t, t);
-  wait_tile(min(nk - 1, STAGES - 2));
+  wait_tile(min(nk - 1, STAGES - 1));
   asm volatile("s_barrier" ::: "memory");
   load_frags(fa0, fb0, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt % STAGES;
-    const int ahead = kt + STAGES - 1;
     const bool more = kt + 1 < nk;
-    // The stage of tile `ahead` held tile kt-1, whose reads ended before the last barrier.
-    if (ahead < nk) issue(ahead, ahead % STAGES);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks + 1 < KS; ++ks) {
@@ -532,15 +546,61 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
     }
     __builtin_amdgcn_sched_barrier(0);
     // Every read of stage `cur` by this wave has been issued and has returned; once each wave is
-    // here with its loads of tile kt+1 landed, tile kt+1 is complete in LDS.
-    wait_tile(min(nk - 1, ahead) - (kt + 1));
+    // here with its loads of tile kt+1 landed, tile kt+1 is complete in LDS. Tiles up to
+    // kt + STAGES - 1 have been issued so far.
+    wait_tile(min(nk - 1, kt + STAGES - 1) - (kt + 1));
     asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    if (more) load_frags(fa0, fb0, (kt + 1) % STAGES, 0);
-    mfmas(fa1, fb1);
-    if (more) interleave();
+    if constexpr (SPREAD) {
+      // Last step of the tile, in a fixed instruction order: each of the 16 MFMAs is followed by
+      // one direct-to-LDS load of tile kt + STAGES (clamped to the last tile, so the sequence has
+      // no branches; the stage of a clamped tile is never read again), and every second one by a
+      // fragment read of tile kt + 1 (in the order the next step consumes them). A burst of 16
+      // loads would fill the load queue and stall the in-order issue of the MFMAs behind it.
+      const int nt = min(kt + STAGES, nk - 1);
+      if (nt == nk1) {
+        ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0), (uint32_t)(((int64_t)(p.M - 1) * p.lda2 + p.K2) * 2));
+        rb = make_rsrc(p.B2, (uint32_t)(((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2));
+        set_offsets(p.lda2, p.ldb2);
+        kbase = nk1;
+      }
+      bf16_t* as = As + cur * BM * BK + wid * RPI * BK;
+      bf16_t* bs = Bs + cur * BN * BK + wid * RPI * BK;
+      const uint32_t kb = (uint32_t)(nt - kbase) * BK * 2;
+      const int nb = (kt + 1) % STAGES;
+      const bf16_t* fas = As + nb * BM * BK + a_row0;
+      const bf16_t* fbs = Bs + nb * BN * BK + b_row0;
+      const int co = (lg ^ sw) << 3;
+      static_assert(2 * INS == TM * TN, "one load per MFMA");
+#pragma unroll
+      for (int idx = 0; idx < TM * TN; ++idx) {
+        const int i = idx / TN, j = idx % TN;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb1[j], fa1[i], acc[i][j], 0, 0, 0);
+        if (idx < INS) buf_lds16(ra, a_vo[idx], kb, as + idx * NW * RPI * BK);
+        else buf_lds16(rb, b_vo[idx - INS], kb, bs + (idx - INS) * NW * RPI * BK);
+        if (idx % 2 == 0) {
+          const int r = idx / 2;   // 0: fa[0]; 1..4: fb[0..3]; 5..7: fa[1..3]
+          if (r == 0) fa0[0] = *(const bf16x8_t*)&fas[co];
+          else if (r <= TN) fb0[r - 1] = *(const bf16x8_t*)&fbs[(r - 1) * 32 * BK + co];
+          else fa0[r - TN] = *(const bf16x8_t*)&fas[(r - TN) * 32 * BK + co];
+        }
+      }
+#pragma unroll
+      for (int idx = 0; idx < TM * TN; ++idx) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
+        if (idx % 2 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      }
+    } else {
+      if (kt + STAGES < nk) issue(kt + STAGES, cur);
+      if (more) load_frags(fa0, fb0, (kt + 1) % STAGES, 0);
+      mfmas(fa1, fb1);
+      if (more) interleave();
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
+  // Clamped loads of the last tiles may still be in flight: they write LDS.
+  if constexpr (SPREAD) __builtin_amdgcn_s_waitcnt(0x0070);
 
   // Epilogue: 4 consecutive columns per lane and row -> one 8-byte (bf16) / 16-byte (fp32)
   // store, residual read the same way. Columns come in groups of 4 (N % 4 == 0 on the host).
@@ -963,11 +1023,12 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 //   0: 8 waves, BK 64, 2 stages   1: 8 waves, BK 32, 4 stages   2: 8 waves, BK 32, 5 stages
 //   3: 4 waves, BK 32, 4 stages   4: 4 waves, BK 64, 2 stages
 //   5/6/7: 4 waves of 128x128, VGPR double-buffered fragments; BK 64 x 2 stages / BK 32 x 4 / BK 32 x 5
+//   8: as 5, with the next tiles' loads issued as one burst and fragment reads bunched per step
 static int dma_cfg() {
   static int c = [] {
     const char* e = getenv("UNOK_GEMM_CFG");
     const int v = e ? atoi(e) : 5;
-    return (v >= 0 && v <= 7) ? v : 5;
+    return (v >= 0 && v <= 8) ? v : 5;
   }();
   return c;
 }
@@ -983,17 +1044,17 @@ static bool buffer_ranges_ok(const GemmNT& p) {
   return true;
 }
 
-template <int BK, int STAGES, typename OutT>
+template <int BK, int STAGES, typename OutT, bool SPREAD = true>
 static void launch_nt_w4(const GemmNT& p, hipStream_t st) {
   constexpr size_t lds = (size_t)STAGES * (256 + 256) * BK * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4_kernel<BK, STAGES, OutT>,
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SPREAD>,
                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
   const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  hipLaunchKernelGGL((gemm_nt_bf16_w4_kernel<BK, STAGES, OutT>), dim3(nb), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SPREAD>), dim3(nb), dim3(256), lds, st, p);
 }
 
 template <int BM, int BN, int NW, int BK, int STAGES, typename OutT>
@@ -1019,10 +1080,12 @@ static void launch_nt_dma_o(const GemmNT& p, hipStream_t st) {
     case 5:
     case 6:
     case 7:
+    case 8:
       if (!buffer_ranges_ok(p)) { launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break; }
       if (dma_cfg() == 5) launch_nt_w4<64, 2, OutT>(p, st);
-      else if (dma_cfg() == 6) launch_nt_w4<32, 4, OutT>(p, st);
-      else launch_nt_w4<32, 5, OutT>(p, st);
+      else if (dma_cfg() == 8) launch_nt_w4<64, 2, OutT, false>(p, st);
+      else if (dma_cfg() == 6) launch_nt_w4<32, 4, OutT, false>(p, st);
+      else launch_nt_w4<32, 5, OutT, false>(p, st);
       break;
     default: launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break;
   }
