@@ -391,7 +391,7 @@ __device__ __forceinline__ void store4(float* dst, const float* res, const float
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
 
-template <int BK, int STAGES, typename OutT, bool SPREAD>
+template <int BK, int STAGES, typename OutT, int SCHED>
 __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
   constexpr int BM = 256, BN = 256, NW = 4;
   constexpr int TM = 4, TN = 4;
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
   constexpr int INS = BM / (RPI * NW);          // load instructions per wave per operand
   constexpr int LPT = 2 * INS;                  // loads per wave per tile
   static_assert(KS % 2 == 0 && STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * LPT < 64, "bad config");
-  static_assert(!SPREAD || (STAGES == 2 && BK == 64), "the spread schedule is written for 2 stages of BK 64");
+  static_assert(SCHED == 0 || (STAGES == 2 && BK == 64), "the explicit schedules are written for 2 stages of BK 64");
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   bf16_t* As = smem;                            // [STAGES][BM*BK]
   bf16_t* Bs = smem + STAGES * BM * BK;         // [STAGES][BN*BK]
@@ -504,103 +504,141 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
       for (int j = 0; j < TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
   };
-  // 8 fragment reads spread evenly over the 16 MFMAs (one per two), so the four waves' reads
-  // keep the LDS at about half its bandwidth instead of saturating it for half of each step (a
-  // read stalled in a full LDS queue blocks the in-order issue of the MFMAs behind it).
+  // 8 fragment reads spread over the first 8 of 16 MFMAs, then the remaining 8 MFMAs.
   auto interleave = [&]() {
-    if constexpr (SPREAD) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
+    for (int k = 0; k < 8; ++k) {
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
   };
 
-  // All STAGES stages are filled up front; afterwards the stage of tile kt is refilled with tile
-  // kt + STAGES right after the barrier that ends its reads, so every load has a full tile of
-  // MFMA work per stage ahead of it to land.
-#pragma unroll
-  for (int t = 0; t < STAGES; ++t)
-    if (t < nk) issue(t, t);
-  wait_tile(min(nk - 1, STAGES - 1));
-  asm volatile("s_barrier" ::: "memory");
-  load_frags(fa0, fb0, 0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt % STAGES;
-    const bool more = kt + 1 < nk;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int ks = 0; ks + 1 < KS; ++ks) {
-      if (ks % 2 == 0) { load_frags(fa1, fb1, cur, ks + 1); mfmas(fa0, fb0); }
-      else { load_frags(fa0, fb0, cur, ks + 1); mfmas(fa1, fb1); }
-      interleave();
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // Every read of stage `cur` by this wave has been issued and has returned; once each wave is
-    // here with its loads of tile kt+1 landed, tile kt+1 is complete in LDS. Tiles up to
-    // kt + STAGES - 1 have been issued so far.
-    wait_tile(min(nk - 1, kt + STAGES - 1) - (kt + 1));
+  if constexpr (SCHED == 0) {
+    // All STAGES stages are filled up front; afterwards the stage of tile kt is refilled with tile
+    // kt + STAGES right after the barrier that ends its reads, so every load has a full tile of
+    // MFMA work per stage ahead of it to land.
+  #pragma unroll
+    for (int t = 0; t < STAGES; ++t)
+      if (t < nk) issue(t, t);
+    wait_tile(min(nk - 1, STAGES - 1));
     asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (SPREAD) {
-      // Last step of the tile, in a fixed instruction order: each of the 16 MFMAs is followed by
-      // one direct-to-LDS load of tile kt + STAGES (clamped to the last tile, so the sequence has
-      // no branches; the stage of a clamped tile is never read again), and every second one by a
-      // fragment read of tile kt + 1 (in the order the next step consumes them). A burst of 16
-      // loads would fill the load queue and stall the in-order issue of the MFMAs behind it.
-      const int nt = min(kt + STAGES, nk - 1);
-      if (nt == nk1) {
-        ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0), (uint32_t)(((int64_t)(p.M - 1) * p.lda2 + p.K2) * 2));
-        rb = make_rsrc(p.B2, (uint32_t)(((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2));
-        set_offsets(p.lda2, p.ldb2);
-        kbase = nk1;
+    load_frags(fa0, fb0, 0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt % STAGES;
+      const bool more = kt + 1 < nk;
+      __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+      for (int ks = 0; ks + 1 < KS; ++ks) {
+        if (ks % 2 == 0) { load_frags(fa1, fb1, cur, ks + 1); mfmas(fa0, fb0); }
+        else { load_frags(fa0, fb0, cur, ks + 1); mfmas(fa1, fb1); }
+        interleave();
       }
-      bf16_t* as = As + cur * BM * BK + wid * RPI * BK;
-      bf16_t* bs = Bs + cur * BN * BK + wid * RPI * BK;
-      const uint32_t kb = (uint32_t)(nt - kbase) * BK * 2;
-      const int nb = (kt + 1) % STAGES;
-      const bf16_t* fas = As + nb * BM * BK + a_row0;
-      const bf16_t* fbs = Bs + nb * BN * BK + b_row0;
-      const int co = (lg ^ sw) << 3;
-      static_assert(2 * INS == TM * TN, "one load per MFMA");
+      __builtin_amdgcn_sched_barrier(0);
+      // Every read of stage `cur` by this wave has been issued and has returned; once each wave is
+      // here with its loads of tile kt+1 landed, tile kt+1 is complete in LDS. Tiles up to
+      // kt + STAGES - 1 have been issued so far.
+      wait_tile(min(nk - 1, kt + STAGES - 1) - (kt + 1));
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + STAGES < nk) issue(kt + STAGES, cur);
+      if (more) load_frags(fa0, fb0, (kt + 1) % STAGES, 0);
+      mfmas(fa1, fb1);
+      if (more) interleave();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    // Fixed instruction order per step: 16 MFMAs; after every second one a fragment read for the
+    // next step (in the order that step consumes them: fa[0], fb[0..3], fa[1..3]); and the
+    // direct-to-LDS loads of the tile two ahead spread evenly over the step(s) that issue them
+    // (SCHED 1: all 16 in step 3; SCHED 2: its A half in step 3, its B half in step 0 of the next
+    // tile). A burst of loads fills the load queue and stalls the in-order issue of the MFMAs
+    // behind it. Tiles past the end are clamped to the last one, so the instruction stream has
+    // no branches; a clamped tile lands in a stage that is never read again.
+    const int co0 = lg ^ sw;
+    auto step = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[TN], bf16x8_t (&na)[TM], bf16x8_t (&nb)[TN],
+                    int rstage, int rks, auto dma_n, int dma_lo, uint32_t kb, int dstage) {
+      constexpr int ND = decltype(dma_n)::value;
+      constexpr int EVERY = ND ? TM * TN / ND : 1;
+      const bf16_t* fas = As + rstage * BM * BK + a_row0;
+      const bf16_t* fbs = Bs + rstage * BN * BK + b_row0;
+      const int co = ((rks * 2) ^ co0) << 3;    // chunk (2 rks + lg) ^ sw
+      bf16_t* das = As + dstage * BM * BK + wid * RPI * BK;
+      bf16_t* dbs = Bs + dstage * BN * BK + wid * RPI * BK;
 #pragma unroll
       for (int idx = 0; idx < TM * TN; ++idx) {
         const int i = idx / TN, j = idx % TN;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb1[j], fa1[i], acc[i][j], 0, 0, 0);
-        if (idx < INS) buf_lds16(ra, a_vo[idx], kb, as + idx * NW * RPI * BK);
-        else buf_lds16(rb, b_vo[idx - INS], kb, bs + (idx - INS) * NW * RPI * BK);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+        if (ND && idx % EVERY == 0) {
+          const int n = dma_lo + idx / EVERY;
+          if (n < INS) buf_lds16(ra, a_vo[n], kb, das + n * NW * RPI * BK);
+          else buf_lds16(rb, b_vo[n - INS], kb, dbs + (n - INS) * NW * RPI * BK);
+        }
         if (idx % 2 == 0) {
-          const int r = idx / 2;   // 0: fa[0]; 1..4: fb[0..3]; 5..7: fa[1..3]
-          if (r == 0) fa0[0] = *(const bf16x8_t*)&fas[co];
-          else if (r <= TN) fb0[r - 1] = *(const bf16x8_t*)&fbs[(r - 1) * 32 * BK + co];
-          else fa0[r - TN] = *(const bf16x8_t*)&fas[(r - TN) * 32 * BK + co];
+          const int r = idx / 2;
+          if (r == 0) na[0] = *(const bf16x8_t*)&fas[co];
+          else if (r <= TN) nb[r - 1] = *(const bf16x8_t*)&fbs[(r - 1) * 32 * BK + co];
+          else na[r - TN] = *(const bf16x8_t*)&fas[(r - TN) * 32 * BK + co];
         }
       }
 #pragma unroll
       for (int idx = 0; idx < TM * TN; ++idx) {
         __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
+        if (ND && idx % EVERY == 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
         if (idx % 2 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
       }
-    } else {
-      if (kt + STAGES < nk) issue(kt + STAGES, cur);
-      if (more) load_frags(fa0, fb0, (kt + 1) % STAGES, 0);
-      mfmas(fa1, fb1);
-      if (more) interleave();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // Sets up the operand pair of tile t (switching to the LoRA pair at tile nk1; tiles are set
+    // up in order) and returns its k byte offset.
+    auto dma_tile = [&](int t) -> uint32_t {
+      if (t == nk1) {
+        ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0), (uint32_t)(((int64_t)(p.M - 1) * p.lda2 + p.K2) * 2));
+        rb = make_rsrc(p.B2, (uint32_t)(((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2));
+        set_offsets(p.lda2, p.ldb2);
+        kbase = nk1;
+      }
+      return (uint32_t)(t - kbase) * BK * 2;
+    };
+    using D0 = std::integral_constant<int, 0>;
+    using DH = std::integral_constant<int, INS>;
+    using DF = std::integral_constant<int, 2 * INS>;
+
+    // Prologue: tile 0 whole, tile 1 (clamped) whole (SCHED 1) or its A half (SCHED 2).
+    issue(0, 0);
+    uint32_t kb_next = dma_tile(min(1, nk - 1));
+    {
+      bf16_t* as = As + 1 * BM * BK + wid * RPI * BK;
+      bf16_t* bs = Bs + 1 * BN * BK + wid * RPI * BK;
+#pragma unroll
+      for (int i = 0; i < INS; ++i) buf_lds16(ra, a_vo[i], kb_next, as + i * NW * RPI * BK);
+      if constexpr (SCHED == 1) {
+#pragma unroll
+        for (int i = 0; i < INS; ++i) buf_lds16(rb, b_vo[i], kb_next, bs + i * NW * RPI * BK);
+      }
     }
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (SCHED == 1) wait_vm<2 * INS>(); else wait_vm<INS>();   // tile 0 landed
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("s_barrier" ::: "memory");
+    load_frags(fa0, fb0, 0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1, nxt = cur ^ 1;
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (SCHED == 2) step(fa0, fb0, fa1, fb1, cur, 1, DH{}, INS, kb_next, nxt);  // B half of tile kt+1
+      else step(fa0, fb0, fa1, fb1, cur, 1, D0{}, 0, 0u, 0);
+      step(fa1, fb1, fa0, fb0, cur, 2, D0{}, 0, 0u, 0);
+      step(fa0, fb0, fa1, fb1, cur, 3, D0{}, 0, 0u, 0);
+      // Tile kt+1 is complete once every wave is here with all its loads landed (nothing after
+      // tile kt+1 has been issued yet) and its reads of stage cur returned.
+      __builtin_amdgcn_s_waitcnt(0x0070);
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      kb_next = dma_tile(min(kt + 2, nk - 1));
+      if constexpr (SCHED == 2) step(fa1, fb1, fa0, fb0, nxt, 0, DH{}, 0, kb_next, cur);   // A half of tile kt+2
+      else step(fa1, fb1, fa0, fb0, nxt, 0, DF{}, 0, kb_next, cur);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);       // clamped loads still write LDS
   }
-  // Clamped loads of the last tiles may still be in flight: they write LDS.
-  if constexpr (SPREAD) __builtin_amdgcn_s_waitcnt(0x0070);
 
   // Epilogue: 4 consecutive columns per lane and row -> one 8-byte (bf16) / 16-byte (fp32)
   // store, residual read the same way. Columns come in groups of 4 (N % 4 == 0 on the host).
@@ -1023,12 +1061,14 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 //   0: 8 waves, BK 64, 2 stages   1: 8 waves, BK 32, 4 stages   2: 8 waves, BK 32, 5 stages
 //   3: 4 waves, BK 32, 4 stages   4: 4 waves, BK 64, 2 stages
 //   5/6/7: 4 waves of 128x128, VGPR double-buffered fragments; BK 64 x 2 stages / BK 32 x 4 / BK 32 x 5
+//      (5: each tile's direct-to-LDS loads spread over two MFMA steps, A half then B half)
 //   8: as 5, with the next tiles' loads issued as one burst and fragment reads bunched per step
+//   9: as 5, with all 16 loads of a tile spread over one MFMA step
 static int dma_cfg() {
   static int c = [] {
     const char* e = getenv("UNOK_GEMM_CFG");
     const int v = e ? atoi(e) : 5;
-    return (v >= 0 && v <= 8) ? v : 5;
+    return (v >= 0 && v <= 9) ? v : 5;
   }();
   return c;
 }
@@ -1044,17 +1084,17 @@ static bool buffer_ranges_ok(const GemmNT& p) {
   return true;
 }
 
-template <int BK, int STAGES, typename OutT, bool SPREAD = true>
+template <int BK, int STAGES, typename OutT, int SCHED>
 static void launch_nt_w4(const GemmNT& p, hipStream_t st) {
   constexpr size_t lds = (size_t)STAGES * (256 + 256) * BK * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SPREAD>,
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SCHED>,
                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
   const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  hipLaunchKernelGGL((gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SPREAD>), dim3(nb), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SCHED>), dim3(nb), dim3(256), lds, st, p);
 }
 
 template <int BM, int BN, int NW, int BK, int STAGES, typename OutT>
@@ -1081,11 +1121,13 @@ static void launch_nt_dma_o(const GemmNT& p, hipStream_t st) {
     case 6:
     case 7:
     case 8:
+    case 9:
       if (!buffer_ranges_ok(p)) { launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break; }
-      if (dma_cfg() == 5) launch_nt_w4<64, 2, OutT>(p, st);
-      else if (dma_cfg() == 8) launch_nt_w4<64, 2, OutT, false>(p, st);
-      else if (dma_cfg() == 6) launch_nt_w4<32, 4, OutT, false>(p, st);
-      else launch_nt_w4<32, 5, OutT, false>(p, st);
+      if (dma_cfg() == 5) launch_nt_w4<64, 2, OutT, 2>(p, st);
+      else if (dma_cfg() == 8) launch_nt_w4<64, 2, OutT, 0>(p, st);
+      else if (dma_cfg() == 9) launch_nt_w4<64, 2, OutT, 1>(p, st);
+      else if (dma_cfg() == 6) launch_nt_w4<32, 4, OutT, 0>(p, st);
+      else launch_nt_w4<32, 5, OutT, 0>(p, st);
       break;
     default: launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break;
   }
