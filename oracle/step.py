@@ -68,15 +68,20 @@ def compute_loss(params, lora, cfg: Cfg, batch: dict, objective: Objective, *, b
 
 def train_steps(params, lora, cfg: Cfg, batch: dict, objective: Objective, *, block_size: int,
                 mask_token_id: int, seed: int, steps: int, lr: float = 1e-4, first_step: int = 0,
-                max_grad_norm: float = 1.0):
-    """Runs `steps` optimizer steps; returns (losses, first-step grads, final lora)."""
+                max_grad_norm: float = 1.0, block_sizes: list[int] | None = None):
+    """Runs `steps` optimizer steps; returns (losses, first-step grads, final lora).
+
+    `block_sizes[s]`, when given, is the block size of step s (a curriculum that switches block
+    size between optimizer steps, training/trainer.py:182-184 with training/curriculum.py:109-112);
+    otherwise every step uses `block_size`."""
     leaves = {k: v.detach().clone().float().requires_grad_(True) for k, v in lora.items()}
     opt = torch.optim.AdamW(list(leaves.values()), lr=lr, betas=(0.9, 0.999), eps=1e-8,
                             weight_decay=0.0)
     hist, first_grads = [], None
     for s in range(steps):
         opt.zero_grad(set_to_none=True)
-        loss, _ = compute_loss(params, leaves, cfg, batch, objective, block_size=block_size,
+        bs = block_sizes[s] if block_sizes is not None else block_size
+        loss, _ = compute_loss(params, leaves, cfg, batch, objective, block_size=bs,
                                mask_token_id=mask_token_id, seed=seed, step=first_step + s)
         loss.backward()
         if first_grads is None:

@@ -1,0 +1,223 @@
+"""Step-level parity of the HIP path with the oracle for the other workload configurations.
+
+Each case keeps the feature that distinguishes a configuration and shrinks the widths so the
+fp32 oracle finishes in seconds:
+
+* rank-32 adapters with alpha 64 and block 8 (the ~1B configuration: 16 q / 8 kv heads, d 128);
+* multi-head attention (kv heads = q heads) without q/k-norm, alpha = 16 r (the reference's
+  default, training/config.py:67-69), with the curriculum switching block size 4 -> 8 -> 16 -> 32
+  on successive optimizer steps over the same batch (training/trainer.py:182-184,
+  training/curriculum.py:109-112);
+* one packed row of several segments (position_ids restarting at 0, 10% prompt per segment,
+  training/modeling.py:47-98) with block 32.
+
+fp32 runs compare loss and LoRA gradients tightly (1e-5 / 2e-4 relative) or, over several
+optimizer steps, the per-step losses and final adapters; bf16 runs use the same bar as the
+headline-shape step test: loss within 1e-3, gradient cosine >= 0.999 and per-tensor relative L2
+within max(1e-2, 1.1 x the oracle's own bf16-arithmetic error)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import step as ostep
+from oracle.model import Cfg, init_lora, init_params
+from uno_amd.model import UnoQwen3Config, UnoQwen3ForCausalLM
+from uno_amd.training.config import LoraSettings, UnoObjectiveConfig
+from uno_amd.training.curriculum import BlockCurriculumPlan
+from uno_amd.training.lora import create_lora_model
+from uno_amd.training.trainer import UnoTrainer, UnoTrainingArguments
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20260813
+CE = (UnoObjectiveConfig(ce_target="ground_truth", ce_weight=1.0, kl_weight=0.0, tv_weight=0.0),
+      ostep.Objective(1, 0, 0, "data"))
+TV = (UnoObjectiveConfig(ce_weight=0.0, kl_weight=0.0, tv_weight=1.0), ostep.Objective(0, 0, 1))
+
+# rank 32 / alpha 64 / block 8, GQA 2:1, head dim 128
+RANK32 = dict(vocab_size=8192, hidden_size=512, intermediate_size=1408, num_hidden_layers=2, num_attention_heads=4,
+              num_key_value_heads=2, head_dim=128, qk_norm=True, rank=32, alpha=64, B=2, L=512, prompt=64)
+# MHA, no q/k-norm, alpha = 16 r
+MHA = dict(vocab_size=4096, hidden_size=256, intermediate_size=704, num_hidden_layers=2, num_attention_heads=4,
+           num_key_value_heads=4, head_dim=64, qk_norm=False, rank=8, alpha=128, B=2, L=256, prompt=32)
+MHA128 = dict(MHA, hidden_size=512, intermediate_size=1408, head_dim=128, vocab_size=8192)
+# one packed row
+PACKED = dict(vocab_size=4096, hidden_size=256, intermediate_size=768, num_hidden_layers=2, num_attention_heads=4,
+              num_key_value_heads=2, head_dim=64, qk_norm=True, rank=8, alpha=16, B=1, L=512)
+PACKED128 = dict(PACKED, hidden_size=512, intermediate_size=1408, head_dim=128, vocab_size=8192)
+SEGMENTS = [150, 97, 201, 64]          # sums to 512; lengths not multiples of the block size
+
+
+def _plan(blocks, L, B):
+    tps = L * B
+    return BlockCurriculumPlan.from_dict({"tokens_per_step": tps, "sequence_length": L, "global_batch_size": B,
+                                          "seed": 0, "stages": [{"block_size": b, "tokens": tps} for b in blocks]})
+
+
+def _setup(spec, dtype, dev, objective, blocks, seed=0):
+    ocfg = Cfg(spec["vocab_size"], spec["hidden_size"], spec["intermediate_size"], spec["num_hidden_layers"],
+               spec["num_attention_heads"], spec["num_key_value_heads"], spec["head_dim"], qk_norm=spec["qk_norm"],
+               lora_rank=spec["rank"], lora_alpha=spec["alpha"])
+    params = init_params(ocfg, seed=seed)
+    if dtype == torch.bfloat16:
+        params = {k: v.bfloat16().float() for k, v in params.items()}
+    lora = init_lora(ocfg, seed=seed + 1)
+    ucfg = UnoQwen3Config(vocab_size=ocfg.vocab_size, hidden_size=ocfg.hidden_size,
+                          intermediate_size=ocfg.intermediate_size, num_hidden_layers=ocfg.num_hidden_layers,
+                          num_attention_heads=ocfg.num_attention_heads, num_key_value_heads=ocfg.num_key_value_heads,
+                          head_dim=ocfg.head_dim, qk_norm=spec["qk_norm"], block_size=blocks[0])
+    model = UnoQwen3ForCausalLM(ucfg, device=dev, dtype=dtype)
+    model.load_weights(params)
+    lm, _ = create_lora_model(model, LoraSettings("all", spec["rank"], spec["alpha"], 0.0))
+    lm.load_lora(lora)
+    trainer = UnoTrainer(model=lm, objective=objective, curriculum=_plan(blocks, spec["L"], spec["B"]),
+                         args=UnoTrainingArguments(learning_rate=1e-4))
+    return ocfg, params, lora, lm, trainer
+
+
+def _batch(spec, seed=2, segments=None):
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, spec["vocab_size"] - 1, (spec["B"], spec["L"]), generator=g)
+    labels = ids.clone()
+    batch = {"input_ids": ids, "labels": labels, "attention_mask": torch.ones_like(ids)}
+    if segments is None:
+        labels[:, :spec["prompt"]] = -100
+        return batch
+    assert spec["B"] == 1 and sum(segments) == spec["L"]
+    pos, start = [], 0
+    for n in segments:
+        pos.append(torch.arange(n))
+        labels[0, start:start + max(1, n // 10)] = -100        # 10% prompt per segment
+        start += n
+    batch["position_ids"] = torch.cat(pos).unsqueeze(0)
+    return batch
+
+
+def _to(batch, dev):
+    return {k: v.to(dev) for k, v in batch.items()}
+
+
+def _my_grads(lm):
+    return {n.replace("base_model.model.", "", 1): p.grad for n, p in lm.lora_tensors().items()}
+
+
+def _fp32_one_step(dev, spec, objective, block, segments=None, tol=2e-4):
+    mine_obj, ref_obj = objective
+    ocfg, params, lora, lm, trainer = _setup(spec, torch.float32, dev, mine_obj, [block])
+    batch = _batch(spec, segments=segments)
+    leaves = {k: v.clone().requires_grad_(True) for k, v in lora.items()}
+    ref_loss, _ = ostep.compute_loss(params, leaves, ocfg, batch, ref_obj, block_size=block,
+                                     mask_token_id=ocfg.vocab_size - 1, seed=SEED, step=0)
+    ref_loss.backward()
+    loss = trainer.compute_loss(lm, _to(batch, dev))
+    loss.backward()
+    torch.cuda.synchronize()
+    lrel = abs(loss.item() - ref_loss.item()) / abs(ref_loss.item())
+    mine = _my_grads(lm)
+    worst = max(((mine[k].cpu() - v.grad).norm() / v.grad.norm().clamp_min(1e-30)).item() for k, v in leaves.items())
+    print(f"   loss {loss.item():.6f} vs {ref_loss.item():.6f} (rel {lrel:.2e}); worst grad rel L2 {worst:.2e}",
+          flush=True)
+    assert lrel < 1e-5
+    assert worst < tol
+
+
+def _grad_errors(grads, ref):
+    out = {}
+    for k, v in ref.items():
+        a = grads[k].float().cpu()
+        out[k] = (F.cosine_similarity(a.flatten(), v.flatten(), dim=0).item(), ((a - v).norm() / v.norm()).item())
+    return out
+
+
+def _bf16_one_step(dev, spec, objective, block, segments=None):
+    mine_obj, ref_obj = objective
+    ocfg, params, lora, lm, trainer = _setup(spec, torch.bfloat16, dev, mine_obj, [block])
+    batch = _batch(spec, segments=segments)
+    kw = dict(block_size=block, mask_token_id=ocfg.vocab_size - 1, seed=SEED, step=0)
+    leaves = {k: v.clone().requires_grad_(True) for k, v in lora.items()}
+    ref_loss, _ = ostep.compute_loss(params, leaves, ocfg, batch, ref_obj, **kw)
+    ref_loss.backward()
+    ref = {k: v.grad for k, v in leaves.items()}
+    leaves16 = {k: v.clone().requires_grad_(True) for k, v in lora.items()}
+    loss16, _ = ostep.compute_loss({k: v.bfloat16() for k, v in params.items()}, leaves16, ocfg, batch, ref_obj, **kw)
+    loss16.backward()
+    loss = trainer.compute_loss(lm, _to(batch, dev))
+    loss.backward()
+    torch.cuda.synchronize()
+    lrel = abs(loss.item() - ref_loss.item()) / abs(ref_loss.item())
+    mine = _grad_errors(_my_grads(lm), ref)
+    theirs = _grad_errors({k: v.grad for k, v in leaves16.items()}, ref)
+    worst_cos = min(c for c, _ in mine.values())
+    print(f"   bf16 loss rel {lrel:.2e}; worst grad cos {worst_cos:.5f}; worst rel L2 "
+          f"{max(r for _, r in mine.values()):.3e} (bf16 reference arithmetic "
+          f"{max(r for _, r in theirs.values()):.3e})", flush=True)
+    assert lrel < 1e-3
+    assert worst_cos >= 0.999
+    for k, (c, r) in mine.items():
+        assert r <= max(1e-2, 1.1 * theirs[k][1]), (k, r, theirs[k][1])
+
+
+# --- rank 32 / alpha 64 / block 8 ---------------------------------------------------------------
+
+def test_rank32_fp32_step(dev):
+    print("[configs] rank 32, alpha 64, block 8, fp32", flush=True)
+    _fp32_one_step(dev, RANK32, CE, 8)
+
+
+def test_rank32_bf16_step(dev):
+    print("[configs] rank 32, alpha 64, block 8, bf16", flush=True)
+    _bf16_one_step(dev, RANK32, CE, 8)
+
+
+# --- MHA without q/k-norm, block-size sweep ------------------------------------------------------
+
+@pytest.mark.parametrize("block", [4, 8, 16, 32])
+def test_mha_no_qknorm_fp32_step(dev, block):
+    print(f"[configs] MHA, no qk-norm, alpha 16r, block {block}, fp32", flush=True)
+    _fp32_one_step(dev, MHA, CE, block)
+
+
+def test_mha_no_qknorm_bf16_step_d128(dev):
+    print("[configs] MHA, no qk-norm, d 128, block 16, bf16", flush=True)
+    _bf16_one_step(dev, MHA128, CE, 16)
+
+
+def test_block_sweep_curriculum_four_steps(dev):
+    """Four optimizer steps on one batch while the curriculum moves block 4 -> 8 -> 16 -> 32."""
+    blocks = [4, 8, 16, 32]
+    print(f"[configs] MHA, no qk-norm, curriculum blocks {blocks}, fp32", flush=True)
+    mine_obj, ref_obj = CE
+    ocfg, params, lora, lm, trainer = _setup(MHA, torch.float32, dev, mine_obj, blocks)
+    batch = _batch(MHA)
+    hist, _, final = ostep.train_steps(params, lora, ocfg, batch, ref_obj, block_size=blocks[0],
+                                       mask_token_id=ocfg.vocab_size - 1, seed=SEED, steps=len(blocks),
+                                       lr=1e-4, block_sizes=blocks)
+    gb = _to(batch, dev)
+    losses = []
+    for s in range(len(blocks)):
+        losses.append(trainer.train_step(gb).item())
+        assert lm.get_base_model().config.block_size == blocks[s]
+    torch.cuda.synchronize()
+    print(f"   losses {losses} vs oracle {hist}", flush=True)
+    for a, b in zip(losses, hist):
+        assert abs(a - b) / abs(b) < 1e-4, (losses, hist)
+    mine = {n.replace("base_model.model.", "", 1): p.detach().cpu() for n, p in lm.lora_tensors().items()}
+    worst = max(((mine[k] - v).norm() / v.norm()).item() for k, v in final.items())
+    assert worst < 1e-3, worst
+
+
+# --- one packed row of several segments, block 32 ------------------------------------------------
+
+def test_packed_segments_fp32_step(dev):
+    print(f"[configs] packed row {SEGMENTS}, block 32, fp32", flush=True)
+    _fp32_one_step(dev, PACKED, CE, 32, segments=SEGMENTS)
+
+
+def test_packed_segments_tv_fp32_step(dev):
+    print(f"[configs] packed row {SEGMENTS}, block 32, TV objective, fp32", flush=True)
+    _fp32_one_step(dev, PACKED, TV, 32, segments=SEGMENTS, tol=2e-3)
+
+
+def test_packed_segments_bf16_step_d128(dev):
+    print(f"[configs] packed row {SEGMENTS}, block 32, d 128, bf16", flush=True)
+    _bf16_one_step(dev, PACKED128, CE, 32, segments=SEGMENTS)
