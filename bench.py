@@ -30,8 +30,47 @@ QWEN3_8B = dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288, nu
                 num_attention_heads=32, num_key_value_heads=8, head_dim=128)
 WORKLOAD = dict(batch=4, seq_len=4096, prompt=512, block_size=16, lora_rank=64, lora_alpha=128)
 
+# The headline workload and three further ones (--workload), each a (model, batch) pair:
+#   qwen3_8b     Qwen3-8B shape, 4 x 4096 tokens, block 16, rank 64 / alpha 128 (the headline)
+#   dense_1b     16 layers, hidden 2048, 16 q / 8 kv heads, FFN 5632, 8 x 2048 tokens, block 8, rank 32 / alpha 64
+#   mha_7b       32 layers, hidden 4096, 32 q = 32 kv heads, FFN 11008, vocab 32000, no q/k-norm,
+#                4 x 4096 tokens, rank 64 / alpha 1024, curriculum block 4 -> 8 -> 16 -> 32 across the timed steps
+#   packed_16k   Qwen3-8B shape, one row of 16384 tokens packed from log-normal segment lengths
+#                (median 3000, sigma 0.6, clipped to [512, 16384]; 10% prompt per segment), block 32
+WORKLOADS = {
+    "qwen3_8b": (QWEN3_8B, WORKLOAD),
+    "dense_1b": (dict(vocab_size=151936, hidden_size=2048, intermediate_size=5632, num_hidden_layers=16,
+                      num_attention_heads=16, num_key_value_heads=8, head_dim=128),
+                 dict(batch=8, seq_len=2048, prompt=256, block_size=8, lora_rank=32, lora_alpha=64)),
+    "mha_7b": (dict(vocab_size=32000, hidden_size=4096, intermediate_size=11008, num_hidden_layers=32,
+                    num_attention_heads=32, num_key_value_heads=32, head_dim=128, qk_norm=False),
+               dict(batch=4, seq_len=4096, prompt=512, block_size=4, block_sweep=[4, 8, 16, 32], lora_rank=64,
+                    lora_alpha=1024)),
+    "packed_16k": (QWEN3_8B, dict(batch=1, seq_len=16384, packed=True, block_size=32, lora_rank=64, lora_alpha=128)),
+}
 
-def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813):
+
+WORKLOAD_NAMES = {
+    "qwen3_8b": "Qwen3-8B-shape cond-LoRA block-diffusion step (config 3)",
+    "dense_1b": "1B-class (16 layers, hidden 2048, 16q/8kv) cond-LoRA step, rank 32 (config 2)",
+    "mha_7b": "7B MHA (no q/k-norm, vocab 32000) cond-LoRA step, block curriculum 4/8/16/32 (config 4)",
+    "packed_16k": "Qwen3-8B-shape step on one 16384-token row of packed segments, block 32 (config 5)",
+}
+
+
+def packed_segments(total: int, seed: int) -> list[int]:
+    """Log-normal segment lengths (median 3000, sigma 0.6, clipped to [512, total]) filling one row."""
+    g = torch.Generator().manual_seed(seed)
+    out, left = [], total
+    while left > 0:
+        n = int(torch.exp(torch.randn((), generator=g) * 0.6 + torch.log(torch.tensor(3000.0))).item())
+        n = min(max(n, 512), total, left)
+        out.append(n)
+        left -= n
+    return out
+
+
+def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813, total_steps: int = 10 ** 6):
     from uno_amd.model import UnoQwen3Config, UnoQwen3ForCausalLM
     from uno_amd.training.config import LoraSettings, UnoObjectiveConfig
     from uno_amd.training.curriculum import BlockCurriculumPlan
@@ -42,16 +81,35 @@ def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813):
     model = UnoQwen3ForCausalLM(cfg, device=device, dtype=torch.bfloat16)
     model.random_init(seed, std=0.02)
     lm, _ = create_lora_model(model, LoraSettings("all", wl["lora_rank"], wl["lora_alpha"], 0.0), seed=seed + 1)
+    B, L = wl["batch"], wl["seq_len"]
+    if "block_sweep" in wl:
+        # stage i of the sweep covers steps_per_stage optimizer steps (the first stage also the warm-up)
+        tps, sweep = B * L, wl["block_sweep"]
+        per = wl["steps_per_stage"]
+        stages = [{"block_size": b, "tokens": tps * (per + (wl["warmup"] if i == 0 else 0))}
+                  for i, b in enumerate(sweep)]
+        plan = BlockCurriculumPlan.from_dict({"tokens_per_step": tps, "sequence_length": L, "global_batch_size": B,
+                                              "seed": 0, "stages": stages})
+    else:
+        plan = BlockCurriculumPlan.fixed(wl["block_size"], total_steps, L, B)
     trainer = UnoTrainer(model=lm, objective=UnoObjectiveConfig(ce_target="ground_truth", ce_weight=1.0,
                                                                  kl_weight=0.0, tv_weight=0.0),
-                         curriculum=BlockCurriculumPlan.fixed(wl["block_size"], 10 ** 6, wl["seq_len"], wl["batch"]),
-                         args=UnoTrainingArguments(learning_rate=1e-4))
+                         curriculum=plan, args=UnoTrainingArguments(learning_rate=1e-4))
     g = torch.Generator(device=device).manual_seed(seed + 2)
-    B, L = wl["batch"], wl["seq_len"]
     ids = torch.randint(0, cfg.vocab_size - 1, (B, L), device=device, generator=g)
     labels = ids.clone()
-    labels[:, :wl["prompt"]] = -100
     batch = {"input_ids": ids, "labels": labels, "attention_mask": torch.ones_like(ids)}
+    if wl.get("packed"):
+        segs = packed_segments(L, seed + 3)
+        pos, start = [], 0
+        for n in segs:
+            pos.append(torch.arange(n))
+            labels[:, start:start + n // 10] = -100
+            start += n
+        batch["position_ids"] = torch.cat(pos).unsqueeze(0).expand(B, -1).contiguous().to(device)
+        wl["segments"] = segs
+    else:
+        labels[:, :wl["prompt"]] = -100
     return model, lm, trainer, batch
 
 
@@ -154,8 +212,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--layers", type=int, default=QWEN3_8B["num_hidden_layers"],
-                    help="decoder layers (the reported workload uses all 36)")
+    ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS),
+                    help="qwen3_8b is the headline; the others measure further model/batch shapes")
+    ap.add_argument("--layers", type=int, default=None,
+                    help="decoder layers (default: the workload's full depth)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -171,7 +231,11 @@ def main() -> int:
         return 2
     from uno_amd import kernels as K
 
-    cfg = dict(QWEN3_8B, num_hidden_layers=args.layers)
+    base_cfg, wl = WORKLOADS[args.workload]
+    wl = dict(wl, warmup=args.warmup, steps_per_stage=max(1, args.steps // 4))
+    if args.layers is None:
+        args.layers = base_cfg["num_hidden_layers"]
+    cfg = dict(base_cfg, num_hidden_layers=args.layers)
     dev = "cuda:0"
     if args.calibrate_copy:
         src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
@@ -180,23 +244,30 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    model, lm, trainer, batch = build_step(cfg, WORKLOAD, dev)
+    model, lm, trainer, batch = build_step(cfg, wl, dev)
     print(f"[bench] model built: {args.layers} layers; warmup {args.warmup} steps", file=sys.stderr, flush=True)
     for i in range(args.warmup):
         trainer.train_step(batch)
         torch.cuda.synchronize()
         print(f"[bench] warmup step {i} done", file=sys.stderr, flush=True)
 
-    # realised counts of one step for the FLOP accounting
+    # realised counts for the FLOP accounting, per block size of the timed steps
+    from uno_amd.training.losses import shift_labels_for_next_token
     from uno_amd.training.modeling import prepare_uno_layout
     base = lm.get_base_model()
-    pos, mpos, _ = prepare_uno_layout(base, batch["input_ids"], None)
-    _, _, mask, noised, _, _ = base.prepare_for_bd_training(batch["input_ids"], mpos, batch["labels"] == -100,
-                                                            step=10 ** 6)
-    from uno_amd.training.losses import shift_labels_for_next_token
-    shifted = shift_labels_for_next_token(batch["labels"], pos)
-    ce_rows = int((noised & (shifted != -100)).sum())
-    flops = algorithmic_flops(cfg, WORKLOAD, mask, ce_rows, WORKLOAD["lora_rank"])
+    plan = trainer.curriculum
+    blocks = [plan.stage_for_step(min(trainer.state.global_step + i, plan.max_steps - 1)).block_size
+              for i in range(args.steps)]
+    per_block = {}
+    for b in sorted(set(blocks)):
+        base.config.block_size = b
+        pos, mpos, _ = prepare_uno_layout(base, batch["input_ids"], batch.get("position_ids"))
+        _, _, mask, noised, _, _ = base.prepare_for_bd_training(batch["input_ids"], mpos, batch["labels"] == -100,
+                                                                step=10 ** 6)
+        shifted = shift_labels_for_next_token(batch["labels"], pos)
+        ce_rows = int((noised & (shifted != -100)).sum())
+        per_block[b] = algorithmic_flops(cfg, wl, mask, ce_rows, wl["lora_rank"])
+    flops = {k: sum(per_block[b][k] for b in blocks) / len(blocks) for k in per_block[blocks[0]]}
 
     rec = K.LaunchRecorder(lambda dt, M, N, Kd, K2, segs: dt == torch.bfloat16 and K.nt_uses_256_tiles(M, N, segs))
     torch.cuda.synchronize()
@@ -209,28 +280,35 @@ def main() -> int:
     K.set_recorder(None)
     ms_step = (t1 - t0) * 1000.0 / args.steps
     ms, fl = rec.elapsed()
-    tokens = WORKLOAD["batch"] * WORKLOAD["seq_len"]
+    tokens = wl["batch"] * wl["seq_len"]
     value = tokens / (ms_step / 1000.0)
     mfu = flops["total"] / (ms_step / 1000.0) / (PEAK_BF16_TFLOPS * 1e12)
     gemm_ms = sum(ms) / max(len(ms), 1)
     gemm_tflops = (sum(fl) / max(len(fl), 1)) / (gemm_ms / 1000.0) / 1e12 if ms else 0.0
     out = {
-        "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC if args.workload == "qwen3_8b" else
+        f"train tokens/s/GPU, {args.workload} cond-LoRA step; % bf16 MFMA peak",
+        "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 2), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (uniform token ids, random N(0,0.02) weights)",
-        "config": {"workload": "Qwen3-8B-shape cond-LoRA block-diffusion step (config 3)",
-                   "layers": args.layers, "global_batch": WORKLOAD["batch"], "seq_len": WORKLOAD["seq_len"],
-                   "block_size": WORKLOAD["block_size"], "lora_rank": WORKLOAD["lora_rank"],
+        "config": {"workload": WORKLOAD_NAMES[args.workload],
+                   "layers": args.layers, "global_batch": wl["batch"], "seq_len": wl["seq_len"],
+                   "block_size": blocks[0] if len(set(blocks)) == 1 else blocks,
+                   "lora_rank": wl["lora_rank"], "lora_alpha": wl["lora_alpha"],
                    "objective": "CE (data targets, 1/t weights)", "parallelism": "single GPU"},
         "mfu": round(mfu, 4), "algorithmic_tflop_per_step": round(flops["total"] / 1e12, 2),
         "flops_breakdown_tflop": {k: round(v / 1e12, 2) for k, v in flops.items() if k != "total"},
         "roofline": {"kernel": "gemm_nt_bf16_w4_kernel<64,2,*,2> (256x256 tiles; fused LoRA linears, LM head)",
                      "bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": measured_traffic(),
+                     "traffic": measured_traffic() if args.workload == "qwen3_8b" else None,
                      "launches": len(ms), "mean_launch_ms": round(gemm_ms, 4)},
     }
-    if not args.no_cpu_baseline:
+    if wl.get("segments"):
+        out["config"]["segments"] = wl["segments"]
+    if args.workload != "qwen3_8b":
+        out["cpu_baseline"] = None            # the CPU oracle is timed on the headline workload only
+    elif not args.no_cpu_baseline:
         print("[bench] timing CPU baseline", file=sys.stderr, flush=True)
         del model, lm, trainer, batch
         torch.cuda.empty_cache()
