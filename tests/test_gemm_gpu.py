@@ -61,6 +61,22 @@ def test_gemm_nt_direct_to_lds_path(dev, M, N, Kd):
     assert _rel(out, a.float() @ b.float().T) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,Kd", [(16384, 64, 4096), (16384, 128, 1024), (16384, 192, 4096),
+                                    (8237, 64, 12288), (4096, 100, 512), (5000, 160, 640)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gemm_nt_skinny_path(dev, M, N, Kd, out_dtype):
+    """Skinny products (N <= 192, M >= 4096, K a multiple of 64): one 64-row tile spans all N
+    columns. Ragged M and N, a row gate and alpha, bf16 and fp32 outputs."""
+    torch.manual_seed(M + N + Kd)
+    a = torch.randn(M, Kd, device=dev).bfloat16()
+    b = torch.randn(N, Kd, device=dev).bfloat16()
+    gate = torch.rand(M, device=dev) > 0.3
+    out = K.gemm_nt(a, b, gate=gate, alpha=0.75, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    ref = 0.75 * (a.float() @ b.float().T) * gate.float()[:, None]
+    assert _rel(out, ref) < (1e-5 if out_dtype == torch.float32 else 5e-3)
+
+
 def test_gemm_nt_direct_to_lds_lora_residual(dev):
     """q|k|v-shaped fused product on the direct-to-LDS kernel: three 256-aligned segments with
     their LoRA K-extension (K2 = 64), residual, alpha, bf16 output."""

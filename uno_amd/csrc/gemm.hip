@@ -1133,6 +1133,24 @@ static void launch_nt_dma_o(const GemmNT& p, hipStream_t st) {
   }
 }
 
+template <int BM, int BN, int NW, int BK, int STAGES>
+static void launch_nt_dma_o2(const GemmNT& p, int out_dtype, hipStream_t st) {
+  if (out_dtype == UNOK_F32) launch_nt_dma_t<BM, BN, NW, BK, STAGES, float>(p, st);
+  else launch_nt_dma_t<BM, BN, NW, BK, STAGES, bf16_t>(p, st);
+}
+
+// Skinny NT path (N <= 192): 1 = 64xN tiles with 4 LDS stages for N <= 128 and 3 for N <= 192
+// (default), 2 = 2 stages, 3 = 4 stages, 4 = 5 stages, 0 = off
+// (register-staged 128x64 / 128x128 tiles). UNOK_SKINNY_CFG selects one, for tuning.
+static int skinny_cfg() {
+  static int c = [] {
+    const char* e = getenv("UNOK_SKINNY_CFG");
+    const int v = e ? atoi(e) : 1;
+    return (v >= 0 && v <= 4) ? v : 1;
+  }();
+  return c;
+}
+
 static void launch_nt_dma(const GemmNT& p, int out_dtype, hipStream_t st) {
   if (out_dtype == UNOK_F32) launch_nt_dma_o<float>(p, st); else launch_nt_dma_o<bf16_t>(p, st);
 }
@@ -1191,7 +1209,29 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
     return true;
   };
   const long long big_tiles = (long long)((M + 255) / 256) * ((N + 255) / 256);
-  if (N <= 64 || !segs_ok(128)) {
+  const int sk = skinny_cfg();
+  if (sk > 0 && N <= 192 && !p.A2 && K % 64 == 0 && M >= 4096) {
+    // Skinny products (LoRA x·Aᵀ and dY·B, N = r .. 3r): one 64-row tile spans all N columns, so
+    // every activation row is read from HBM once; 4 waves, direct-to-LDS loads, 3-4 stages.
+    const int bn = (N + 63) / 64 * 64;
+    if (sk == 1) {
+      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 4>(p, out_dtype, st);
+      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 4>(p, out_dtype, st);
+      else launch_nt_dma_o2<64, 192, 4, 64, 3>(p, out_dtype, st);
+    } else if (sk == 3) {
+      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 4>(p, out_dtype, st);
+      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 4>(p, out_dtype, st);
+      else launch_nt_dma_o2<64, 192, 4, 64, 4>(p, out_dtype, st);
+    } else if (sk == 4) {
+      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 5>(p, out_dtype, st);
+      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 5>(p, out_dtype, st);
+      else launch_nt_dma_o2<64, 192, 4, 64, 5>(p, out_dtype, st);
+    } else {
+      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 2>(p, out_dtype, st);
+      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 2>(p, out_dtype, st);
+      else launch_nt_dma_o2<64, 192, 4, 64, 2>(p, out_dtype, st);
+    }
+  } else if (N <= 64 || !segs_ok(128)) {
     UNOK_REQUIRE(segs_ok(64), UNOK_EINVAL, "gemm_nt(bf16): segment ends must be multiples of 64");
     launch_nt_bf16<128, 64>(p, out_dtype, st);
   } else if (N <= 128 || !segs_ok(256) || big_tiles < 256) {
