@@ -234,10 +234,18 @@ __device__ __forceinline__ void dma_tile(const bf16_t* src, int64_t ld, int col0
   constexpr int CPR = D / 8, RPI = 64 / CPR, INS = 64 / (RPI * NW);
   static_assert(INS >= 1, "tile too small for the wave count");
   const int rl = lane / CPR, slot = lane % CPR;
-  const int nrows = max(0, min(kend - k0, 64));
+  // The tile's source, start row and row count are workgroup-uniform; reading them through
+  // readfirstlane keeps the buffer resource in SGPRs (a resource the compiler cannot prove
+  // uniform is issued through a per-load waterfall loop).
+  const int nrows = __builtin_amdgcn_readfirstlane(max(0, min(kend - k0, 64)));
+  const uintptr_t base = (uintptr_t)(src + (int64_t)k0 * ld);
+  const uintptr_t ubase = ((uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32)) << 32) |
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  const int64_t uld = ((int64_t)__builtin_amdgcn_readfirstlane((int)(ld >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ld);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<bf16_t*>(src + (int64_t)k0 * ld), (short)0, (int)((int64_t)nrows * ld * 2), 0x00020000);
-  const uint32_t ldb = (uint32_t)ld * 2;
+      (void*)ubase, (short)0, (int)((int64_t)nrows * uld * 2), 0x00020000);
+  const uint32_t ldb = (uint32_t)uld * 2;
 #pragma unroll
   for (int i = 0; i < INS; ++i) {
     const int r = (i * NW + wid) * RPI + rl;
