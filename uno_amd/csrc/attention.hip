@@ -303,11 +303,14 @@ __device__ __forceinline__ Bounds merge_bounds(const Bounds& a, const Bounds& b)
 template <int D, int QG>
 __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(const AttnArgs p) {
   constexpr int BK = ATT_BK, NKS = D / 16, NDT = D / 32, BQ = 128 * QG;
-  // Dynamic LDS: K tiles [2][64*D] (direct-to-LDS double buffer), V rows [64*D], V^T [D][72].
+  // Dynamic LDS: K tiles [2][64*D] (direct-to-LDS double buffer) and V rows [64*D]. V^T [D][72]
+  // is a separate static array: as a distinct object the compiler can tell that reading it does
+  // not depend on the direct-to-LDS loads of the next tile still in flight (with one shared array
+  // it waits for those loads before the first V^T read of every tile).
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  __shared__ __attribute__((aligned(16))) bf16_t Vt[D * ATT_TS];
   bf16_t* Ks = smem;
   bf16_t* Vr = smem + 2 * BK * D;
-  bf16_t* Vt = Vr + BK * D;
   __shared__ int sh[8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
   const int nqt = (p.Mq + BQ - 1) / BQ;
@@ -962,7 +965,7 @@ static int attn_qg() {
 
 template <int D, int QG>
 static void launch_fwd_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
-  constexpr size_t lds = (3 * ATT_BK * D + D * ATT_TS) * sizeof(bf16_t);
+  constexpr size_t lds = 3 * ATT_BK * D * sizeof(bf16_t);   // + the static V^T array
   static bool configured = false;
   if (!configured) {
     hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<D, QG>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
