@@ -72,67 +72,18 @@ __device__ __forceinline__ int wave_max_i(int v) {
   return v;
 }
 
-// Register staging of a [64 rows x D] tile: global loads into four flat uint4 registers
-// (issued early so they overlap the current tile's math), then row-major and/or transposed LDS
-// stores. Flat locals (rather than an array or struct) keep the staging in VGPRs under this
-// kernel's register pressure. D = 128 uses all four registers per thread, D = 64 the first two.
-__device__ __forceinline__ uint4 tile_ld(const bf16_t* __restrict__ src, int64_t ld, int col0, int r0, int rend, int i,
-                                         int cpr) {
-  const int c = threadIdx.x + 256 * i, r = c / cpr, dc = (c % cpr) * 8;
-  // Rows past rend re-read the last valid row: their scores are masked (p = 0) and the data is
-  // finite, so no zero fill (and no divergent branch) is needed.
-  const int row = min(r0 + r, rend - 1);
-  return *(const uint4*)(src + (int64_t)row * ld + col0 + dc);
-}
-
-__device__ __forceinline__ void tile_st_row(uint4 v, bf16_t* dst, int rs, int i, int cpr) {
-  const int c = threadIdx.x + 256 * i, r = c / cpr, dc = (c % cpr) * 8;
-  *(uint4*)&dst[r * rs + dc] = v;
-}
-
-__device__ __forceinline__ void tile_st_trans(uint4 v, bf16_t* dst, int ts, int i, int cpr) {
-  const int c = threadIdx.x + 256 * i, r = c / cpr, dc = (c % cpr) * 8;
-  bf16_t* col = dst + dc * ts + r;
-  col[0 * ts] = (bf16_t)(v.x & 0xffffu);
-  col[1 * ts] = (bf16_t)(v.x >> 16);
-  col[2 * ts] = (bf16_t)(v.y & 0xffffu);
-  col[3 * ts] = (bf16_t)(v.y >> 16);
-  col[4 * ts] = (bf16_t)(v.z & 0xffffu);
-  col[5 * ts] = (bf16_t)(v.z >> 16);
-  col[6 * ts] = (bf16_t)(v.w & 0xffffu);
-  col[7 * ts] = (bf16_t)(v.w >> 16);
-}
-
-#define UNOK_TILE_LOAD(pfx, src, ld, col0, r0, rend)                         \
-  do {                                                                       \
-    pfx##0 = tile_ld(src, ld, col0, r0, rend, 0, D / 8);                     \
-    pfx##1 = tile_ld(src, ld, col0, r0, rend, 1, D / 8);                     \
-    if constexpr (D == 128) {                                                \
-      pfx##2 = tile_ld(src, ld, col0, r0, rend, 2, D / 8);                   \
-      pfx##3 = tile_ld(src, ld, col0, r0, rend, 3, D / 8);                   \
-    }                                                                        \
-  } while (0)
-#define UNOK_TILE_STORE(fn, pfx, dst, stride)                                \
-  do {                                                                       \
-    fn(pfx##0, dst, stride, 0, D / 8);                                       \
-    fn(pfx##1, dst, stride, 1, D / 8);                                       \
-    if constexpr (D == 128) {                                                \
-      fn(pfx##2, dst, stride, 2, D / 8);                                     \
-      fn(pfx##3, dst, stride, 3, D / 8);                                     \
-    }                                                                        \
-  } while (0)
-
 // Interval bounds reduced over a workgroup's 4 waves. Empty intervals are ignored.
 struct Bounds { int lo, hi, maxlo, minhi; };
 
 __device__ __forceinline__ Bounds wave_bounds(bool valid, int lo, int hi) {
   const bool use = valid && lo < hi;
+  // Wave-wide reductions, so uniform: readfirstlane lets the tile tests branch on scalars.
   Bounds b;
-  b.lo = wave_min_i(use ? lo : INT_MAX);
-  b.hi = wave_max_i(use ? hi : INT_MIN);
+  b.lo = __builtin_amdgcn_readfirstlane(wave_min_i(use ? lo : INT_MAX));
+  b.hi = __builtin_amdgcn_readfirstlane(wave_max_i(use ? hi : INT_MIN));
   // for the "whole tile visible" test every valid query counts (an empty one forces the mask)
-  b.maxlo = wave_max_i(valid ? lo : INT_MIN);
-  b.minhi = wave_min_i(valid ? (lo < hi ? hi : INT_MIN) : INT_MAX);
+  b.maxlo = __builtin_amdgcn_readfirstlane(wave_max_i(valid ? lo : INT_MIN));
+  b.minhi = __builtin_amdgcn_readfirstlane(wave_min_i(valid ? (lo < hi ? hi : INT_MIN) : INT_MAX));
   return b;
 }
 
@@ -148,82 +99,68 @@ __device__ __forceinline__ int2 wg_bounds(const Bounds& w, int* sh) {
 }
 
 // ---------------------------------------------------------------------------------------
-// K/V tile staging for the 64-query-per-wave kernels. A 64-key tile is loaded into registers
-// one tile ahead; threads [0, 128) own V (or K for the dQ transposed copy) as 8-key x 8-dim
-// blocks, which they transpose in registers and store as 16-byte rows of a [D][keys] LDS tile;
-// threads [128, 256) own row-major 16-byte chunks. The transposed tile has 72-element rows and
-// its 16-byte key group kg of dim row d sits at slot kg ^ ((d >> 4) & 7), which keeps both the
-// transposed stores and the P.V operand reads on distinct banks.
+// Transposed [D][keys] LDS tiles (K for dQ, Q and dO for dK/dV) have 72-element rows; the
+// 16-byte chunk kg of dim row d sits at slot kg ^ ((d >> 4) & 7), which keeps both the
+// transposed stores and the MFMA operand reads on distinct banks.
 // ---------------------------------------------------------------------------------------
 constexpr int ATT_BK = 64;     // keys per tile
 constexpr int ATT_TS = 72;     // transposed tile row pitch (elements)
 
 __device__ __forceinline__ int tslot(int d, int kg) { return kg ^ ((d >> 4) & 7); }
 
-template <int D>
-struct TileStage {
-  static constexpr int CPR = D / 8;            // 16-byte chunks per key row
-  static constexpr int TBLK = 8 * CPR;         // 8x8 blocks of the transposed operand (<= 128)
-  static constexpr int RPT = 64 * CPR / 128;   // row-major chunks per thread of [128, 256)
-  uint4 st[8];
-  // Transposed role (tid < TBLK): block (key group tid / CPR, dim group tid % CPR).
-  __device__ __forceinline__ void load_t(const bf16_t* src, int64_t ld, int col0, int k0, int kend, int tid) {
-    const int kg = tid / CPR, dg = tid % CPR;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = min(k0 + kg * 8 + i, kend - 1);
-      st[i] = *(const uint4*)(src + (int64_t)row * ld + col0 + dg * 8);
-    }
-  }
-  __device__ __forceinline__ void store_t(bf16_t* dst, int tid) const {
-    const int kg = tid / CPR, dg = tid % CPR;
-    // column e of the block = element e of every row; each column is stored as soon as it is
-    // formed, so only the 8 staged rows are live.
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      uint32_t w[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint4 a = st[2 * k], b = st[2 * k + 1];
-        const uint32_t da = (e >> 1) == 0 ? a.x : (e >> 1) == 1 ? a.y : (e >> 1) == 2 ? a.z : a.w;
-        const uint32_t db = (e >> 1) == 0 ? b.x : (e >> 1) == 1 ? b.y : (e >> 1) == 2 ? b.z : b.w;
-        w[k] = (e & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
-      }
-      const int d = dg * 8 + e;
-      *(uint4*)&dst[d * ATT_TS + tslot(d, kg) * 8] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-  }
-  // Row-major role (128 <= tid < 256).
-  __device__ __forceinline__ void load_r(const bf16_t* src, int64_t ld, int col0, int k0, int kend, int tid) {
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int c = (tid - 128) + 128 * i, r = c / CPR, dc = (c % CPR) * 8;
-      const int row = min(k0 + r, kend - 1);
-      st[i] = *(const uint4*)(src + (int64_t)row * ld + col0 + dc);
-    }
-  }
-  __device__ __forceinline__ void store_r(bf16_t* dst, int rs, int tid) const {
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int c = (tid - 128) + 128 * i, r = c / CPR, dc = (c % CPR) * 8;
-      *(uint4*)&dst[r * rs + dc] = st[i];
-    }
-  }
-};
-
-// A operand of a 16-key MFMA step from a transposed tile (dim row d), in the accumulator's key
-// order: lane group g supplies keys 8*kg0 + 4g + {0..3} and 8*(kg0 + 1) + 4g + {0..3}.
+// Transposed tiles hold each 16-key group (chunks 2p, 2p + 1 of a dim row) in the order the
+// MFMA accumulator holds probabilities: chunk 2p + g = keys 16p + 4g + {0..3}, 16p + 8 + 4g + {0..3}.
+// The A operand of a 16-key MFMA step (lane group g, dim row d, first chunk kg0 = 2p) is then
+// one 16-byte read.
 __device__ __forceinline__ bf16x8_t ld_perm_t(const bf16_t* t, int d, int kg0, int g) {
-  const bf16_t* row = t + d * ATT_TS + 4 * g;
-  const uint2 lo = *(const uint2*)(row + tslot(d, kg0) * 8);
-  const uint2 hi = *(const uint2*)(row + tslot(d, kg0 + 1) * 8);
-  return __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+  return *(const bf16x8_t*)(t + d * ATT_TS + tslot(d, kg0 + g) * 8);
+}
+
+// Stores keys 8*kg + {0..7} of dim row d (w[k] = keys 2k, 2k + 1) into that layout: keys
+// {0..3} go to chunk kg & ~1, keys {4..7} to chunk kg | 1, each at element offset 4 * (kg & 1).
+__device__ __forceinline__ void store_t8(bf16_t* t, int d, int kg, const uint32_t (&w)[4]) {
+  bf16_t* row = t + d * ATT_TS + 4 * (kg & 1);
+  *(uint2*)(row + tslot(d, kg & ~1) * 8) = make_uint2(w[0], w[1]);
+  *(uint2*)(row + tslot(d, kg | 1) * 8) = make_uint2(w[2], w[3]);
 }
 
 // Row-major [64 keys x D] tiles filled by direct global->LDS loads (16 bytes per lane). The
 // 16-byte chunk c of row r sits at slot c ^ kswz(r), which spreads the 16 rows one LDS cycle
 // serves over all banks for both the MFMA fragment reads and the transposition reads.
 template <int D> __device__ __forceinline__ int kswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+
+// A operand of a 16-key MFMA step read straight from a row-major, kswz-swizzled [64 keys x D]
+// tile with two LDS transpose loads (ds_read_b64_tr_b16). Within each 16-lane group the load
+// hands result lane j the (j % 4)-th element of the 8-byte rows supplied by source lanes j / 4 +
+// {0, 4, 8, 12}. Source lane s of group G supplies row r0 = 16p + 4 * (G >> 1) + s / 4 (then
+// r0 + 8), columns c = 32 tt + 16 * (G & 1) + 4 * (s % 4) .. + 3, so result lane (lq, g) receives
+// dim 32 tt + lq of keys 16p + 4g + {0..3} and 16p + 8 + 4g + {0..3}: the accumulator's key order.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// LDS byte addresses of the two 8-byte rows lane `lane` supplies for operand (tt, p).
+template <int D>
+__device__ __forceinline__ uint2 tr_frag_addr(const bf16_t* tile, int tt, int p, int lane) {
+  const int G = lane >> 4, sl = lane & 15;
+  const int c = tt * 32 + 16 * (G & 1) + 4 * (sl & 3);
+  const int r0 = 16 * p + 4 * (G >> 1) + (sl >> 2);
+  const bf16_t* a0 = tile + r0 * D + (((c >> 3) ^ kswz<D>(r0)) << 3) + (c & 7);
+  const bf16_t* a1 = tile + (r0 + 8) * D + (((c >> 3) ^ kswz<D>(r0 + 8)) << 3) + (c & 7);
+  return make_uint2((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) bf16_t*)a0,
+                    (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) bf16_t*)a1);
+}
+
+// Issues the two transpose loads of an operand. They are written as inline assembly: the
+// compiler would otherwise wait for every direct-to-LDS load still in flight (the next tile's)
+// before the first of them, since it cannot tell the stages apart. The caller waits for them
+// (s_waitcnt lgkmcnt with the results as operands) before using the result.
+__device__ __forceinline__ void tr_issue(uint2 addr, u32x2_t& lo, u32x2_t& hi) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(addr.x));
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(hi) : "v"(addr.y));
+}
+
+__device__ __forceinline__ bf16x8_t tr_join(u32x2_t lo, u32x2_t hi) {
+  return __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
 
 // One 64-row tile of a row-major [rows, ld] bf16 matrix (columns [col0, col0 + D)) via buffer
 // loads straight into LDS. The buffer resource starts at row k0 and covers rows [k0, kend), so
@@ -261,33 +198,6 @@ __device__ __forceinline__ bf16x8_t ld_frag(const bf16_t* tile, int r, int c) {
   return *(const bf16x8_t*)&tile[r * D + ((c ^ kswz<D>(r)) << 3)];
 }
 
-// LDS -> LDS transposition of a swizzled row-major V tile into the [D][keys] layout read by
-// ld_perm_t: thread tid < 8*D/8 handles the 8-key x 8-dim block (tid / CPR, tid % CPR).
-template <int D>
-__device__ __forceinline__ void transpose_tile(const bf16_t* vr, bf16_t* vt, int tid) {
-  constexpr int CPR = D / 8;
-  if (tid >= 8 * CPR) return;
-  const int kg = tid / CPR, dg = tid % CPR;
-  uint4 st[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = kg * 8 + i;
-    st[i] = *(const uint4*)&vr[r * D + ((dg ^ kswz<D>(r)) << 3)];
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint4 a = st[2 * k], b = st[2 * k + 1];
-      const uint32_t da = (e >> 1) == 0 ? a.x : (e >> 1) == 1 ? a.y : (e >> 1) == 2 ? a.z : a.w;
-      const uint32_t db = (e >> 1) == 0 ? b.x : (e >> 1) == 1 ? b.y : (e >> 1) == 2 ? b.z : b.w;
-      w[k] = (e & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
-    }
-    const int d = dg * 8 + e;
-    *(uint4*)&vt[d * ATT_TS + tslot(d, kg) * 8] = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-}
 
 __device__ __forceinline__ Bounds merge_bounds(const Bounds& a, const Bounds& b) {
   Bounds r;
@@ -303,14 +213,11 @@ __device__ __forceinline__ Bounds merge_bounds(const Bounds& a, const Bounds& b)
 template <int D, int QG>
 __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(const AttnArgs p) {
   constexpr int BK = ATT_BK, NKS = D / 16, NDT = D / 32, BQ = 128 * QG;
-  // Dynamic LDS: K tiles [2][64*D] (direct-to-LDS double buffer) and V rows [64*D]. V^T [D][72]
-  // is a separate static array: as a distinct object the compiler can tell that reading it does
-  // not depend on the direct-to-LDS loads of the next tile still in flight (with one shared array
-  // it waits for those loads before the first V^T read of every tile).
+  // Dynamic LDS: K and V tiles [2][64*D] each, double-buffered, filled by direct-to-LDS loads;
+  // the P.V operand is read from the row-major V tile with LDS transpose loads.
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
-  __shared__ __attribute__((aligned(16))) bf16_t Vt[D * ATT_TS];
   bf16_t* Ks = smem;
-  bf16_t* Vr = smem + 2 * BK * D;
+  bf16_t* Vs = smem + 2 * BK * D;
   __shared__ int sh[8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
   const int nqt = (p.Mq + BQ - 1) / BQ;
@@ -366,8 +273,9 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
   const bf16_t* K2 = (const bf16_t*)p.K2;
   const bf16_t* V2 = (const bf16_t*)p.V2;
   const int wid = __builtin_amdgcn_readfirstlane(w);
-  // Tile t streams into K stage t&1 and the V row buffer; every thread issues its loads of tile
-  // t+1 right after V(t) has been transposed, so they fly during tile t's math.
+  // Tile t streams into K and V stage t & 1; every thread issues its loads of tile t+1 right
+  // after the barrier that ends tile t-1 (whose stage they overwrite), so they fly during tile
+  // t's math.
   // The source is chosen arithmetically (f2 in {0, 1}), not with selects between variables:
   // the compiler would otherwise turn those into selected addresses of stack/kernarg memory.
   const uintptr_t k1a = (uintptr_t)K1, v1a = (uintptr_t)V1;
@@ -379,17 +287,16 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
     const int fkt = (f2 ? kt2 : kt1) + t * BK;
     const int fke = ke1 + f2 * (ke2 - ke1);
     dma_tile<D>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, kvh * D, fkt, fke, Ks + stage * BK * D, wid, lane);
-    dma_tile<D>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, kvh * D, fkt, fke, Vr, wid, lane);
+    dma_tile<D>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, kvh * D, fkt, fke, Vs + stage * BK * D, wid, lane);
   };
   if (nt > 0) fetch(0, 0);
 #pragma unroll 1
   for (int t = 0; t < nt; ++t) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();                       // K(t) and V rows(t) are in LDS
-    transpose_tile<D>(Vr, Vt, tid);
-    __syncthreads();                       // V^T(t) complete; V rows free for tile t+1
+    __syncthreads();                       // K(t), V(t) in LDS; every wave is done with tile t-1
     if (t + 1 < nt) fetch(t + 1, (t + 1) & 1);
     const bf16_t* Kc = Ks + (t & 1) * BK * D;
+    const bf16_t* Vc = Vs + (t & 1) * BK * D;
     const bool s2 = t >= n1;
     const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
     const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
@@ -466,9 +373,19 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
           for (int i = 0; i < 8; ++i) pv[i] = sacc[kk][qg][8 * hh + i];
           pb[qg] = pack_bf16x8(pv);
         }
+        u32x2_t vlo[NDT], vhi[NDT];
+#pragma unroll
+        for (int tt = 0; tt < NDT; ++tt) tr_issue(tr_frag_addr<D>(Vc, tt, kk * 2 + hh, lane), vlo[tt], vhi[tt]);
+        // all transpose loads of this step have returned (the results pass through the wait, so
+        // nothing reads them earlier)
+        if constexpr (NDT == 4)
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vlo[0]), "+v"(vhi[0]), "+v"(vlo[1]), "+v"(vhi[1]), "+v"(vlo[2]),
+                       "+v"(vhi[2]), "+v"(vlo[3]), "+v"(vhi[3]));
+        else
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vlo[0]), "+v"(vhi[0]), "+v"(vlo[1]), "+v"(vhi[1]));
 #pragma unroll
         for (int tt = 0; tt < NDT; ++tt) {
-          const bf16x8_t vf = ld_perm_t(Vt, tt * 32 + lq, kk * 4 + 2 * hh, g);
+          const bf16x8_t vf = tr_join(vlo[tt], vhi[tt]);
 #pragma unroll
           for (int qg = 0; qg < QG; ++qg)
             oacc[qg][tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[qg], oacc[qg][tt], 0, 0, 0);
@@ -523,7 +440,6 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   bf16_t* Ks = smem;                      // [2][64*D]
   bf16_t* Vs = smem + 2 * BK * D;         // [2][64*D]
-  bf16_t* Kt = Vs + 2 * BK * D;           // [D][ATT_TS]
   __shared__ int sh[16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(w);
@@ -606,9 +522,7 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
     __syncthreads();                       // K(t), V(t) in LDS; previous tile's reads are done
     const bf16_t* Kc = Ks + (t & 1) * BK * D;
     const bf16_t* Vc = Vs + (t & 1) * BK * D;
-    transpose_tile<D>(Kc, Kt, tid);
     if (t + 1 < nt) fetch(t + 1, (t + 1) & 1);
-    __syncthreads();                       // K^T(t) complete
     const bool s2 = t >= n1;
     const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
     const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
@@ -649,10 +563,18 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) dv[i] = sacc[8 * hh + i];
         const bf16x8_t b = pack_bf16x8(dv);
+        // K^T operand of dQ += dS K straight from the row-major K tile (transpose loads), two
+        // output tiles at a time to stay within two waves per SIMD
 #pragma unroll
-        for (int tt = 0; tt < NDT; ++tt)
-          dq[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm_t(Kt, tt * 32 + lq, kk * 4 + 2 * hh, g), b, dq[tt],
-                                                            0, 0, 0);
+        for (int t0 = 0; t0 < NDT; t0 += 2) {
+          u32x2_t klo[2], khi[2];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) tr_issue(tr_frag_addr<D>(Kc, t0 + i, kk * 2 + hh, lane), klo[i], khi[i]);
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(klo[0]), "+v"(khi[0]), "+v"(klo[1]), "+v"(khi[1]));
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            dq[t0 + i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(klo[i], khi[i]), b, dq[t0 + i], 0, 0, 0);
+        }
       }
     }
   }
@@ -695,8 +617,7 @@ __device__ __forceinline__ void stage_rows_and_t(const bf16_t* src, int64_t ld, 
       const uint32_t db = (e >> 1) == 0 ? b.x : (e >> 1) == 1 ? b.y : (e >> 1) == 2 ? b.z : b.w;
       w[k] = (e & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
     }
-    const int d = dg * 8 + e;
-    *(uint4*)&trndst[d * ATT_TS + tslot(d, kg) * 8] = make_uint4(w[0], w[1], w[2], w[3]);
+    store_t8(trndst, dg * 8 + e, kg, w);
   }
 }
 
@@ -965,7 +886,7 @@ static int attn_qg() {
 
 template <int D, int QG>
 static void launch_fwd_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
-  constexpr size_t lds = 3 * ATT_BK * D * sizeof(bf16_t);   // + the static V^T array
+  constexpr size_t lds = 4 * ATT_BK * D * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
     hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<D, QG>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -977,7 +898,7 @@ static void launch_fwd_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
 
 template <int D>
 static void launch_dq(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
-  constexpr size_t lds = (4 * ATT_BK * D + D * ATT_TS) * sizeof(bf16_t);
+  constexpr size_t lds = 4 * ATT_BK * D * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
     hipFuncSetAttribute((const void*)attn_dq_bf16_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
