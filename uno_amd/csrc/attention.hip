@@ -137,25 +137,38 @@ template <int D> __device__ __forceinline__ int kswz(int r) { return D == 128 ? 
 // dim 32 tt + lq of keys 16p + 4g + {0..3} and 16p + 8 + 4g + {0..3}: the accumulator's key order.
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
-// LDS byte addresses of the two 8-byte rows lane `lane` supplies for operand (tt, p).
+// Element offsets (within a [64 keys x D] tile) of the two rows lane `lane` supplies for operand
+// (tt, p = 0); operand p adds 16 * p * D (the kswz swizzle does not depend on p).
 template <int D>
-__device__ __forceinline__ uint2 tr_frag_addr(const bf16_t* tile, int tt, int p, int lane) {
+__device__ __forceinline__ int2 tr_frag_off(int tt, int lane) {
   const int G = lane >> 4, sl = lane & 15;
   const int c = tt * 32 + 16 * (G & 1) + 4 * (sl & 3);
-  const int r0 = 16 * p + 4 * (G >> 1) + (sl >> 2);
-  const bf16_t* a0 = tile + r0 * D + (((c >> 3) ^ kswz<D>(r0)) << 3) + (c & 7);
-  const bf16_t* a1 = tile + (r0 + 8) * D + (((c >> 3) ^ kswz<D>(r0 + 8)) << 3) + (c & 7);
-  return make_uint2((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) bf16_t*)a0,
-                    (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) bf16_t*)a1);
+  const int r0 = 4 * (G >> 1) + (sl >> 2);
+  return make_int2(r0 * D + (((c >> 3) ^ kswz<D>(r0)) << 3) + (c & 7),
+                   (r0 + 8) * D + (((c >> 3) ^ kswz<D>(r0 + 8)) << 3) + (c & 7));
 }
 
-// Issues the two transpose loads of an operand. They are written as inline assembly: the
+// Transpose loads of operand p from LDS byte addresses a (rows at p = 0): the step's 16-row
+// displacement is the instruction's immediate offset. They are written as inline assembly: the
 // compiler would otherwise wait for every direct-to-LDS load still in flight (the next tile's)
 // before the first of them, since it cannot tell the stages apart. The caller waits for them
-// (s_waitcnt lgkmcnt with the results as operands) before using the result.
-__device__ __forceinline__ void tr_issue(uint2 addr, u32x2_t& lo, u32x2_t& hi) {
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(addr.x));
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(hi) : "v"(addr.y));
+// (s_waitcnt lgkmcnt with the results as operands) before using the results.
+template <int OFF>
+__device__ __forceinline__ void tr_issue_at(uint2 a, u32x2_t& lo, u32x2_t& hi) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(lo) : "v"(a.x), "i"(OFF));
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(a.y), "i"(OFF));
+}
+template <int D>
+__device__ __forceinline__ void tr_issue_p(uint2 a, int p, u32x2_t& lo, u32x2_t& hi) {
+  constexpr int STEP = 16 * D * 2;   // bytes per 16 key rows
+  if (p == 0) tr_issue_at<0>(a, lo, hi);
+  else if (p == 1) tr_issue_at<STEP>(a, lo, hi);
+  else if (p == 2) tr_issue_at<2 * STEP>(a, lo, hi);
+  else tr_issue_at<3 * STEP>(a, lo, hi);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 __device__ __forceinline__ bf16x8_t tr_join(u32x2_t lo, u32x2_t hi) {
@@ -289,6 +302,14 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
     dma_tile<D>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, kvh * D, fkt, fke, Ks + stage * BK * D, wid, lane);
     dma_tile<D>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, kvh * D, fkt, fke, Vs + stage * BK * D, wid, lane);
   };
+  // Per-lane LDS offsets, fixed for the whole walk: K fragments (row lq, chunk 2 ks + g) and the
+  // rows this lane supplies to the V transpose loads.
+  int koff[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) koff[ks] = lq * D + (((ks * 2 + g) ^ kswz<D>(lq)) << 3);
+  int2 voff[NDT];
+#pragma unroll
+  for (int tt = 0; tt < NDT; ++tt) voff[tt] = tr_frag_off<D>(tt, lane);
   if (nt > 0) fetch(0, 0);
 #pragma unroll 1
   for (int t = 0; t < nt; ++t) {
@@ -296,7 +317,7 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
     __syncthreads();                       // K(t), V(t) in LDS; every wave is done with tile t-1
     if (t + 1 < nt) fetch(t + 1, (t + 1) & 1);
     const bf16_t* Kc = Ks + (t & 1) * BK * D;
-    const bf16_t* Vc = Vs + (t & 1) * BK * D;
+    const uint32_t vbase = lds_addr(Vs + (t & 1) * BK * D);
     const bool s2 = t >= n1;
     const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
     const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
@@ -314,7 +335,7 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
         for (int r = 0; r < 16; ++r) sacc[kk][qg][r] = 0.f;
       bf16x8_t kf[NKS];
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) kf[ks] = ld_frag<D>(Kc, kk * 32 + lq, ks * 2 + g);
+      for (int ks = 0; ks < NKS; ++ks) kf[ks] = *(const bf16x8_t*)(Kc + kk * 32 * D + koff[ks]);
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
@@ -375,7 +396,8 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
         }
         u32x2_t vlo[NDT], vhi[NDT];
 #pragma unroll
-        for (int tt = 0; tt < NDT; ++tt) tr_issue(tr_frag_addr<D>(Vc, tt, kk * 2 + hh, lane), vlo[tt], vhi[tt]);
+        for (int tt = 0; tt < NDT; ++tt)
+          tr_issue_p<D>(make_uint2(vbase + 2 * voff[tt].x, vbase + 2 * voff[tt].y), kk * 2 + hh, vlo[tt], vhi[tt]);
         // all transpose loads of this step have returned (the results pass through the wait, so
         // nothing reads them earlier)
         if constexpr (NDT == 4)
@@ -515,6 +537,13 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
     dma_tile<D, NW>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, kvh * D, fkt, fke, Ks + stage * BK * D, wid, lane);
     dma_tile<D, NW>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, kvh * D, fkt, fke, Vs + stage * BK * D, wid, lane);
   };
+  // Per-lane LDS offsets, fixed for the whole walk (see the forward kernel).
+  int koff[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) koff[ks] = lq * D + (((ks * 2 + g) ^ kswz<D>(lq)) << 3);
+  int2 toff[NDT];
+#pragma unroll
+  for (int tt = 0; tt < NDT; ++tt) toff[tt] = tr_frag_off<D>(tt, lane);
   if (nt > 0) fetch(0, 0);
 #pragma unroll 1
   for (int t = 0; t < nt; ++t) {
@@ -522,6 +551,7 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
     __syncthreads();                       // K(t), V(t) in LDS; previous tile's reads are done
     const bf16_t* Kc = Ks + (t & 1) * BK * D;
     const bf16_t* Vc = Vs + (t & 1) * BK * D;
+    const uint32_t kbase_lds = lds_addr(Kc);
     if (t + 1 < nt) fetch(t + 1, (t + 1) & 1);
     const bool s2 = t >= n1;
     const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
@@ -541,9 +571,9 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
       for (int k0 = 0; k0 < NKS; k0 += 4) {
         bf16x8_t f[4], v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = ld_frag<D>(Kc, kk * 32 + lq, (k0 + i) * 2 + g);
+        for (int i = 0; i < 4; ++i) f[i] = *(const bf16x8_t*)(Kc + kk * 32 * D + koff[k0 + i]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = ld_frag<D>(Vc, kk * 32 + lq, (k0 + i) * 2 + g);
+        for (int i = 0; i < 4; ++i) v[i] = *(const bf16x8_t*)(Vc + kk * 32 * D + koff[k0 + i]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], qreg[k0 + i], sacc, 0, 0, 0);
@@ -569,7 +599,9 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
         for (int t0 = 0; t0 < NDT; t0 += 2) {
           u32x2_t klo[2], khi[2];
 #pragma unroll
-          for (int i = 0; i < 2; ++i) tr_issue(tr_frag_addr<D>(Kc, t0 + i, kk * 2 + hh, lane), klo[i], khi[i]);
+          for (int i = 0; i < 2; ++i)
+            tr_issue_p<D>(make_uint2(kbase_lds + 2 * toff[t0 + i].x, kbase_lds + 2 * toff[t0 + i].y), kk * 2 + hh,
+                          klo[i], khi[i]);
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(klo[0]), "+v"(khi[0]), "+v"(klo[1]), "+v"(khi[1]));
 #pragma unroll
           for (int i = 0; i < 2; ++i)
