@@ -1057,6 +1057,196 @@ static void launch_nt_bf16(const GemmNT& p, int out_dtype, hipStream_t st) {
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// ---------------------------------------------------------------------------------------
+// 256x256 bf16 NT kernel with 16x16x32 MFMAs: 4 waves of 128x128 (8 x 8 accumulators of 4 floats,
+// 256 AGPRs), BK 64 in 2 LDS stages filled by direct-to-LDS loads with the same swizzled layout as
+// the 32x32x16 kernel. A tile is two 32-wide k-steps: step 0 reads step 1's fragments, then the
+// barrier that frees the stage, then step 1 reads the next tile's step-0 fragments and issues the
+// loads of the tile two ahead into the freed stage (one per four MFMAs). Per 32 k and wave: 8 A +
+// 8 B fragment reads (16 bytes per lane) and 64 MFMAs. With the B fragment as the first operand,
+// lane l holds C[row 16i + l % 16][cols 16j + 4 (l / 16) + 0..3] of accumulator (i, j).
+// ---------------------------------------------------------------------------------------
+template <typename OutT>
+__global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p) {
+  constexpr int BM = 256, BN = 256, BK = 64, NW = 4, TM = 8, TN = 8;
+  constexpr int CPR = BK / 8, RPI = 64 / CPR, INS = BM / (RPI * NW);   // 8 loads per operand and wave
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  bf16_t* As = smem;                            // [2][BM*BK]
+  bf16_t* Bs = smem + 2 * BM * BK;              // [2][BN*BK]
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
+  const int lin = xcd_remap(blockIdx.x, nM * nN);
+  constexpr int GROUP = 8;
+  const int group = lin / (GROUP * nN);
+  const int first_m = group * GROUP;
+  const int gsz = min(nM - first_m, GROUP);
+  const int ing = lin % (GROUP * nN);
+  const int m0 = (first_m + ing % gsz) * BM;
+  const int n0 = (ing / gsz) * BN;
+  const bool ext = p.A2 != nullptr && p.K2 > 0;
+  const int nk1 = p.K / BK;
+  const int nk = nk1 + (ext ? p.K2 / BK : 0);
+
+  const int lrowi = lane / CPR, slot = lane % CPR;
+  __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(((int64_t)(p.M - 1) * p.lda + p.K) * 2));
+  __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)(((int64_t)(p.N - 1) * p.ldb + p.K) * 2));
+  uint32_t a_vo[INS], b_vo[INS];
+  auto set_offsets = [&](int64_t lda, int64_t ldb) {
+#pragma unroll
+    for (int i = 0; i < INS; ++i) {
+      const int r = (i * NW + wid) * RPI + lrowi;
+      const int chunk = slot ^ dma_swz<BK>(r);
+      a_vo[i] = (uint32_t)(((int64_t)min(m0 + r, p.M - 1) * lda + chunk * 8) * 2);
+      b_vo[i] = (uint32_t)(((int64_t)min(n0 + r, p.N - 1) * ldb + chunk * 8) * 2);
+    }
+  };
+  set_offsets(p.lda, p.ldb);
+  int kbase = 0;
+  // Sets up the operand pair of tile t (the LoRA pair from tile nk1 on; tiles are set up in
+  // order) and returns its k byte offset.
+  auto dma_tile = [&](int t) -> uint32_t {
+    if (t == nk1) {
+      ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0), (uint32_t)(((int64_t)(p.M - 1) * p.lda2 + p.K2) * 2));
+      rb = make_rsrc(p.B2, (uint32_t)(((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2));
+      set_offsets(p.lda2, p.ldb2);
+      kbase = nk1;
+    }
+    return (uint32_t)(t - kbase) * BK * 2;
+  };
+  auto dma_one = [&](int n, uint32_t kb, int stage) {
+    bf16_t* as = As + stage * BM * BK + wid * RPI * BK;
+    bf16_t* bs = Bs + stage * BN * BK + wid * RPI * BK;
+    if (n < INS) buf_lds16(ra, a_vo[n], kb, as + n * NW * RPI * BK);
+    else buf_lds16(rb, b_vo[n - INS], kb, bs + (n - INS) * NW * RPI * BK);
+  };
+
+  // Fragment rows wm*128 + 16i + lane%16 (A) / wn*128 + 16j + lane%16 (B); chunk 4s + lane/16 of
+  // the 8 in a row (k-step s); every such row has the swizzle dma_swz(lane % 16).
+  const int wm = wid >> 1, wn = wid & 1;
+  const int lr = lane & 15, lk = lane >> 4;
+  const int sw = dma_swz<BK>(lr);
+  const int a_row0 = (wm * 128 + lr) * BK, b_row0 = (wn * 128 + lr) * BK;
+  bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+
+  f32x4_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
+
+  // One k-step: 64 MFMAs on (fa, fb); after every fourth a fragment read of (rstage, rs) in the
+  // order the next step consumes them (fa[0], fb[0..7], fa[1..7]); with ND loads, one
+  // direct-to-LDS load after every 64/ND-th MFMA.
+  auto step = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[TN], bf16x8_t (&na)[TM], bf16x8_t (&nb)[TN],
+                  int rstage, int rs, auto dma_n, uint32_t kb, int dstage) {
+    constexpr int ND = decltype(dma_n)::value;
+    constexpr int EVERY = ND ? TM * TN / ND : 1;
+    const bf16_t* as = As + rstage * BM * BK + a_row0;
+    const bf16_t* bs = Bs + rstage * BN * BK + b_row0;
+    const int co = ((4 * rs + lk) ^ sw) << 3;
+#pragma unroll
+    for (int idx = 0; idx < TM * TN; ++idx) {
+      const int i = idx / TN, j = idx % TN;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+      if (ND && idx % EVERY == 0) dma_one(idx / EVERY, kb, dstage);
+      if (idx % 4 == 0) {
+        const int r = idx / 4;   // 0: fa[0]; 1..8: fb[0..7]; 9..15: fa[1..7]
+        if (r == 0) na[0] = *(const bf16x8_t*)&as[co];
+        else if (r <= TN) nb[r - 1] = *(const bf16x8_t*)&bs[(r - 1) * 16 * BK + co];
+        else na[r - TN] = *(const bf16x8_t*)&as[(r - TN) * 16 * BK + co];
+      }
+    }
+#pragma unroll
+    for (int idx = 0; idx < TM * TN; ++idx) {
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      if (ND && idx % EVERY == 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
+      if (idx % 4 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using D0 = std::integral_constant<int, 0>;
+  using DF = std::integral_constant<int, 2 * INS>;
+
+  // Prologue: tiles 0 and 1 (clamped) in full; wait for tile 0; its step-0 fragments.
+  {
+    uint32_t kb = dma_tile(0);
+#pragma unroll
+    for (int n = 0; n < 2 * INS; ++n) dma_one(n, kb, 0);
+    kb = dma_tile(min(1, nk - 1));
+#pragma unroll
+    for (int n = 0; n < 2 * INS; ++n) dma_one(n, kb, 1);
+  }
+  wait_vm<2 * INS>();
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("s_barrier" ::: "memory");
+  {
+    const bf16_t* as = As + a_row0;
+    const bf16_t* bs = Bs + b_row0;
+    const int co = (lk ^ sw) << 3;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa0[i] = *(const bf16x8_t*)&as[i * 16 * BK + co];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb0[j] = *(const bf16x8_t*)&bs[j * 16 * BK + co];
+  }
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1, nxt = cur ^ 1;
+    __builtin_amdgcn_sched_barrier(0);
+    step(fa0, fb0, fa1, fb1, cur, 1, D0{}, 0u, 0);
+    // Tile kt+1 is complete once every wave is here with its loads landed; stage cur is free.
+    __builtin_amdgcn_s_waitcnt(0x0070);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t kb = dma_tile(min(kt + 2, nk - 1));
+    step(fa1, fb1, fa0, fb0, nxt, 0, DF{}, kb, cur);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0070);       // clamped loads still write LDS
+
+  OutT* C = (OutT*)p.C;
+  const OutT* R = (const OutT*)p.R;
+  auto epilogue = [&](auto has_res, auto checked) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm * 128 + i * 16 + lr;
+      if (checked && row >= p.M) continue;
+      const float sc = (!checked || p.gate == nullptr || p.gate[row] != 0) ? p.alpha : 0.f;
+      OutT* crow = C + (int64_t)row * p.ldc;
+      const OutT* rrow = has_res ? R + (int64_t)row * p.ldr : nullptr;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * 128 + j * 16 + lk * 4;
+        if (checked && col >= p.N) continue;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = acc[i][j][q] * sc;
+        store4(crow + col, has_res ? rrow + col : nullptr, v);
+      }
+    }
+  };
+  const bool interior = m0 + BM <= p.M && n0 + BN <= p.N && p.gate == nullptr;
+  if (R) {
+    if (interior) epilogue(std::true_type{}, std::false_type{}); else epilogue(std::true_type{}, std::true_type{});
+  } else {
+    if (interior) epilogue(std::false_type{}, std::false_type{}); else epilogue(std::false_type{}, std::true_type{});
+  }
+}
+
+template <typename OutT>
+static void launch_nt_w4m16(const GemmNT& p, hipStream_t st) {
+  constexpr size_t lds = 2 * (256 + 256) * 64 * sizeof(bf16_t);
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4m16_kernel<OutT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)lds);
+    configured = true;
+  }
+  const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
+  hipLaunchKernelGGL((gemm_nt_bf16_w4m16_kernel<OutT>), dim3(nb), dim3(256), lds, st, p);
+}
+
 // Configuration of the 256x256 direct-to-LDS kernel (UNOK_GEMM_CFG selects one, for tuning):
 //   0: 8 waves, BK 64, 2 stages   1: 8 waves, BK 32, 4 stages   2: 8 waves, BK 32, 5 stages
 //   3: 4 waves, BK 32, 4 stages   4: 4 waves, BK 64, 2 stages
@@ -1064,11 +1254,12 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 //      (5: each tile's direct-to-LDS loads spread over two MFMA steps, A half then B half)
 //   8: as 5, with the next tiles' loads issued as one burst and fragment reads bunched per step
 //   9: as 5, with all 16 loads of a tile spread over one MFMA step
+//  10: 4 waves of 128x128 with 16x16x32 MFMAs (BK 64 x 2 stages); the default
 static int dma_cfg() {
   static int c = [] {
     const char* e = getenv("UNOK_GEMM_CFG");
-    const int v = e ? atoi(e) : 5;
-    return (v >= 0 && v <= 9) ? v : 5;
+    const int v = e ? atoi(e) : 10;
+    return (v >= 0 && v <= 10) ? v : 10;
   }();
   return c;
 }
@@ -1122,10 +1313,12 @@ static void launch_nt_dma_o(const GemmNT& p, hipStream_t st) {
     case 7:
     case 8:
     case 9:
+    case 10:
       if (!buffer_ranges_ok(p)) { launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break; }
       if (dma_cfg() == 5) launch_nt_w4<64, 2, OutT, 2>(p, st);
       else if (dma_cfg() == 8) launch_nt_w4<64, 2, OutT, 0>(p, st);
       else if (dma_cfg() == 9) launch_nt_w4<64, 2, OutT, 1>(p, st);
+      else if (dma_cfg() == 10) launch_nt_w4m16<OutT>(p, st);
       else if (dma_cfg() == 6) launch_nt_w4<32, 4, OutT, 0>(p, st);
       else launch_nt_w4<32, 5, OutT, 0>(p, st);
       break;
