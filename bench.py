@@ -182,7 +182,7 @@ def cpu_baseline(threads: int) -> dict:
 
 
 TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "hbm_traffic_gemm_nt_w4_256_qwen3_8b_step.md")
+                               "hbm_traffic_gemm_nt_w4m16_256_qwen3_8b_step.md")
 
 
 def measured_traffic() -> int | None:
