@@ -125,9 +125,14 @@ __device__ __forceinline__ void store_t8(bf16_t* t, int d, int kg, const uint32_
 }
 
 // Row-major [64 keys x D] tiles filled by direct global->LDS loads (16 bytes per lane). The
-// 16-byte chunk c of row r sits at slot c ^ kswz(r), which spreads the 16 rows one LDS cycle
-// serves over all banks for both the MFMA fragment reads and the transposition reads.
-template <int D> __device__ __forceinline__ int kswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+// 16-byte chunk c of row r sits at slot c ^ kswz(r). For D = 128 (256-byte rows, one full pass
+// over the 64 banks) kswz rotates the row's low four bits: it is a bijection on any 16
+// consecutive rows (16-byte fragment reads: 16 rows, one chunk, per LDS cycle) and its two high
+// bits differ across any 4 aligned rows (transpose loads: 4 rows x 4 consecutive chunks per half
+// wave), so both read patterns hit distinct banks. kswz(r + 16) = kswz(r).
+template <int D> __device__ __forceinline__ int kswz(int r) {
+  return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((r >> 1) & 7);
+}
 
 // A operand of a 16-key MFMA step read straight from a row-major, kswz-swizzled [64 keys x D]
 // tile with two LDS transpose loads (ds_read_b64_tr_b16). Within each 16-lane group the load
