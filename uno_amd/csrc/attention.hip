@@ -180,15 +180,49 @@ __device__ __forceinline__ bf16x8_t tr_join(u32x2_t lo, u32x2_t hi) {
   return __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
-// One 64-row tile of a row-major [rows, ld] bf16 matrix (columns [col0, col0 + D)) via buffer
-// loads straight into LDS. The buffer resource starts at row k0 and covers rows [k0, kend), so
-// rows past kend read as zeros without any clamping arithmetic (their keys are masked).
+// Waits for every LDS load in flight; the transpose-load results of two 16-key steps pass
+// through the wait as operands, so nothing reads them before it.
+template <int NDT>
+__device__ __forceinline__ void tr_wait_all(u32x2_t (&lo)[2][NDT], u32x2_t (&hi)[2][NDT]) {
+  if constexpr (NDT == 4)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(lo[0][0]), "+v"(hi[0][0]), "+v"(lo[0][1]), "+v"(hi[0][1]), "+v"(lo[0][2]), "+v"(hi[0][2]),
+                   "+v"(lo[0][3]), "+v"(hi[0][3]), "+v"(lo[1][0]), "+v"(hi[1][0]), "+v"(lo[1][1]), "+v"(hi[1][1]),
+                   "+v"(lo[1][2]), "+v"(hi[1][2]), "+v"(lo[1][3]), "+v"(hi[1][3]));
+  else
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(lo[0][0]), "+v"(hi[0][0]), "+v"(lo[0][1]), "+v"(hi[0][1]), "+v"(lo[1][0]), "+v"(hi[1][0]),
+                   "+v"(lo[1][1]), "+v"(hi[1][1]));
+}
+
+// max(v[l], v[l ^ 32]) in every lane l, by swapping the two 32-lane halves in registers
+// (v_permlane32_swap) instead of a round trip through the LDS crossbar.
+__device__ __forceinline__ float half_swap_max(float v) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
+// Byte offset, within a 64-row tile of a row-major [rows, ld] bf16 matrix (columns [col0,
+// col0 + D)), of the 16 bytes this lane moves in its first direct-to-LDS load of the tile. Load i
+// adds i * NW * RPI rows: kswz repeats every 16 rows, so the swizzled chunk is the same for all i.
 template <int D, int NW = 4>
-__device__ __forceinline__ void dma_tile(const bf16_t* src, int64_t ld, int col0, int k0, int kend, bf16_t* dst,
-                                         int wid, int lane) {
+__device__ __forceinline__ uint32_t dma_lane_off(int64_t ld, int col0, int wid, int lane) {
+  constexpr int CPR = D / 8, RPI = 64 / CPR;
+  static_assert((NW * RPI) % 16 == 0, "the swizzle must repeat across a lane's loads");
+  const int rl = lane / CPR, slot = lane % CPR;
+  const int r = wid * RPI + rl;
+  return (uint32_t)(((int64_t)r * ld + col0 + ((slot ^ kswz<D>(r)) << 3)) * 2);
+}
+
+// One 64-row tile of a row-major [rows, ld] bf16 matrix via buffer loads straight into LDS, at
+// the per-lane offsets of dma_lane_off. The buffer resource starts at row k0 and covers rows
+// [k0, kend), so rows past kend read as zeros without any clamping arithmetic (their keys are
+// masked).
+template <int D, int NW = 4>
+__device__ __forceinline__ void dma_tile(const bf16_t* src, int64_t ld, uint32_t lane_off, int k0, int kend,
+                                         bf16_t* dst, int wid) {
   constexpr int CPR = D / 8, RPI = 64 / CPR, INS = 64 / (RPI * NW);
   static_assert(INS >= 1, "tile too small for the wave count");
-  const int rl = lane / CPR, slot = lane % CPR;
   // The tile's source, start row and row count are workgroup-uniform; reading them through
   // readfirstlane keeps the buffer resource in SGPRs (a resource the compiler cannot prove
   // uniform is issued through a per-load waterfall loop).
@@ -200,14 +234,11 @@ __device__ __forceinline__ void dma_tile(const bf16_t* src, int64_t ld, int col0
                       (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ld);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)ubase, (short)0, (int)((int64_t)nrows * uld * 2), 0x00020000);
-  const uint32_t ldb = (uint32_t)uld * 2;
+  const uint32_t step = (uint32_t)uld * (2 * NW * RPI);
 #pragma unroll
-  for (int i = 0; i < INS; ++i) {
-    const int r = (i * NW + wid) * RPI + rl;
-    const uint32_t voff = (uint32_t)r * ldb + (uint32_t)(col0 + ((slot ^ kswz<D>(r)) << 3)) * 2;
+  for (int i = 0; i < INS; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + (i * NW + wid) * RPI * D),
-                                             16, voff, 0, 0, 0);
-  }
+                                             16, lane_off + i * step, 0, 0, 0);
 }
 
 // MFMA fragment (row r, 16-byte chunk c) of a swizzled row-major tile.
@@ -300,12 +331,16 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
   const uintptr_t kd = (uintptr_t)K2 - k1a, vd = (uintptr_t)V2 - v1a;
   const int64_t ldkd = p.ldk2 - p.ldk1, ldvd = p.ldv2 - p.ldv1;
   const int kt1 = (kb1 / BK) * BK, kt2 = (kb2 / BK) * BK - n1 * BK;
+  // Per-lane byte offsets of the direct-to-LDS loads, one per source tensor, fixed for the walk.
+  const uint32_t ko1 = dma_lane_off<D>(p.ldk1, kvh * D, wid, lane), vo1 = dma_lane_off<D>(p.ldv1, kvh * D, wid, lane);
+  const uint32_t ko2 = has2 ? dma_lane_off<D>(p.ldk2, kvh * D, wid, lane) : 0u;
+  const uint32_t vo2 = has2 ? dma_lane_off<D>(p.ldv2, kvh * D, wid, lane) : 0u;
   auto fetch = [&](int t, int stage) {
     const int f2 = t >= n1 ? 1 : 0;
     const int fkt = (f2 ? kt2 : kt1) + t * BK;
     const int fke = ke1 + f2 * (ke2 - ke1);
-    dma_tile<D>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, kvh * D, fkt, fke, Ks + stage * BK * D, wid, lane);
-    dma_tile<D>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, kvh * D, fkt, fke, Vs + stage * BK * D, wid, lane);
+    dma_tile<D>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, f2 ? ko2 : ko1, fkt, fke, Ks + stage * BK * D, wid);
+    dma_tile<D>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, f2 ? vo2 : vo1, fkt, fke, Vs + stage * BK * D, wid);
   };
   // Per-lane LDS offsets, fixed for the whole walk: K fragments (row lq, chunk 2 ks + g) and the
   // rows this lane supplies to the V transpose loads.
@@ -329,96 +364,129 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
     const int w_maxlo = s2 ? wb2.maxlo : wb1.maxlo, w_minhi = s2 ? wb2.minhi : wb1.minhi;
     if (kt >= w_hi || kt + BK <= w_lo) continue;
     const bool full = kt >= w_maxlo && kt + BK <= w_minhi;
-    // Scores of both 32-key halves (kk) are issued first; the softmax of one half then runs on
-    // the VALU while the MFMA pipe works through the other half's products.
+    // Scores of both 32-key halves (kk). All K fragments of the tile are read before the first
+    // product, so the two MFMA chains run back to back instead of each MFMA waiting for its read.
     f32x16_t sacc[2][QG];
+    {
+      bf16x8_t kf[2][NKS];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+      for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int qg = 0; qg < QG; ++qg)
+        for (int ks = 0; ks < NKS; ++ks) kf[kk][ks] = *(const bf16x8_t*)(Kc + kk * 32 * D + koff[ks]);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kk][qg][r] = 0.f;
-      bf16x8_t kf[NKS];
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) kf[ks] = *(const bf16x8_t*)(Kc + kk * 32 * D + koff[ks]);
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-        for (int qg = 0; qg < QG; ++qg)
-          sacc[kk][qg] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qreg[qg][ks], sacc[kk][qg], 0, 0, 0);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-      for (int qg = 0; qg < QG; ++qg) {
-        f32x16_t& sv = sacc[kk][qg];
-        if (!full) {   // wave-uniform: only tiles that cut through some query's interval
-          const int lo = s2 ? ivq[qg].z : ivq[qg].x, hi = s2 ? ivq[qg].w : ivq[qg].y;
-          const int kbase = kt + kk * 32 + 4 * g;
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int key = kbase + 8 * (j >> 2) + (j & 3);
-            sv[j] = (key >= lo && key < hi) ? sv[j] : -INFINITY;
-          }
-        }
-        // Raw scores; the scale (> 0) is applied inside the exponent: p = 2^(s*scale_log2 - m).
-        float tmax = sv[0];
-#pragma unroll
-        for (int j = 1; j < 16; ++j) tmax = fmaxf(tmax, sv[j]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
-        // Lazy rescaling: the running max moves only when a row's max exceeds it by more than
-        // 8 (log2 units), so weights stay <= 2^8 and most steps skip rescaling the accumulators.
-        const bool grow = tmax > m_run[qg] + 8.f;
-        if (__any(grow)) {
-          const float m_new = grow ? fmaxf(m_run[qg], tmax) : m_run[qg];
-          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[qg] - m_new);
-          l_run[qg] *= alpha;
-#pragma unroll
-          for (int tt = 0; tt < NDT; ++tt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[qg][tt][r] *= alpha;
-          m_run[qg] = m_new;
-        }
-        // Branch-free when nothing is visible yet (m_run = -inf): every lane keeps feeding the
-        // shared MFMAs, with weights 2^-inf = 0.
-        const float neg_m = m_run[qg] == -INFINITY ? 0.f : -m_run[qg];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float e = fast_exp2(fmaf(sv[j], p.scale_log2, neg_m));
-          sv[j] = e;
-          l_run[qg] += e;
-        }
-      }
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        bf16x8_t pb[QG];
+      for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int qg = 0; qg < QG; ++qg) {
-          float pv[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) pv[i] = sacc[kk][qg][8 * hh + i];
-          pb[qg] = pack_bf16x8(pv);
+          for (int r = 0; r < 16; ++r) sacc[kk][qg][r] = 0.f;
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks)
+            sacc[kk][qg] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk][ks], qreg[qg][ks], sacc[kk][qg], 0, 0, 0);
         }
-        u32x2_t vlo[NDT], vhi[NDT];
 #pragma unroll
-        for (int tt = 0; tt < NDT; ++tt)
-          tr_issue_p<D>(make_uint2(vbase + 2 * voff[tt].x, vbase + 2 * voff[tt].y), kk * 2 + hh, vlo[tt], vhi[tt]);
-        // all transpose loads of this step have returned (the results pass through the wait, so
-        // nothing reads them earlier)
-        if constexpr (NDT == 4)
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vlo[0]), "+v"(vhi[0]), "+v"(vlo[1]), "+v"(vhi[1]), "+v"(vlo[2]),
-                       "+v"(vhi[2]), "+v"(vlo[3]), "+v"(vhi[3]));
-        else
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vlo[0]), "+v"(vhi[0]), "+v"(vlo[1]), "+v"(vhi[1]));
+      for (int i = 0; i < 2 * NKS; ++i) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
 #pragma unroll
-        for (int tt = 0; tt < NDT; ++tt) {
-          const bf16x8_t vf = tr_join(vlo[tt], vhi[tt]);
+      for (int i = 0; i < 2 * NKS * QG; ++i) __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!full) {   // wave-uniform: only tiles that cut through some query's interval
 #pragma unroll
-          for (int qg = 0; qg < QG; ++qg)
-            oacc[qg][tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[qg], oacc[qg][tt], 0, 0, 0);
+      for (int qg = 0; qg < QG; ++qg) {
+        const int lo = s2 ? ivq[qg].z : ivq[qg].x, hi = s2 ? ivq[qg].w : ivq[qg].y;
+        // key in [lo, hi)  <=>  (unsigned)(key - lo) < (unsigned)(hi - lo)
+        const uint32_t span = (uint32_t)max(hi - lo, 0);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int d0 = kt + kk * 32 + 4 * g - lo;
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            sacc[kk][qg][j] = (uint32_t)(d0 + 8 * (j >> 2) + (j & 3)) < span ? sacc[kk][qg][j] : -INFINITY;
         }
       }
     }
+    // V operands of the two 16-key steps of half kk ([kk][step][tt]).
+    u32x2_t vlo[2][2][NDT], vhi[2][2][NDT];
+    auto issue_v = [&](int kk) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int tt = 0; tt < NDT; ++tt)
+          tr_issue_p<D>(make_uint2(vbase + 2 * voff[tt].x, vbase + 2 * voff[tt].y), kk * 2 + hh, vlo[kk][hh][tt],
+                        vhi[kk][hh][tt]);
+    };
+    issue_v(0);   // in flight during the softmax
+    // One running-max update per tile. Raw scores; the scale (> 0) is applied inside the
+    // exponent: p = 2^(s*scale_log2 - m).
+    float neg_m[QG];
+#pragma unroll
+    for (int qg = 0; qg < QG; ++qg) {
+      float tmax = sacc[0][qg][0];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int j = kk ? 0 : 1; j < 16; ++j) tmax = fmaxf(tmax, sacc[kk][qg][j]);
+      tmax = half_swap_max(tmax) * p.scale_log2;
+      // Lazy rescaling: the running max moves only when a row's max exceeds it by more than
+      // 8 (log2 units), so weights stay <= 2^8 and most tiles skip rescaling the accumulators.
+      const bool grow = tmax > m_run[qg] + 8.f;
+      if (__any(grow)) {
+        const float m_new = grow ? fmaxf(m_run[qg], tmax) : m_run[qg];
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[qg] - m_new);
+        l_run[qg] *= alpha;
+#pragma unroll
+        for (int tt = 0; tt < NDT; ++tt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[qg][tt][r] *= alpha;
+        m_run[qg] = m_new;
+      }
+      // Branch-free when nothing is visible yet (m_run = -inf): every lane keeps feeding the
+      // shared MFMAs, with weights 2^-inf = 0.
+      neg_m[qg] = m_run[qg] == -INFINITY ? 0.f : -m_run[qg];
+    }
+    // Weights of half kk, packed to bf16 as the B operands of its two 16-key steps.
+    bf16x8_t pb[2][2][QG];
+    auto softmax_half = [&](int kk) {
+#pragma unroll
+      for (int qg = 0; qg < QG; ++qg) {
+        float e[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          e[j] = fast_exp2(fmaf(sacc[kk][qg][j], p.scale_log2, neg_m[qg]));
+          l_run[qg] += e[j];
+        }
+        pb[kk][0][qg] = pack_bf16x8(e);
+        pb[kk][1][qg] = pack_bf16x8(e + 8);
+      }
+    };
+    auto pv_half = [&](int kk) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int tt = 0; tt < NDT; ++tt) {
+          const bf16x8_t vf = tr_join(vlo[kk][hh][tt], vhi[kk][hh][tt]);
+#pragma unroll
+          for (int qg = 0; qg < QG; ++qg)
+            oacc[qg][tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kk][hh][qg], oacc[qg][tt], 0, 0, 0);
+        }
+    };
+    softmax_half(0);
+    // Results pass through the waits as operands, so nothing reads them earlier.
+    tr_wait_all<NDT>(vlo[0], vhi[0]);
+    issue_v(1);
+    // The first half's products run on the MFMA pipe while the VALU computes the second half's
+    // weights (independent work), one MFMA between every few VALU instructions.
+    pv_half(0);
+    softmax_half(1);
+    {
+      constexpr int NM = 2 * NDT * QG, NV = (56 * QG + NM - 1) / NM;
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_VALU, NV, 0);
+      }
+    }
+    tr_wait_all<NDT>(vlo[1], vhi[1]);
+    pv_half(1);
   }
 #pragma unroll
   for (int qg = 0; qg < QG; ++qg) {
@@ -535,12 +603,16 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
   const uintptr_t kd = (uintptr_t)p.K2 - k1a, vd = (uintptr_t)p.V2 - v1a;
   const int64_t ldkd = p.ldk2 - p.ldk1, ldvd = p.ldv2 - p.ldv1;
   const int kt1 = (kb1 / BK) * BK, kt2 = (kb2 / BK) * BK - n1 * BK;
+  const uint32_t ko1 = dma_lane_off<D, NW>(p.ldk1, kvh * D, wid, lane);
+  const uint32_t vo1 = dma_lane_off<D, NW>(p.ldv1, kvh * D, wid, lane);
+  const uint32_t ko2 = has2 ? dma_lane_off<D, NW>(p.ldk2, kvh * D, wid, lane) : 0u;
+  const uint32_t vo2 = has2 ? dma_lane_off<D, NW>(p.ldv2, kvh * D, wid, lane) : 0u;
   auto fetch = [&](int t, int stage) {
     const int f2 = t >= n1 ? 1 : 0;
     const int fkt = (f2 ? kt2 : kt1) + t * BK;
     const int fke = ke1 + f2 * (ke2 - ke1);
-    dma_tile<D, NW>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, kvh * D, fkt, fke, Ks + stage * BK * D, wid, lane);
-    dma_tile<D, NW>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, kvh * D, fkt, fke, Vs + stage * BK * D, wid, lane);
+    dma_tile<D, NW>((const bf16_t*)(k1a + f2 * kd), p.ldk1 + f2 * ldkd, f2 ? ko2 : ko1, fkt, fke, Ks + stage * BK * D, wid);
+    dma_tile<D, NW>((const bf16_t*)(v1a + f2 * vd), p.ldv1 + f2 * ldvd, f2 ? vo2 : vo1, fkt, fke, Vs + stage * BK * D, wid);
   };
   // Per-lane LDS offsets, fixed for the whole walk (see the forward kernel).
   int koff[NKS];

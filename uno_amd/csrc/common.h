@@ -122,6 +122,9 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return r;
 }
 
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
+
 // Maps a linear workgroup id so that consecutive logical tiles land on the same XCD.
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X; grouping logical
 // neighbours on one XCD lets them share that XCD's L2.

@@ -388,9 +388,6 @@ __device__ __forceinline__ void store4(float* dst, const float* res, const float
   *(float4*)dst = o;
 }
 
-// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
-
 template <int BK, int STAGES, typename OutT, int SCHED>
 __global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
   constexpr int BM = 256, BN = 256, NW = 4;
