@@ -525,13 +525,13 @@ __global__ __launch_bounds__(256) void attn_dsum_kernel(const T* __restrict__ dO
   if (lane == 0) Dsum[item] = s;
 }
 
-// dQ, bf16: per workgroup 256 queries (8 waves x 32) of one head; same tile walk as the forward.
-// K and V tiles stream into LDS by buffer loads (two stages); the transposed K used by the dQ
-// product is built LDS -> LDS at the start of each tile. Per 32-key half: S = K Q^T and
-// dP = V dO^T, then dS = P (dP - Dsum), then dQ += dS K.
-template <int D>
-__global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
-  constexpr int BK = ATT_BK, NKS = D / 16, NDT = D / 32, NW = 8, BQ = 32 * NW;
+// dQ, bf16: per workgroup 32 NW queries (NW waves x 32) of one head; same tile walk as the
+// forward. K and V tiles stream into LDS by buffer loads (two stages). Per 32-key half: S = K Q^T
+// and dP = V dO^T, then dS = P (dP - Dsum), then dQ += dS K, whose K^T operand comes from the
+// row-major K tile by transpose loads issued before the dS arithmetic.
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const AttnArgs p) {
+  constexpr int BK = ATT_BK, NKS = D / 16, NDT = D / 32, BQ = 32 * NW;
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   bf16_t* Ks = smem;                      // [2][64*D]
   bf16_t* Vs = smem + 2 * BK * D;         // [2][64*D]
@@ -657,6 +657,15 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
           dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[i], oreg[k0 + i], dpacc, 0, 0, 0);
         }
       }
+      // K^T operands of dQ += dS K for both 16-key steps, straight from the row-major K tile
+      // (transpose loads), issued before the dS arithmetic so that their latency hides behind it.
+      u32x2_t klo[2][NDT], khi[2][NDT];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int tt = 0; tt < NDT; ++tt)
+          tr_issue_p<D>(make_uint2(kbase_lds + 2 * toff[tt].x, kbase_lds + 2 * toff[tt].y), kk * 2 + hh, klo[hh][tt],
+                        khi[hh][tt]);
       const int kbase = kt + kk * 32 + 4 * g;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -664,27 +673,20 @@ __global__ __launch_bounds__(512) void attn_dq_bf16_kernel(const AttnArgs p) {
         const float pr = (key >= lo && key < hi) ? fast_exp2(fmaf(sacc[j], p.scale_log2, -lse)) : 0.f;
         sacc[j] = pr * (dpacc[j] - dsum);
       }
+      bf16x8_t b[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         float dv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) dv[i] = sacc[8 * hh + i];
-        const bf16x8_t b = pack_bf16x8(dv);
-        // K^T operand of dQ += dS K straight from the row-major K tile (transpose loads), two
-        // output tiles at a time to stay within two waves per SIMD
-#pragma unroll
-        for (int t0 = 0; t0 < NDT; t0 += 2) {
-          u32x2_t klo[2], khi[2];
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-            tr_issue_p<D>(make_uint2(kbase_lds + 2 * toff[t0 + i].x, kbase_lds + 2 * toff[t0 + i].y), kk * 2 + hh,
-                          klo[i], khi[i]);
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(klo[0]), "+v"(khi[0]), "+v"(klo[1]), "+v"(khi[1]));
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-            dq[t0 + i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(klo[i], khi[i]), b, dq[t0 + i], 0, 0, 0);
-        }
+        b[hh] = pack_bf16x8(dv);
       }
+      tr_wait_all<NDT>(klo, khi);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int tt = 0; tt < NDT; ++tt)
+          dq[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(klo[hh][tt], khi[hh][tt]), b[hh], dq[tt], 0, 0, 0);
     }
   }
   if (qvalid) {
@@ -1005,16 +1007,33 @@ static void launch_fwd_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
   hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, QG>), dim3(blocks), dim3(256), lds, st, a);
 }
 
-template <int D>
-static void launch_dq(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
+// Waves per dQ workgroup: 4 (128 queries, two independent workgroups per CU, whose phases
+// interleave on each SIMD; the default) or 8 (256 queries, one workgroup per CU: the two waves of
+// a SIMD then pass the same per-tile barrier and stall together). UNOK_ATTN_DQ_WAVES selects.
+static int attn_dq_waves() {
+  static int w = [] {
+    const char* e = getenv("UNOK_ATTN_DQ_WAVES");
+    return (e && atoi(e) == 8) ? 8 : 4;
+  }();
+  return w;
+}
+
+template <int D, int NW>
+static void launch_dq_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
   constexpr size_t lds = 4 * ATT_BK * D * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)attn_dq_bf16_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)attn_dq_bf16_kernel<D, NW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
-  const unsigned blocks = (unsigned)(((Mq + 255) / 256) * Hq);
-  hipLaunchKernelGGL(attn_dq_bf16_kernel<D>, dim3(blocks), dim3(512), lds, st, a);
+  const unsigned blocks = (unsigned)(((Mq + 32 * NW - 1) / (32 * NW)) * Hq);
+  hipLaunchKernelGGL((attn_dq_bf16_kernel<D, NW>), dim3(blocks), dim3(NW * 64), lds, st, a);
+}
+
+template <int D>
+static void launch_dq(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
+  if (attn_dq_waves() == 4) launch_dq_t<D, 4>(Mq, Hq, st, a);
+  else launch_dq_t<D, 8>(Mq, Hq, st, a);
 }
 
 template <int D>
