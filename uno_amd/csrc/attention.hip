@@ -195,6 +195,16 @@ __device__ __forceinline__ void tr_wait_all(u32x2_t (&lo)[2][NDT], u32x2_t (&hi)
                    "+v"(lo[1][1]), "+v"(hi[1][1]));
 }
 
+// As tr_wait_all, for the transpose-load results of one 16-key step.
+template <int NDT>
+__device__ __forceinline__ void tr_wait_one(u32x2_t (&lo)[NDT], u32x2_t (&hi)[NDT]) {
+  if constexpr (NDT == 4)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(lo[0]), "+v"(hi[0]), "+v"(lo[1]), "+v"(hi[1]), "+v"(lo[2]), "+v"(hi[2]), "+v"(lo[3]), "+v"(hi[3]));
+  else
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo[0]), "+v"(hi[0]), "+v"(lo[1]), "+v"(hi[1]));
+}
+
 // max(v[l], v[l ^ 32]) in every lane l, by swapping the two 32-lane halves in registers
 // (v_permlane32_swap) instead of a round trip through the LDS crossbar.
 __device__ __forceinline__ float half_swap_max(float v) {
@@ -636,8 +646,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
     const int w_maxlo = s2 ? wb2.maxlo : wb1.maxlo, w_minhi = s2 ? wb2.minhi : wb1.minhi;
     if (kt >= w_hi || kt + BK <= w_lo) continue;
     const bool full = kt >= w_maxlo && kt + BK <= w_minhi;
-    const int lo = full ? INT_MIN / 2 : (s2 ? ivq.z : ivq.x);
-    const int hi = full ? INT_MAX / 2 : (s2 ? ivq.w : ivq.y);
+    // key in [lo, hi)  <=>  (unsigned)(key - lo) < (unsigned)(hi - lo)
+    const int lo = s2 ? ivq.z : ivq.x;
+    const uint32_t span = (uint32_t)max((s2 ? ivq.w : ivq.y) - lo, 0);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       f32x16_t sacc, dpacc;
@@ -657,22 +668,27 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
           dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[i], oreg[k0 + i], dpacc, 0, 0, 0);
         }
       }
-      // K^T operands of dQ += dS K for both 16-key steps, straight from the row-major K tile
-      // (transpose loads), issued before the dS arithmetic so that their latency hides behind it.
+      // K^T operands of dQ += dS K straight from the row-major K tile (transpose loads): those of
+      // the first 16-key step are issued before the dS arithmetic, so that their latency hides
+      // behind it, those of the second after it (in flight during the first step's products).
       u32x2_t klo[2][NDT], khi[2][NDT];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
+      auto issue_k = [&](int hh) {
 #pragma unroll
         for (int tt = 0; tt < NDT; ++tt)
           tr_issue_p<D>(make_uint2(kbase_lds + 2 * toff[tt].x, kbase_lds + 2 * toff[tt].y), kk * 2 + hh, klo[hh][tt],
                         khi[hh][tt]);
-      const int kbase = kt + kk * 32 + 4 * g;
+      };
+      issue_k(0);
+      float pr[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = kbase + 8 * (j >> 2) + (j & 3);
-        const float pr = (key >= lo && key < hi) ? fast_exp2(fmaf(sacc[j], p.scale_log2, -lse)) : 0.f;
-        sacc[j] = pr * (dpacc[j] - dsum);
+      for (int j = 0; j < 16; ++j) pr[j] = fast_exp2(fmaf(sacc[j], p.scale_log2, -lse));
+      if (!full) {   // wave-uniform: only tiles that cut through some query's interval
+        const int d0 = kt + kk * 32 + 4 * g - lo;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) pr[j] = (uint32_t)(d0 + 8 * (j >> 2) + (j & 3)) < span ? pr[j] : 0.f;
       }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sacc[j] = pr[j] * (dpacc[j] - dsum);
       bf16x8_t b[2];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -681,12 +697,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
         for (int i = 0; i < 8; ++i) dv[i] = sacc[8 * hh + i];
         b[hh] = pack_bf16x8(dv);
       }
-      tr_wait_all<NDT>(klo, khi);
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
+      for (int hh = 0; hh < 2; ++hh) {
+        tr_wait_one<NDT>(klo[hh], khi[hh]);
+        if (hh == 0) issue_k(1);
 #pragma unroll
         for (int tt = 0; tt < NDT; ++tt)
           dq[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(klo[hh][tt], khi[hh][tt]), b[hh], dq[tt], 0, 0, 0);
+      }
     }
   }
   if (qvalid) {
