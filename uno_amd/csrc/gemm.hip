@@ -206,7 +206,7 @@ template <int N> __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int BM, int BN, int NW, int BK, int STAGES, typename OutT>
+template <int BM, int BN, int NW, int BK, int STAGES, typename OutT, bool ROT = false>
 __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT p) {
   constexpr int CPR = BK / 8;                     // 16-byte chunks per tile row
   constexpr int RPI = 64 / CPR;                   // tile rows per wave load instruction
@@ -259,11 +259,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT 
     b_off[i] = (int64_t)gn * p.ldb + chunk * 8;
     b2_off[i] = (int64_t)gn * p.ldb2 + chunk * 8;
   }
+  // With ROT, workgroup b walks the main K tiles starting at tile (7 b) mod nk1: workgroups that
+  // run at the same time then read different column offsets of their rows instead of the same one.
+  const int rot = ROT && nk1 > 0 ? (int)((7u * blockIdx.x) % (unsigned)nk1) : 0;
   auto issue = [&](int kt, int buf) {
     bf16_t* as = As + buf * BM * BK;
     bf16_t* bs = Bs + buf * BN * BK;
     if (kt < nk1) {
-      const int kk = kt * BK;
+      const int kr = kt + rot;
+      const int kk = (kr >= nk1 ? kr - nk1 : kr) * BK;
 #pragma unroll
       for (int i = 0; i < A_INS; ++i) lds_dma16(A + a_off[i] + kk, as + (i * NW + wid) * RPI * BK);
 #pragma unroll
@@ -1285,17 +1289,17 @@ static void launch_nt_w4(const GemmNT& p, hipStream_t st) {
   hipLaunchKernelGGL((gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SCHED>), dim3(nb), dim3(256), lds, st, p);
 }
 
-template <int BM, int BN, int NW, int BK, int STAGES, typename OutT>
+template <int BM, int BN, int NW, int BK, int STAGES, typename OutT, bool ROT = false>
 static void launch_nt_dma_t(const GemmNT& p, hipStream_t st) {
   constexpr size_t lds = (size_t)STAGES * (BM + BN) * BK * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT>,
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT, ROT>,
                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
   const int nb = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT>), dim3(nb), dim3(NW * 64), lds, st, p);
+  hipLaunchKernelGGL((gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT, ROT>), dim3(nb), dim3(NW * 64), lds, st, p);
 }
 
 template <typename OutT>
@@ -1323,20 +1327,22 @@ static void launch_nt_dma_o(const GemmNT& p, hipStream_t st) {
   }
 }
 
-template <int BM, int BN, int NW, int BK, int STAGES>
+template <int BM, int BN, int NW, int BK, int STAGES, bool ROT = false>
 static void launch_nt_dma_o2(const GemmNT& p, int out_dtype, hipStream_t st) {
-  if (out_dtype == UNOK_F32) launch_nt_dma_t<BM, BN, NW, BK, STAGES, float>(p, st);
-  else launch_nt_dma_t<BM, BN, NW, BK, STAGES, bf16_t>(p, st);
+  if (out_dtype == UNOK_F32) launch_nt_dma_t<BM, BN, NW, BK, STAGES, float, ROT>(p, st);
+  else launch_nt_dma_t<BM, BN, NW, BK, STAGES, bf16_t, ROT>(p, st);
 }
 
-// Skinny NT path (N <= 192): 1 = 64xN tiles with 4 LDS stages for N <= 128 and 3 for N <= 192
-// (default), 2 = 2 stages, 3 = 4 stages, 4 = 5 stages, 0 = off
-// (register-staged 128x64 / 128x128 tiles). UNOK_SKINNY_CFG selects one, for tuning.
+// Skinny NT path (N <= 192): 1 = 64xN tiles with 4 LDS stages for N <= 128 and 3 for N <= 192,
+// 2 = 2 stages, 3 = 4 stages, 4 = 5 stages, 5 = 8 / 6 / 4 stages, 6 = as 1 with each workgroup's
+// K walk rotated (default; the concurrent reads then spread over the rows' column offsets instead
+// of all hitting the same one), 0 = off (register-staged 128x64 / 128x128 tiles).
+// UNOK_SKINNY_CFG selects one, for tuning.
 static int skinny_cfg() {
   static int c = [] {
     const char* e = getenv("UNOK_SKINNY_CFG");
-    const int v = e ? atoi(e) : 1;
-    return (v >= 0 && v <= 4) ? v : 1;
+    const int v = e ? atoi(e) : 6;
+    return (v >= 0 && v <= 6) ? v : 6;
   }();
   return c;
 }
@@ -1411,6 +1417,14 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
     } else if (sk == 3) {
       if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 4>(p, out_dtype, st);
       else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 4>(p, out_dtype, st);
+      else launch_nt_dma_o2<64, 192, 4, 64, 4>(p, out_dtype, st);
+    } else if (sk == 6) {
+      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 4, true>(p, out_dtype, st);
+      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 4, true>(p, out_dtype, st);
+      else launch_nt_dma_o2<64, 192, 4, 64, 3, true>(p, out_dtype, st);
+    } else if (sk == 5) {
+      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 8>(p, out_dtype, st);
+      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 6>(p, out_dtype, st);
       else launch_nt_dma_o2<64, 192, 4, 64, 4>(p, out_dtype, st);
     } else if (sk == 4) {
       if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 5>(p, out_dtype, st);
