@@ -51,16 +51,6 @@ __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
 // denormal flush towards zero, which is immaterial for softmax weights).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// A operand for a 16-key MFMA step read from a transposed [D][keys] LDS tile, with the key
-// permutation of the accumulator layout: lane group g supplies keys base+4g+{0..3} and
-// base+8+4g+{0..3}.
-__device__ __forceinline__ bf16x8_t ld_perm(const bf16_t* row, int base, int g) {
-  const uint2 lo = *(const uint2*)(row + base + 4 * g);
-  const uint2 hi = *(const uint2*)(row + base + 8 + 4 * g);
-  uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
-  return __builtin_bit_cast(bf16x8_t, u);
-}
-
 __device__ __forceinline__ int wave_min_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
@@ -98,31 +88,7 @@ __device__ __forceinline__ int2 wg_bounds(const Bounds& w, int* sh) {
   return make_int2(__builtin_amdgcn_readfirstlane(lo), __builtin_amdgcn_readfirstlane(hi));
 }
 
-// ---------------------------------------------------------------------------------------
-// Transposed [D][keys] LDS tiles (K for dQ, Q and dO for dK/dV) have 72-element rows; the
-// 16-byte chunk kg of dim row d sits at slot kg ^ ((d >> 4) & 7), which keeps both the
-// transposed stores and the MFMA operand reads on distinct banks.
-// ---------------------------------------------------------------------------------------
 constexpr int ATT_BK = 64;     // keys per tile
-constexpr int ATT_TS = 72;     // transposed tile row pitch (elements)
-
-__device__ __forceinline__ int tslot(int d, int kg) { return kg ^ ((d >> 4) & 7); }
-
-// Transposed tiles hold each 16-key group (chunks 2p, 2p + 1 of a dim row) in the order the
-// MFMA accumulator holds probabilities: chunk 2p + g = keys 16p + 4g + {0..3}, 16p + 8 + 4g + {0..3}.
-// The A operand of a 16-key MFMA step (lane group g, dim row d, first chunk kg0 = 2p) is then
-// one 16-byte read.
-__device__ __forceinline__ bf16x8_t ld_perm_t(const bf16_t* t, int d, int kg0, int g) {
-  return *(const bf16x8_t*)(t + d * ATT_TS + tslot(d, kg0 + g) * 8);
-}
-
-// Stores keys 8*kg + {0..7} of dim row d (w[k] = keys 2k, 2k + 1) into that layout: keys
-// {0..3} go to chunk kg & ~1, keys {4..7} to chunk kg | 1, each at element offset 4 * (kg & 1).
-__device__ __forceinline__ void store_t8(bf16_t* t, int d, int kg, const uint32_t (&w)[4]) {
-  bf16_t* row = t + d * ATT_TS + 4 * (kg & 1);
-  *(uint2*)(row + tslot(d, kg & ~1) * 8) = make_uint2(w[0], w[1]);
-  *(uint2*)(row + tslot(d, kg | 1) * 8) = make_uint2(w[2], w[3]);
-}
 
 // Row-major [64 keys x D] tiles filled by direct global->LDS loads (16 bytes per lane). The
 // 16-byte chunk c of row r sits at slot c ^ kswz(r). For D = 128 (256-byte rows, one full pass
@@ -719,50 +685,47 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
   }
 }
 
-// Stages a [64 rows x D] tile of Q or dO for the dK/dV kernel: row-major (pitch RS) and
-// transposed ([D][ATT_TS] with the tslot swizzle), from 8x8 register blocks so both copies are
-// written with 16-byte stores. `half` selects the thread group (threads [128 * half, +128)).
-template <int D, int RS>
-__device__ __forceinline__ void stage_rows_and_t(const bf16_t* src, int64_t ld, int col0, int r0, int rend,
-                                                 bf16_t* rowdst, bf16_t* trndst, int t) {
-  constexpr int CPR = D / 8;
-  if (t >= 8 * CPR) return;
-  const int kg = t / CPR, dg = t % CPR;
-  uint4 st[8];
+// Rows [q0, q0 + 32) (columns [col0, col0 + D)) of a row-major bf16 matrix into a wave-private
+// [32 x D] LDS tile (kswz swizzle) by direct-to-LDS loads issued by one wave; the buffer resource
+// covers rows [q0, rend), so rows past rend read as zeros.
+template <int D>
+__device__ __forceinline__ void dma_rows32(const bf16_t* src, int64_t ld, int col0, int q0, int rend, bf16_t* dst,
+                                           int lane) {
+  constexpr int CPR = D / 8, RPI = 64 / CPR, INS = 32 / RPI;
+  const int rl = lane / CPR, slot = lane % CPR;
+  const int nrows = __builtin_amdgcn_readfirstlane(max(0, min(rend - q0, 32)));
+  const uintptr_t base = (uintptr_t)(src + (int64_t)q0 * ld + col0);
+  const uintptr_t ubase = ((uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32)) << 32) |
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  const int64_t uld = ((int64_t)__builtin_amdgcn_readfirstlane((int)(ld >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ld);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)ubase, (short)0, (int)((int64_t)nrows * uld * 2), 0x00020000);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = kg * 8 + i;
-    const int row = r0 + r;
-    st[i] = row < rend ? *(const uint4*)(src + (int64_t)row * ld + col0 + dg * 8) : make_uint4(0, 0, 0, 0);
-    *(uint4*)&rowdst[r * RS + dg * 8] = st[i];
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint4 a = st[2 * k], b = st[2 * k + 1];
-      const uint32_t da = (e >> 1) == 0 ? a.x : (e >> 1) == 1 ? a.y : (e >> 1) == 2 ? a.z : a.w;
-      const uint32_t db = (e >> 1) == 0 ? b.x : (e >> 1) == 1 ? b.y : (e >> 1) == 2 ? b.z : b.w;
-      w[k] = (e & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
-    }
-    store_t8(trndst, dg * 8 + e, kg, w);
+  for (int i = 0; i < INS; ++i) {
+    const int r = i * RPI + rl;
+    const uint32_t voff = (uint32_t)r * (uint32_t)uld * 2 + (uint32_t)((slot ^ kswz<D>(r)) << 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * RPI * D), 16,
+                                             voff, 0, 0, 0);
   }
 }
 
-// dK, dV of source-2 keys, bf16: per workgroup 128 keys (4 waves x 32) of one kv-head; walks
-// the query rows [qlo2, qhi2) of those keys for every q-head of the GQA group.
+// dK, dV of source-2 keys, bf16: per workgroup 128 keys (4 waves x 32) of one kv-head. Each wave
+// walks, for every q-head of the GQA group, the 32-query sub-tiles that its keys' query intervals
+// [qlo2, qhi2) touch (one per head for blocks up to 32 when the 32 keys fall in aligned blocks),
+// staging the Q and dO rows of a sub-tile into its own LDS region (no workgroup barriers).
+// Per sub-tile: S = Q K^T and dP = dO V^T with K, V in registers (lane = key), P and dS from
+// LSE and Dsum, then dV^T += dO^T P and dK^T += Q^T dS with the transposed operands read from the
+// row-major tiles by transpose loads in the accumulator's query order.
 template <int D>
-__global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
-  constexpr int BQ = 64, RS = D + 8, NKS = D / 16, NDT = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16_t Qs[BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Qt[D * ATT_TS];
-  __shared__ __attribute__((aligned(16))) bf16_t Os[BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Ot[D * ATT_TS];
-  __shared__ float s_lse[BQ], s_dsum[BQ];
-  __shared__ int s_lo[BQ], s_hi[BQ];
-  __shared__ int sh[8];
+__global__ __launch_bounds__(256, 2) void attn_dkv_bf16_kernel(const AttnArgs p) {
+  constexpr int NKS = D / 16, NDT = D / 32, QT = 32;
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];   // per wave: Q [32*D], dO [32*D]
+  __shared__ __attribute__((aligned(16))) float s_ld[4][2][QT];     // per wave: LSE, Dsum of the sub-tile
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, lq = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(w);
+  bf16_t* Qw = smem + wid * 2 * QT * D;
+  bf16_t* Ow = Qw + QT * D;
   const int nkt = (p.Mk2 + 127) / 128;
   const int lin = xcd_remap(blockIdx.x, nkt * p.Hkv);
   const int kvh = lin % p.Hkv, kt = lin / p.Hkv;
@@ -775,6 +738,8 @@ __global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
     qlo = a.x;
     qhi = a.y;
   }
+  // query q sees this key  <=>  (unsigned)(q - qlo) < span  (span = 0: no query, or no key)
+  const uint32_t span = (uint32_t)max(qhi - qlo, 0);
   const bf16_t* K = (const bf16_t*)p.K2;
   const bf16_t* V = (const bf16_t*)p.V2;
   bf16x8_t kreg[NKS], vreg[NKS];
@@ -787,75 +752,87 @@ __global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
       kreg[ks] = vreg[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
     }
   }
-  const Bounds wb = wave_bounds(kvalid, qlo, qhi);
-  const int2 rq = wg_bounds(wb, sh);
-  const int qb = rq.x, qe = rq.y;
+  const int wlo = __builtin_amdgcn_readfirstlane(wave_min_i(span ? qlo : INT_MAX));
+  const int whi = __builtin_amdgcn_readfirstlane(wave_max_i(span ? qhi : INT_MIN));
   f32x16_t dk[NDT], dv[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) { dk[t][r] = 0.f; dv[t][r] = 0.f; }
+  // Fragment (row lq, chunk 2 ks + g) of a row-major tile sits at lq D + 8 ((2 ks + g) ^ kswz(lq))
+  // = kb0 + 16 (ks ^ ksh): two per-lane values instead of NKS offsets.
+  const int ksw = kswz<D>(lq);
+  const int kb0 = lq * D + 8 * (g ^ (ksw & 1)), ksh = ksw >> 1;
+  int2 toff[NDT];
+#pragma unroll
+  for (int tt = 0; tt < NDT; ++tt) toff[tt] = tr_frag_off<D>(tt, lane);
+  const uint32_t qbase = lds_addr(Qw), obase = lds_addr(Ow);
   const bf16_t* Q = (const bf16_t*)p.Q;
   const bf16_t* dO = (const bf16_t*)p.dO;
-  if (qb < qe) {
+  if (wlo < whi) {
 #pragma unroll 1
     for (int hr = 0; hr < rep; ++hr) {
       const int h = kvh * rep + hr;
 #pragma unroll 1
-      for (int q0 = (qb / BQ) * BQ; q0 < qe; q0 += BQ) {
-        __syncthreads();
-        if (tid < 128) stage_rows_and_t<D, RS>(Q, p.ldq, h * D, q0, qe, Qs, Qt, tid);
-        else stage_rows_and_t<D, RS>(dO, p.lddo, h * D, q0, qe, Os, Ot, tid - 128);
-        if (tid < BQ) {
-          const int qr = q0 + tid;
-          const bool ok = qr < qe;
-          s_lse[tid] = ok ? p.LSE[(int64_t)qr * p.Hq + h] : 0.f;
-          s_dsum[tid] = ok ? p.Dsum[(int64_t)qr * p.Hq + h] : 0.f;
-          s_lo[tid] = ok ? p.iv[(int64_t)qr * 8 + 2] : 0;
-          s_hi[tid] = ok ? p.iv[(int64_t)qr * 8 + 3] : 0;
+      for (int q0 = (wlo / QT) * QT; q0 < whi; q0 += QT) {
+        // The previous sub-tile's LDS reads have all returned (their results fed MFMAs).
+        dma_rows32<D>(Q, p.ldq, h * D, q0, p.Mq, Qw, lane);
+        dma_rows32<D>(dO, p.lddo, h * D, q0, p.Mq, Ow, lane);
+        if (lane < QT) {
+          const int qr = q0 + lane;
+          const bool ok = qr < p.Mq;
+          s_ld[wid][0][lane] = ok ? p.LSE[(int64_t)qr * p.Hq + h] : 0.f;
+          s_ld[wid][1][lane] = ok ? p.Dsum[(int64_t)qr * p.Hq + h] : 0.f;
         }
-        __syncthreads();
-        if (q0 >= wb.hi || q0 + BQ <= wb.lo) continue;
-        f32x16_t sacc[2], dpacc[2];
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        f32x16_t sacc, dpacc;
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
+        for (int r = 0; r < 16; ++r) { sacc[r] = 0.f; dpacc[r] = 0.f; }
 #pragma unroll
-          for (int r = 0; r < 16; ++r) { sacc[qq][r] = 0.f; dpacc[qq][r] = 0.f; }
+        for (int ks = 0; ks < NKS; ++ks) {
+          const int off = kb0 + 16 * (ks ^ ksh);
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(Qw + off), kreg[ks], sacc, 0, 0, 0);
+          dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8_t*)(Ow + off), vreg[ks], dpacc, 0, 0, 0);
+        }
+        // Lane holds queries q0 + 8 (j / 4) + 4 g + (j % 4) of key krow.
+        const int dq0 = q0 + 4 * g - qlo;
 #pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            sacc[qq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Qs[(qq * 32 + lq) * RS + ks * 16 + g * 8]),
-                                                                kreg[ks], sacc[qq], 0, 0, 0);
-            dpacc[qq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(&Os[(qq * 32 + lq) * RS + ks * 16 + g * 8]),
-                                                                 vreg[ks], dpacc[qq], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          const float4 l4 = *(const float4*)&s_ld[wid][0][8 * i + 4 * g];
+          const float4 d4 = *(const float4*)&s_ld[wid][1][8 * i + 4 * g];
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = 4 * i + e;
+            const float pe = fast_exp2(fmaf(sacc[j], p.scale_log2, -lv[e]));
+            const float pr = (uint32_t)(dq0 + 8 * i + e) < span ? pe : 0.f;
+            sacc[j] = pr;
+            dpacc[j] = pr * (dpacc[j] - dv4[e]);
           }
         }
-        // lane holds rows q = q0 + qq*32 + 8(j/4) + 4g + (j%4), key = krow
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq)
+        for (int hh = 0; hh < 2; ++hh) {
+          float pv[8], dsv[8];
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int ql = qq * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-            float pr = 0.f;
-            if (kvalid && krow >= s_lo[ql] && krow < s_hi[ql]) pr = fast_exp2(sacc[qq][j] * p.scale_log2 - s_lse[ql]);
-            sacc[qq][j] = pr;
-            dpacc[qq][j] = pr * (dpacc[qq][j] - s_dsum[ql]);
-          }
+          for (int i = 0; i < 8; ++i) { pv[i] = sacc[8 * hh + i]; dsv[i] = dpacc[8 * hh + i]; }
+          const bf16x8_t bp = pack_bf16x8(pv), bds = pack_bf16x8(dsv);
+          // dO^T and Q^T operands of this 16-query step, two output tiles at a time.
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq)
+          for (int t0 = 0; t0 < NDT; t0 += 2) {
+            u32x2_t lo[2][2], hi[2][2];   // [dO, Q][tile]
 #pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            float pv[8], dsv[8];
+            for (int i = 0; i < 2; ++i) {
+              tr_issue_p<D>(make_uint2(obase + 2 * toff[t0 + i].x, obase + 2 * toff[t0 + i].y), hh, lo[0][i], hi[0][i]);
+              tr_issue_p<D>(make_uint2(qbase + 2 * toff[t0 + i].x, qbase + 2 * toff[t0 + i].y), hh, lo[1][i], hi[1][i]);
+            }
+            tr_wait_all<2>(lo, hi);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) { pv[i] = sacc[qq][8 * hh + i]; dsv[i] = dpacc[qq][8 * hh + i]; }
-            const bf16x8_t bp = pack_bf16x8(pv), bds = pack_bf16x8(dsv);
-#pragma unroll
-            for (int t = 0; t < NDT; ++t) {
-              dv[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm_t(Ot, t * 32 + lq, qq * 4 + 2 * hh, g), bp,
-                                                               dv[t], 0, 0, 0);
-              dk[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_perm_t(Qt, t * 32 + lq, qq * 4 + 2 * hh, g), bds,
-                                                               dk[t], 0, 0, 0);
+            for (int i = 0; i < 2; ++i) {
+              dv[t0 + i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(lo[0][i], hi[0][i]), bp, dv[t0 + i], 0, 0, 0);
+              dk[t0 + i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(lo[1][i], hi[1][i]), bds, dk[t0 + i], 0, 0, 0);
             }
           }
+        }
       }
     }
   }
@@ -879,6 +856,7 @@ __global__ __launch_bounds__(256) void attn_dkv_bf16_kernel(const AttnArgs p) {
       }
   }
 }
+
 
 // ---------------------------------------------------------------------------------------
 // fp32 kernels (fp32 parity mode): one wavefront per (row, head), keys walked one at a time.
@@ -1055,6 +1033,17 @@ static void launch_dq(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
 }
 
 template <int D>
+static void launch_dkv(unsigned blocks, hipStream_t st, const AttnArgs& a) {
+  constexpr size_t lds = 4 * 2 * 32 * D * sizeof(bf16_t);
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)attn_dkv_bf16_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    configured = true;
+  }
+  hipLaunchKernelGGL(attn_dkv_bf16_kernel<D>, dim3(blocks), dim3(256), lds, st, a);
+}
+
+template <int D>
 static void launch_fwd(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
   if (attn_qg() == 2) launch_fwd_t<D, 2>(Mq, Hq, st, a);
   else launch_fwd_t<D, 1>(Mq, Hq, st, a);
@@ -1129,7 +1118,7 @@ UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D
   rc = unok::check_launch("attn_dq_bf16");
   if (rc || !want_kv) return rc;
   const unsigned kblocks = (unsigned)(((Mk2 + 127) / 128) * Hkv);
-  if (D == 128) hipLaunchKernelGGL(attn_dkv_bf16_kernel<128>, dim3(kblocks), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(attn_dkv_bf16_kernel<64>, dim3(kblocks), dim3(256), 0, st, a);
+  if (D == 128) launch_dkv<128>(kblocks, st, a);
+  else launch_dkv<64>(kblocks, st, a);
   return unok::check_launch("attn_dkv_bf16");
 }
