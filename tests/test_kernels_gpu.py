@@ -228,11 +228,15 @@ class _Head:
         self.weight_t = w.t().contiguous()
 
 
+@pytest.mark.parametrize("keep", [True, False], ids=["kept_logits", "recomputed_logits"])
 @pytest.mark.parametrize("dtype,R,H,V,chunk", [(torch.float32, 50, 64, 5000, 2048),
                                                (torch.bfloat16, 300, 256, 8192, 3000),
                                                (torch.bfloat16, 1000, 512, 151936, 16384)])
-def test_chunked_weighted_ce(dev, dtype, R, H, V, chunk):
+def test_chunked_weighted_ce(dev, dtype, R, H, V, chunk, keep, monkeypatch):
+    from uno_amd import objectives
     from uno_amd.objectives import fused_weighted_ce, teacher_argmax
+    # both backward paths: logits kept from the forward, or recomputed chunk by chunk
+    monkeypatch.setattr(objectives, "CE_KEEP_LOGITS_BYTES", (16 << 30) if keep else 0)
     torch.manual_seed(5)
     h = (torch.randn(R, H, device=dev) * 0.5).to(dtype)
     w = (torch.randn(V, H, device=dev) * 0.05).to(dtype)

@@ -1,10 +1,12 @@
 """LM-head objectives of the Uno step on the HIP kernels.
 
 * ``fused_weighted_ce``: CE with the diffusion 1/t weighting (training/trainer.py:267-283),
-  evaluated over vocabulary chunks: each chunk's logits are produced by the MFMA GEMM into a
-  chunk buffer and folded into a running per-row log-sum-exp; the backward recomputes each
-  chunk and feeds dz = g w (softmax - onehot) straight into the data-gradient GEMM. The full
-  [rows x vocab] logits are never materialised.
+  evaluated over vocabulary chunks: each chunk's logits are produced by the MFMA GEMM and folded
+  into a running per-row log-sum-exp; the backward turns each chunk into dz = g w (softmax -
+  onehot) and feeds it straight into the data-gradient GEMM. When the fp32 logits of all rows fit
+  in CE_KEEP_LOGITS_BYTES (4.6 GB for the 7.6K supervised rows x 151936 vocabulary of the 4 x 4096
+  step) the vocabulary is one chunk and its logits are kept from the forward to the backward (no
+  recomputation); otherwise a chunk buffer is reused and the backward recomputes each chunk.
 * ``teacher_argmax``: first-index argmax of the clean-stream logits, chunked the same way
   (training/losses.py:38-56, target source "clean_argmax").
 * ``distribution_losses``: reverse KL and total variation (training/losses.py:59-183) over
@@ -18,6 +20,8 @@ from . import _native as N
 from . import kernels as K
 
 DEFAULT_CE_CHUNK = 16384
+# Largest fp32 [rows x vocab] logits buffer kept between the CE forward and backward.
+CE_KEEP_LOGITS_BYTES = 16 << 30
 
 
 def lm_head_logits(lm_head, x: torch.Tensor) -> torch.Tensor:
@@ -56,30 +60,36 @@ class ChunkedWeightedCE(torch.autograd.Function):
         run_max, run_sum, zt = torch.empty(R, **f32), torch.empty(R, **f32), torch.zeros(R, **f32)
         lse = torch.empty(R, **f32)
         loss = torch.empty((), **f32)
-        buf = torch.empty((R, min(chunk, V)), **f32)
+        keep = R * V * 4 <= CE_KEEP_LOGITS_BYTES
+        if keep:
+            chunk = V   # one GEMM over the whole vocabulary, no partial last wave of tiles per chunk
+        buf = torch.empty((R, V if keep else min(chunk, V)), **f32)
         for i, (c0, c1) in enumerate(_chunks(V, chunk)):
-            z = buf[:, :c1 - c0]
+            z = buf[:, c0:c1] if keep else buf[:, :c1 - c0]
             K.gemm_nt(h, w_lm[c0:c1], out=z)
             N.call("unok_row_lse_update", N.F32, R, c1 - c0, N.ptr(z), buf.stride(0), c0, N.ptr(targets),
                    N.ptr(run_max), N.ptr(run_sum), N.ptr(zt), int(i == 0), N.stream())
         N.call("unok_ce_finish", R, N.ptr(run_max), N.ptr(run_sum), N.ptr(zt), N.ptr(weights), N.ptr(inv_n),
                N.ptr(lse), N.ptr(loss), N.stream())
-        ctx.save = (h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk)
+        ctx.save = (h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, buf if keep else None)
         return loss
 
     @staticmethod
     def backward(ctx, g):
-        h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk = ctx.save
+        h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, kept = ctx.save
         ctx.save = None
         R, V = h.shape[0], w_lm.shape[0]
         g = g.reshape(1).float().contiguous()
         f32 = dict(device=h.device, dtype=torch.float32)
-        buf = torch.empty((R, min(chunk, V)), **f32)
+        buf = kept if kept is not None else torch.empty((R, min(chunk, V)), **f32)
         dz = torch.empty((R, min(chunk, V)), device=h.device, dtype=h.dtype)
         dh = torch.zeros(h.shape, **f32)
         for c0, c1 in _chunks(V, chunk):
-            z = buf[:, :c1 - c0]
-            K.gemm_nt(h, w_lm[c0:c1], out=z)
+            if kept is not None:
+                z = buf[:, c0:c1]
+            else:
+                z = buf[:, :c1 - c0]
+                K.gemm_nt(h, w_lm[c0:c1], out=z)
             d = dz[:, :c1 - c0]
             N.call("unok_ce_grad_chunk", N.dtype_code(h.dtype), R, c1 - c0, N.ptr(z), buf.stride(0), c0, N.ptr(lse),
                    N.ptr(targets), N.ptr(weights), N.ptr(g), N.ptr(inv_n), N.ptr(d), dz.stride(0), N.stream())
