@@ -16,6 +16,7 @@
 // The LoRA weight gradients dB = s h^T dY and dA = g^T x are "TN" products (reduction over
 // token rows); gemm_tn computes them with split-K partials into a caller workspace.
 #include "common.h"
+#include "lds_tile.h"
 
 #include <stdlib.h>
 #include <type_traits>
@@ -1477,10 +1478,153 @@ static int tn_skinny_splits(int Mrows, int NX) {
   return nz < 1 ? 1 : nz;
 }
 
+// Skinny TN product with both operands read as columns of row-major LDS tiles: per workgroup,
+// out tile [NS x 128] (rows s of the skinny operand S, columns x0 .. x0 + 127 of the wide operand
+// X) over one split of the token rows. 64-row tiles of X (128 columns) and S (NS columns) stream
+// into two LDS stages by direct-to-LDS loads (kswz-swizzled rows); every MFMA operand is an LDS
+// transpose load of 16 rows (the same permuted row order for both operands, so the products
+// pair up). Wave w owns x columns x0 + 32 w .. + 31 and all NS / 32 row blocks. Partials are
+// written in the layout of gemm_tn_skinny_kernel, for the same split-K reduction. Three
+// workgroups per CU for NS = 64 (48 KB of LDS each), so the split counts of the LoRA shapes
+// (e.g. 96 strips x 6 splits for 12288 columns) run in one round.
+template <int NS, bool TOUT>
+__global__ __launch_bounds__(256, NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const GemmTNSkinny p) {
+  constexpr int BK = 64, XB = 128, TS = NS / 32;
+  static_assert(NS == 64 || NS == 128, "swizzled transpose tiles are defined for 64 and 128 columns");
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  bf16_t* Xs = smem;                   // [2][BK * XB]
+  bf16_t* Ss = smem + 2 * BK * XB;     // [2][BK * NS]
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, lq = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(w);
+  const int nstrip = (p.NX + XB - 1) / XB;
+  const int lin = xcd_remap(blockIdx.x, gridDim.x);
+  const int x0 = (lin % nstrip) * XB, z = lin / nstrip;
+  const int mbeg = z * p.rows_per_split;
+  const int mend = min(p.Mrows, mbeg + p.rows_per_split);
+  const int nt = mend > mbeg ? (mend - mbeg + BK - 1) / BK : 0;
+  const uint32_t xo = dma_lane_off<XB>(p.ldx, x0, wid, lane), so = dma_lane_off<NS>(p.lds, 0, wid, lane);
+  auto fetch = [&](int t) {
+    const int m0 = mbeg + t * BK;
+    dma_tile<XB>(p.X, p.ldx, xo, m0, mend, Xs + (t & 1) * BK * XB, wid);
+    dma_tile<NS>(p.S, p.lds, so, m0, mend, Ss + (t & 1) * BK * NS, wid);
+  };
+  const int2 xoff = tr_frag_off<XB>(w, lane);
+  int2 soff[TS];
+#pragma unroll
+  for (int i = 0; i < TS; ++i) soff[i] = tr_frag_off<NS>(i, lane);
+  f32x16_t acc[TS];
+#pragma unroll
+  for (int i = 0; i < TS; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+  if (nt > 0) fetch(0);
+#pragma unroll 1
+  for (int t = 0; t < nt; ++t) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();                       // tile t in LDS; every wave is done with tile t-1
+    if (t + 1 < nt) fetch(t + 1);
+    const uint32_t xb = lds_addr(Xs + (t & 1) * BK * XB), sb = lds_addr(Ss + (t & 1) * BK * NS);
+    // All operands of the tile's four 16-row steps, then one wait, then the MFMAs.
+    u32x2_t xl[4], xh[4], sl[4][TS], sh[4][TS];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      tr_issue_p<XB>(make_uint2(xb + 2 * xoff.x, xb + 2 * xoff.y), q, xl[q], xh[q]);
+#pragma unroll
+      for (int i = 0; i < TS; ++i)
+        tr_issue_p<NS>(make_uint2(sb + 2 * soff[i].x, sb + 2 * soff[i].y), q, sl[q][i], sh[q][i]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // The results pass through these empty statements after the wait, so nothing reads them earlier.
+      asm volatile("" : "+v"(xl[q]), "+v"(xh[q]));
+      const bf16x8_t xf = tr_join(xl[q], xh[q]);
+#pragma unroll
+      for (int i = 0; i < TS; ++i) {
+        asm volatile("" : "+v"(sl[q][i]), "+v"(sh[q][i]));
+        const bf16x8_t sf = tr_join(sl[q][i], sh[q][i]);
+        acc[i] = TOUT ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf, sf, acc[i], 0, 0, 0)
+                      : __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf, xf, acc[i], 0, 0, 0);
+      }
+    }
+  }
+
+  if (TOUT) {
+    // acc[i][r] = result[x = x0 + 32 w + 8 (r / 4) + 4 g + r % 4][s = 32 i + lq]
+    float* W = p.WS + (int64_t)z * p.NX * NS;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int x = x0 + w * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+      if (x < p.NX) {
+#pragma unroll
+        for (int i = 0; i < TS; ++i) W[(int64_t)x * NS + i * 32 + lq] = acc[i][r] * p.alpha;
+      }
+    }
+  } else {
+    // acc[i][r] = result[s = 32 i + 8 (r / 4) + 4 g + r % 4][x = x0 + 32 w + lq]
+    const int col = x0 + w * 32 + lq;
+    if (col < p.NX) {
+      float* W = p.WS + (int64_t)z * NS * p.NX + col;
+#pragma unroll
+      for (int i = 0; i < TS; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = i * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+          W[(int64_t)row * p.NX] = acc[i][r] * p.alpha;
+        }
+    }
+  }
+}
+
+// Skinny TN kernel choice: 1 = transpose-load kernel for NS in {64, 128} (default), 0 = the
+// register-transposing kernel for every NS. UNOK_TN_CFG selects, for tuning.
+static int tn_cfg() {
+  static int c = [] {
+    const char* e = getenv("UNOK_TN_CFG");
+    return (e && atoi(e) == 0) ? 0 : 1;
+  }();
+  return c;
+}
+
+template <int NS>
+static void launch_tn_tr_t(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
+  constexpr size_t lds = 2 * 64 * (128 + NS) * sizeof(bf16_t);
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)gemm_tn_tr_kernel<NS, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)gemm_tn_tr_kernel<NS, false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    configured = true;
+  }
+  const int nstrip = (p.NX + 127) / 128;
+  if (tout)
+    hipLaunchKernelGGL((gemm_tn_tr_kernel<NS, true>), dim3(nstrip * nz), dim3(256), lds, st, p);
+  else
+    hipLaunchKernelGGL((gemm_tn_tr_kernel<NS, false>), dim3(nstrip * nz), dim3(256), lds, st, p);
+}
+
+// Row splits of the transpose-load TN kernel: about one round of workgroups (3 per CU for NS = 64,
+// 2 for NS = 128 on 256 CUs), at most 16 splits for wide sides (2048 columns and more, where the
+// partials and their reduction would grow faster than the parallelism helps) and 64 otherwise,
+// at least 256 rows per split.
+static int tn_tr_splits(int Mrows, int NX, int NS) {
+  const int nstrip = (NX + 127) / 128;
+  const int slots = NS == 64 ? 768 : 512;
+  int nz = slots / nstrip;
+  const int cap = NX >= 2048 ? 16 : 64;
+  if (nz > cap) nz = cap;
+  const int max_split = (Mrows + 255) / 256;
+  if (nz > max_split) nz = max_split;
+  return nz < 1 ? 1 : nz;
+}
+
 UNOK_EXPORT int64_t unok_gemm_tn_workspace(int Mrows, int P, int Q) {
   const int a = tn_general_splits(Mrows, P, Q);
   const int b = tn_skinny_splits(Mrows, P <= Q ? Q : P);
-  return (int64_t)(a > b ? a : b) * P * Q * 4;
+  const int c = tn_tr_splits(Mrows, P <= Q ? Q : P, P <= Q ? P : Q);
+  int m = a > b ? a : b;
+  if (c > m) m = c;
+  return (int64_t)m * P * Q * 4;
 }
 
 template <int NS>
@@ -1493,6 +1637,8 @@ static void launch_tn_skinny_t(const GemmTNSkinny& p, int nz, bool tout, hipStre
 }
 
 static void launch_tn_skinny(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
+  if (tn_cfg() == 1 && p.NS == 64) { launch_tn_tr_t<64>(p, nz, tout, st); return; }
+  if (tn_cfg() == 1 && p.NS == 128) { launch_tn_tr_t<128>(p, nz, tout, st); return; }
   switch (p.NS) {
     case 32: launch_tn_skinny_t<32>(p, nz, tout, st); break;
     case 64: launch_tn_skinny_t<64>(p, nz, tout, st); break;
@@ -1524,7 +1670,8 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
     const void* X = a_small ? B : A;
     if (NS % 32 == 0 && NS <= 256 && NX >= TNS_QB && NX % 8 == 0 && lds_ % 8 == 0 && ldx % 8 == 0 &&
         aligned16(S) && aligned16(X)) {
-      const int nz0 = tn_skinny_splits(Mrows, NX);
+      const bool tr = tn_cfg() == 1 && (NS == 64 || NS == 128);
+      const int nz0 = tr ? tn_tr_splits(Mrows, NX, NS) : tn_skinny_splits(Mrows, NX);
       int rps = (Mrows + nz0 - 1) / nz0;
       rps = ((rps + TNS_BK - 1) / TNS_BK) * TNS_BK;
       const int nz = (Mrows + rps - 1) / rps;
