@@ -45,6 +45,15 @@ int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
                  void* C, int64_t ldc, const void* R, int64_t ldr,
                  const uint8_t* gate, float alpha, void* stream);
 
+/* C[M, N/2] = silu(G) (.) U of the gate/up product A[M,K] B[N,K]^T, bf16, for B with 64-row
+ * interleaved gate/up rows (rows 128 b + [0, 64): gate features 64 b + [0, 64); rows
+ * 128 b + [64, 128): the same up features); rounded exactly as unok_gemm_nt followed by
+ * unok_swiglu_fwd. M and N multiples of 256, K of 64. Clean-stream (forward-only) MLP of the
+ * remote Qwen3 decoder: down_proj input act_fn(gate_proj(x)) * up_proj(x)
+ * (modeling_qwen3.py:81-82). */
+int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
+                        void* C, int64_t ldc, void* stream);
+
 /* C[P,Q] (fp32) = beta * C + alpha * A[Mrows,P]^T B[Mrows,Q] (split-K over rows through a
  * caller workspace of unok_gemm_tn_workspace() bytes). LoRA weight gradients
  * dB = s dY^T h, dA = g^T x. Replaces: autograd of lora_A / lora_B (peft 0.15.2) under

@@ -162,3 +162,24 @@ def test_gemm_strided_views(dev):
     torch.cuda.synchronize()
     assert _rel(out, a.float() @ b.float().T) < 8e-3
     assert out_big[:, :64].abs().sum().item() == 0 and out_big[:, 384:].abs().sum().item() == 0
+
+
+@pytest.mark.parametrize("M,F,Kd", [(512, 512, 256), (1024, 1536, 512), (256, 128, 64)])
+def test_gemm_nt_swiglu_matches_unfused(dev, M, F, Kd):
+    """Gate/up product with SwiGLU in the GEMM epilogue (64-row interleaved weights) equals the
+    plain product on the [gate; up] layout followed by the SwiGLU kernel, bit for bit."""
+    torch.manual_seed(M + F)
+    x = (torch.randn(M, Kd, device=dev) * 0.5).bfloat16()
+    w = (torch.randn(2 * F, Kd, device=dev) * 0.1).bfloat16()
+    ref = K.swiglu_fwd(K.gemm_nt(x, w), F)
+    fused = K.gemm_nt_swiglu(x, K.interleave_gate_up(w, F))
+    torch.cuda.synchronize()
+    assert fused.shape == (M, F)
+    assert torch.equal(fused, ref)
+
+
+def test_gemm_nt_swiglu_rejects_unaligned_shapes(dev):
+    x = torch.randn(300, 64, device=dev).bfloat16()
+    w = torch.randn(256, 64, device=dev).bfloat16()
+    with pytest.raises(ValueError, match="multiples of 256"):
+        K.gemm_nt_swiglu(x, w)

@@ -122,6 +122,10 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return r;
 }
 
+// Logistic function of the SwiGLU gate (one definition, so the fused GEMM epilogue and the
+// stand-alone SwiGLU kernel round identically).
+__device__ __forceinline__ float sigmoidf_(float g) { return 1.f / (1.f + expf(-g)); }
+
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
 

@@ -1068,7 +1068,7 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 // 8 B fragment reads (16 bytes per lane) and 64 MFMAs. With the B fragment as the first operand,
 // lane l holds C[row 16i + l % 16][cols 16j + 4 (l / 16) + 0..3] of accumulator (i, j).
 // ---------------------------------------------------------------------------------------
-template <typename OutT>
+template <typename OutT, bool SWIGLU = false>
 __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p) {
   constexpr int BM = 256, BN = 256, BK = 64, NW = 4, TM = 8, TN = 8;
   constexpr int CPR = BK / 8, RPI = 64 / CPR, INS = BM / (RPI * NW);   // 8 loads per operand and wave
@@ -1228,6 +1228,30 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
       }
     }
   };
+  if constexpr (SWIGLU) {
+    // Gate/up product with 64-row interleaved weights (rows 128 b + [0, 64) = gate features
+    // 64 b + [0, 64), rows 128 b + [64, 128) = the same up features): the wave's 128 columns are
+    // one such pair, accumulator j < 4 the gate and j + 4 the up value of the same feature. Writes
+    // C[row][64 b + c] = bf16(bf16(silu(g)) u) with g, u rounded to bf16 first, as a bf16 GEMM
+    // followed by the SwiGLU kernel computes it. Interior tiles only (checked by the caller).
+    const int f0 = (n0 + wn * 128) / 2;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      OutT* crow = C + (int64_t)(m0 + wm * 128 + i * 16 + lr) * p.ldc;
+#pragma unroll
+      for (int j = 0; j < TN / 2; ++j) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float gv = bf16_to_f32(f32_to_bf16(acc[i][j][q] * p.alpha));
+          const float uv = bf16_to_f32(f32_to_bf16(acc[i][j + TN / 2][q] * p.alpha));
+          v[q] = bf16_to_f32(f32_to_bf16(gv * sigmoidf_(gv))) * uv;
+        }
+        store4(crow + f0 + j * 16 + lk * 4, nullptr, v);
+      }
+    }
+    return;
+  }
   const bool interior = m0 + BM <= p.M && n0 + BN <= p.N && p.gate == nullptr;
   if (R) {
     if (interior) epilogue(std::true_type{}, std::false_type{}); else epilogue(std::true_type{}, std::true_type{});
@@ -1236,17 +1260,17 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
   }
 }
 
-template <typename OutT>
+template <typename OutT, bool SWIGLU = false>
 static void launch_nt_w4m16(const GemmNT& p, hipStream_t st) {
   constexpr size_t lds = 2 * (256 + 256) * 64 * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4m16_kernel<OutT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)lds);
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4m16_kernel<OutT, SWIGLU>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
   const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  hipLaunchKernelGGL((gemm_nt_bf16_w4m16_kernel<OutT>), dim3(nb), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((gemm_nt_bf16_w4m16_kernel<OutT, SWIGLU>), dim3(nb), dim3(256), lds, st, p);
 }
 
 // Configuration of the 256x256 direct-to-LDS kernel (UNOK_GEMM_CFG selects one, for tuning):
@@ -1355,6 +1379,27 @@ static void launch_nt_dma(const GemmNT& p, int out_dtype, hipStream_t st) {
 // C = alpha * gate (.) (A B^T + A2[:, seg_col] B2^T) + R.
 // in_dtype: dtype of A, B, A2, B2; out_dtype: dtype of C and R.
 // seg_end/seg_col: `nseg` (<= 4) extension segments over N (ignored when A2 is null).
+// C[M, N/2] = silu(G) * U for the gate/up product A[M,K] B[N,K]^T with 64-row interleaved B (rows
+// 128 b + [0, 64) gate, 128 b + [64, 128) up of features 64 b + [0, 64)), bf16, rounded as the
+// unfused product followed by unok_swiglu_fwd. M and N multiples of 256, K of 64.
+UNOK_EXPORT int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
+                                    void* C, int64_t ldc, void* stream) {
+  UNOK_REQUIRE(M >= 0 && N >= 0 && K >= 0, UNOK_EINVAL, "gemm_nt_swiglu: negative size M=%d N=%d K=%d", M, N, K);
+  if (M == 0 || N == 0) return 0;
+  UNOK_REQUIRE(M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && K > 0, UNOK_EINVAL,
+               "gemm_nt_swiglu: M=%d and N=%d must be multiples of 256, K=%d of 64", M, N, K);
+  UNOK_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldc % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(C),
+               UNOK_EALIGN, "gemm_nt_swiglu: row strides must be multiples of 8 and rows 16-byte aligned");
+  GemmNT p{};
+  p.A = A; p.lda = lda; p.B = B; p.ldb = ldb;
+  p.C = C; p.ldc = ldc;
+  p.M = M; p.N = N; p.K = K; p.alpha = 1.f; p.nseg = 1;
+  for (int i = 0; i < 4; ++i) { p.seg_end[i] = N; p.seg_col[i] = 0; }
+  UNOK_REQUIRE(buffer_ranges_ok(p), UNOK_EINVAL, "gemm_nt_swiglu: operands exceed 32-bit buffer offsets");
+  launch_nt_w4m16<bf16_t, true>(p, (hipStream_t)stream);
+  return unok::check_launch("gemm_nt_swiglu");
+}
+
 UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
                              const void* A, int64_t lda, const void* B, int64_t ldb,
                              const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,

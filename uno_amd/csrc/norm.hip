@@ -288,7 +288,6 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const T* __restric
 // ---------------------------------------------------------------------------------------
 // SwiGLU on the fused gate|up projection: out = round(silu(g)) * u.
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float sigmoidf_(float g) { return 1.f / (1.f + expf(-g)); }
 
 template <typename T>
 __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const T* __restrict__ gu, int64_t ld, T* __restrict__ out,

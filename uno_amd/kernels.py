@@ -205,6 +205,34 @@ def qknorm_rope_bwd(dq, dk, qkv, nq, nk, d, wq, wk, pos, inv_freq, rstd, dqkv):
     return dqkv
 
 
+def gemm_nt_swiglu(a: torch.Tensor, b_interleaved: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up of a @ b.T for gate/up weight rows interleaved in blocks of 64
+    (``interleave_gate_up``); bf16, M and the row count of b multiples of 256."""
+    _rowmajor(a, "a")
+    _rowmajor(b_interleaved, "b")
+    M, K = a.shape
+    rows = b_interleaved.shape[0]
+    if b_interleaved.shape[1] != K or a.dtype != torch.bfloat16 or b_interleaved.dtype != torch.bfloat16:
+        raise RuntimeError("gemm_nt_swiglu: bf16 a [M,K] and b [N,K] required")
+    out = out if out is not None else torch.empty((M, rows // 2), device=a.device, dtype=a.dtype)
+    _rowmajor(out, "out")
+    N.call("unok_gemm_nt_swiglu", M, rows, K, N.ptr(a), _ld(a), N.ptr(b_interleaved), _ld(b_interleaved),
+           N.ptr(out), _ld(out), N.stream())
+    return out
+
+
+def swiglu_fused_ok(M: int, F: int, K: int) -> bool:
+    """Shapes the fused gate/up + SwiGLU product accepts."""
+    return M % 256 == 0 and (2 * F) % 256 == 0 and K % 64 == 0 and K > 0
+
+
+def interleave_gate_up(w_gu: torch.Tensor, F: int) -> torch.Tensor:
+    """[gate; up] rows [2F, H] -> rows interleaved in blocks of 64 (gate 64 b.., then up 64 b..)."""
+    H = w_gu.shape[1]
+    g, u = w_gu[:F].reshape(F // 64, 64, H), w_gu[F:].reshape(F // 64, 64, H)
+    return torch.stack((g, u), dim=1).reshape(2 * F, H).contiguous()
+
+
 def swiglu_fwd(gu, F, out=None):
     _rowmajor(gu, "gu")
     M = gu.shape[0]

@@ -40,6 +40,7 @@ class LayerWeights:
     ln_post: torch.Tensor
     q_norm: torch.Tensor | None
     k_norm: torch.Tensor | None
+    w_gu_i: torch.Tensor | None = None   # [2F, H], gate/up rows interleaved in blocks of 64
 
 
 @dataclass
@@ -82,8 +83,10 @@ def clean_layer(h: torch.Tensor, lw: LayerWeights, g: Geometry, sc: StreamContex
     o, _ = K.attn_fwd(q, k, v, sc.iv_clean, g.nq, g.nk, g.d)
     h1 = K.gemm_nt(o, lw.w_o, residual=h)
     x2, _ = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
-    gu = K.gemm_nt(x2, lw.w_gu)
-    s = K.swiglu_fwd(gu, g.F)
+    if lw.w_gu_i is not None and x2.dtype == torch.bfloat16 and K.swiglu_fused_ok(M, g.F, g.H):
+        s = K.gemm_nt_swiglu(x2, lw.w_gu_i)      # gate/up product with SwiGLU in its epilogue
+    else:
+        s = K.swiglu_fwd(K.gemm_nt(x2, lw.w_gu), g.F)
     h2 = K.gemm_nt(s, lw.w_d, residual=h1)
     return h2, k, v
 

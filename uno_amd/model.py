@@ -272,6 +272,10 @@ class UnoDecoderLayer(nn.Module):
         self.register_buffer("w_o_t", torch.zeros(q, H, **e), persistent=False)
         self.register_buffer("w_gu", torch.zeros(2 * F, H, **e), persistent=False)
         self.register_buffer("w_gu_t", torch.zeros(H, 2 * F, **e), persistent=False)
+        # gate/up rows interleaved in blocks of 64 for the fused clean-stream gate/up + SwiGLU
+        # product (when the shapes allow it)
+        fuse = F % 128 == 0 and dtype == torch.bfloat16
+        self.register_buffer("w_gu_i", torch.zeros(2 * F, H, **e) if fuse else None, persistent=False)
         self.register_buffer("w_d", torch.zeros(H, F, **e), persistent=False)
         self.register_buffer("w_d_t", torch.zeros(F, H, **e), persistent=False)
         self.q_norm_w = torch.ones(geo.d, **e) if cfg.qk_norm else None
@@ -285,12 +289,15 @@ class UnoDecoderLayer(nn.Module):
         qn = self.self_attn.q_norm.weight if hasattr(self.self_attn, "q_norm") else None
         kn = self.self_attn.k_norm.weight if hasattr(self.self_attn, "k_norm") else None
         return Lyr.LayerWeights(self.w_qkv, self.w_qkv_t, self.w_o, self.w_o_t, self.w_gu, self.w_gu_t, self.w_d,
-                                self.w_d_t, self.input_layernorm.weight, self.post_attention_layernorm.weight, qn, kn)
+                                self.w_d_t, self.input_layernorm.weight, self.post_attention_layernorm.weight, qn, kn,
+                                self.w_gu_i)
 
     @torch.no_grad()
     def refresh_transposed(self):
         for a, b in (("w_qkv", "w_qkv_t"), ("w_o", "w_o_t"), ("w_gu", "w_gu_t"), ("w_d", "w_d_t")):
             getattr(self, b).copy_(getattr(self, a).t())
+        if self.w_gu_i is not None:
+            self.w_gu_i.copy_(K.interleave_gate_up(self.w_gu, self.geo.F))
 
 
 class UnoQwen3Model(nn.Module):
