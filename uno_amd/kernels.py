@@ -216,8 +216,17 @@ def gemm_nt_swiglu(a: torch.Tensor, b_interleaved: torch.Tensor, out: torch.Tens
         raise RuntimeError("gemm_nt_swiglu: bf16 a [M,K] and b [N,K] required")
     out = out if out is not None else torch.empty((M, rows // 2), device=a.device, dtype=a.dtype)
     _rowmajor(out, "out")
+    rec = _recorder
+    if rec is not None and rec.predicate(a.dtype, M, rows, K, 0, [rows]):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    else:
+        rec = None
     N.call("unok_gemm_nt_swiglu", M, rows, K, N.ptr(a), _ld(a), N.ptr(b_interleaved), _ld(b_interleaved),
            N.ptr(out), _ld(out), N.stream())
+    if rec is not None:
+        ev1.record()
+        rec.records.append((ev0, ev1, 2.0 * M * rows * K))
     return out
 
 
