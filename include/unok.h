@@ -54,6 +54,15 @@ int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
 int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
                         void* C, int64_t ldc, void* stream);
 
+/* dgu[M, 2F] = SwiGLU backward of dS = A[M,K] B[F,K]^T + A2[M,K2] B2[F,K2]^T against
+ * gu[M, 2F] = [gate | up] (dS is never stored); bf16, rounded exactly as unok_gemm_nt followed by
+ * unok_swiglu_bwd. M and F multiples of 256, K and K2 of 64. Backward of the remote decoder's MLP
+ * act_fn(gate_proj(x)) * up_proj(x) through down_proj (modeling_qwen3.py:81-82) with the LoRA
+ * data-gradient extension of down_proj (peft 0.15.2 lora.Linear). */
+int unok_gemm_nt_swiglu_bwd(int M, int F, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
+                            const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,
+                            const void* gu, int64_t ldgu, void* dgu, int64_t lddgu, void* stream);
+
 /* C[P,Q] (fp32) = beta * C + alpha * A[Mrows,P]^T B[Mrows,Q] (split-K over rows through a
  * caller workspace of unok_gemm_tn_workspace() bytes). LoRA weight gradients
  * dB = s dY^T h, dA = g^T x. Replaces: autograd of lora_A / lora_B (peft 0.15.2) under

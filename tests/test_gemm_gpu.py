@@ -183,3 +183,20 @@ def test_gemm_nt_swiglu_rejects_unaligned_shapes(dev):
     w = torch.randn(256, 64, device=dev).bfloat16()
     with pytest.raises(ValueError, match="multiples of 256"):
         K.gemm_nt_swiglu(x, w)
+
+
+@pytest.mark.parametrize("M,F,Kd,K2", [(512, 512, 256, 64), (1024, 1536, 512, 64), (256, 256, 128, 0)])
+def test_gemm_nt_swiglu_bwd_matches_unfused(dev, M, F, Kd, K2):
+    """SwiGLU backward in the epilogue of the down-projection data-gradient GEMM (with the LoRA
+    K-extension) equals the product followed by the SwiGLU backward kernel, bit for bit."""
+    torch.manual_seed(M + F + K2)
+    dy = (torch.randn(M, Kd, device=dev) * 0.5).bfloat16()
+    wt = (torch.randn(F, Kd, device=dev) * 0.1).bfloat16()
+    gu = (torch.randn(M, 2 * F, device=dev) * 2.0).bfloat16()
+    a2 = (torch.randn(M, K2, device=dev) * 0.5).bfloat16() if K2 else None
+    b2 = (torch.randn(F, K2, device=dev) * 0.1).bfloat16() if K2 else None
+    ds = K.gemm_nt(dy, wt, a2=a2, b2=b2)
+    ref = K.swiglu_bwd(ds, gu, F)
+    fused = K.gemm_nt_swiglu_bwd(dy, wt, a2, b2, gu)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, ref)

@@ -126,6 +126,15 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // stand-alone SwiGLU kernel round identically).
 __device__ __forceinline__ float sigmoidf_(float g) { return 1.f / (1.f + expf(-g)); }
 
+// Gradients of out = bf16(silu(g)) * u for upstream d: the same expression in the SwiGLU backward
+// kernel and the fused GEMM epilogue, so both round identically.
+__device__ __forceinline__ void swiglu_grad(float d, float g, float u, float& dg, float& du) {
+  const float sg = sigmoidf_(g);
+  const float silu = bf16_to_f32(f32_to_bf16(g * sg));
+  du = d * silu;
+  dg = d * u * sg * (1.f + g * (1.f - sg));
+}
+
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM = 0x010, SG_DS_READ = 0x100;
 

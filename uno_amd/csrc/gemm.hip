@@ -1068,7 +1068,7 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 // 8 B fragment reads (16 bytes per lane) and 64 MFMAs. With the B fragment as the first operand,
 // lane l holds C[row 16i + l % 16][cols 16j + 4 (l / 16) + 0..3] of accumulator (i, j).
 // ---------------------------------------------------------------------------------------
-template <typename OutT, bool SWIGLU = false>
+template <typename OutT, int EPI = 0>
 __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p) {
   constexpr int BM = 256, BN = 256, BK = 64, NW = 4, TM = 8, TN = 8;
   constexpr int CPR = BK / 8, RPI = 64 / CPR, INS = BM / (RPI * NW);   // 8 loads per operand and wave
@@ -1228,7 +1228,76 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
       }
     }
   };
-  if constexpr (SWIGLU) {
+  if constexpr (EPI == 2) {
+    // SwiGLU backward of the down-projection data gradient: this product is dS[M, F] (never
+    // stored); with R = gu [M, 2F] (ldr) and C = dgu [M, 2F] (ldc), writes dgu[:, f] and
+    // dgu[:, F + f] from bf16(dS), g = gu[:, f], u = gu[:, F + f], as the SwiGLU backward kernel
+    // does after a bf16 product. Interior tiles only (checked by the caller). Each wave rounds its
+    // 128 x 128 quadrant of dS into a private 32 KB of the (now idle) LDS stages, 16-byte chunks
+    // XOR-swizzled by row so that both the fragment-ordered writes and the row-ordered reads are
+    // conflict-free, then walks it four rows per step: every gu load and dgu store is a 256-byte
+    // run per row (16 bytes per lane), with the gu loads of the next eight rows in flight.
+    constexpr int PB = 2, NBATCH = 128 / (4 * PB);
+    const int F = p.N;
+    const int rsub = lane >> 4, c16 = lane & 15;
+    const int64_t row0 = m0 + wm * 128 + rsub;
+    const int col = n0 + wn * 128 + c16 * 8;
+    const bf16_t* gsrc = (const bf16_t*)p.R + row0 * p.ldr + col;
+    bf16_t* dst = (bf16_t*)p.C + row0 * p.ldc + col;
+    uint4 gw[2][PB], uw[2][PB];
+    auto load_batch = [&](int b, int buf) {
+#pragma unroll
+      for (int t = 0; t < PB; ++t) {
+        const bf16_t* g = gsrc + (int64_t)((b * PB + t) * 4) * p.ldr;
+        gw[buf][t] = *(const uint4*)g;
+        uw[buf][t] = *(const uint4*)(g + F);
+      }
+    };
+    load_batch(0, 0);
+    asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed (waited above)
+    bf16_t* q = smem + wid * 128 * 128;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        uint2 w;
+        w.x = (uint32_t)f32_to_bf16(acc[i][j][0] * p.alpha) | ((uint32_t)f32_to_bf16(acc[i][j][1] * p.alpha) << 16);
+        w.y = (uint32_t)f32_to_bf16(acc[i][j][2] * p.alpha) | ((uint32_t)f32_to_bf16(acc[i][j][3] * p.alpha) << 16);
+        *(uint2*)&q[(i * 16 + lr) * 128 + (((2 * j + (lk >> 1)) ^ lr) << 3) + (lk & 1) * 4] = w;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < NBATCH; ++b) {
+      if (b + 1 < NBATCH) load_batch(b + 1, (b + 1) & 1);
+#pragma unroll
+      for (int t = 0; t < PB; ++t) {
+        const int r = (b * PB + t) * 4 + rsub;
+        const uint4 dw = *(const uint4*)&q[r * 128 + ((c16 ^ (r & 15)) << 3)];
+        const bf16_t* dv = (const bf16_t*)&dw;
+        const bf16_t* gv = (const bf16_t*)&gw[b & 1][t];
+        const bf16_t* uv = (const bf16_t*)&uw[b & 1][t];
+        float dg[8], du[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          swiglu_grad(bf16_to_f32(dv[e]), bf16_to_f32(gv[e]), bf16_to_f32(uv[e]), dg[e], du[e]);
+        uint4 og, ou;
+        uint32_t* pg = (uint32_t*)&og;
+        uint32_t* pu = (uint32_t*)&ou;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pg[e] = (uint32_t)f32_to_bf16(dg[2 * e]) | ((uint32_t)f32_to_bf16(dg[2 * e + 1]) << 16);
+          pu[e] = (uint32_t)f32_to_bf16(du[2 * e]) | ((uint32_t)f32_to_bf16(du[2 * e + 1]) << 16);
+        }
+        bf16_t* d = dst + (int64_t)((b * PB + t) * 4) * p.ldc;
+        *(uint4*)d = og;
+        *(uint4*)(d + F) = ou;
+      }
+    }
+    return;
+  }
+  if constexpr (EPI == 1) {
     // Gate/up product with 64-row interleaved weights (rows 128 b + [0, 64) = gate features
     // 64 b + [0, 64), rows 128 b + [64, 128) = the same up features): the wave's 128 columns are
     // one such pair, accumulator j < 4 the gate and j + 4 the up value of the same feature. Writes
@@ -1260,17 +1329,17 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
   }
 }
 
-template <typename OutT, bool SWIGLU = false>
+template <typename OutT, int EPI = 0>
 static void launch_nt_w4m16(const GemmNT& p, hipStream_t st) {
   constexpr size_t lds = 2 * (256 + 256) * 64 * sizeof(bf16_t);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4m16_kernel<OutT, SWIGLU>,
+    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4m16_kernel<OutT, EPI>,
                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
   const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  hipLaunchKernelGGL((gemm_nt_bf16_w4m16_kernel<OutT, SWIGLU>), dim3(nb), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((gemm_nt_bf16_w4m16_kernel<OutT, EPI>), dim3(nb), dim3(256), lds, st, p);
 }
 
 // Configuration of the 256x256 direct-to-LDS kernel (UNOK_GEMM_CFG selects one, for tuning):
@@ -1396,8 +1465,34 @@ UNOK_EXPORT int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t 
   p.M = M; p.N = N; p.K = K; p.alpha = 1.f; p.nseg = 1;
   for (int i = 0; i < 4; ++i) { p.seg_end[i] = N; p.seg_col[i] = 0; }
   UNOK_REQUIRE(buffer_ranges_ok(p), UNOK_EINVAL, "gemm_nt_swiglu: operands exceed 32-bit buffer offsets");
-  launch_nt_w4m16<bf16_t, true>(p, (hipStream_t)stream);
+  launch_nt_w4m16<bf16_t, 1>(p, (hipStream_t)stream);
   return unok::check_launch("gemm_nt_swiglu");
+}
+
+// dgu[M, 2F] = SwiGLU backward of dS = A[M,K] B[F,K]^T + A2[M,K2] B2[F,K2]^T (bf16, never stored)
+// against gu[M, 2F] = [gate | up]; rounded exactly as unok_gemm_nt followed by unok_swiglu_bwd.
+// M and F multiples of 256, K and K2 of 64.
+UNOK_EXPORT int unok_gemm_nt_swiglu_bwd(int M, int F, int K, const void* A, int64_t lda, const void* B,
+                                        int64_t ldb, const void* A2, int64_t lda2, const void* B2, int64_t ldb2,
+                                        int K2, const void* gu, int64_t ldgu, void* dgu, int64_t lddgu,
+                                        void* stream) {
+  UNOK_REQUIRE(M >= 0 && F >= 0 && K >= 0 && K2 >= 0, UNOK_EINVAL, "gemm_nt_swiglu_bwd: negative size");
+  if (M == 0 || F == 0) return 0;
+  UNOK_REQUIRE(M % 256 == 0 && F % 256 == 0 && K % 64 == 0 && K > 0 && K2 % 64 == 0, UNOK_EINVAL,
+               "gemm_nt_swiglu_bwd: M=%d and F=%d must be multiples of 256, K=%d and K2=%d of 64", M, F, K, K2);
+  UNOK_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldgu % 8 == 0 && lddgu % 8 == 0 && aligned16(A) && aligned16(B) &&
+                   aligned16(gu) && aligned16(dgu) && (K2 == 0 || (lda2 % 8 == 0 && ldb2 % 8 == 0 && aligned16(A2) &&
+                                                                   aligned16(B2))),
+               UNOK_EALIGN, "gemm_nt_swiglu_bwd: row strides must be multiples of 8 and rows 16-byte aligned");
+  GemmNT p{};
+  p.A = A; p.lda = lda; p.B = B; p.ldb = ldb;
+  p.A2 = (A2 && K2 > 0) ? A2 : nullptr; p.lda2 = lda2; p.B2 = B2; p.ldb2 = ldb2;
+  p.C = dgu; p.ldc = lddgu; p.R = gu; p.ldr = ldgu;
+  p.M = M; p.N = F; p.K = K; p.K2 = p.A2 ? K2 : 0; p.alpha = 1.f; p.nseg = 1;
+  for (int i = 0; i < 4; ++i) { p.seg_end[i] = F; p.seg_col[i] = 0; }
+  UNOK_REQUIRE(buffer_ranges_ok(p), UNOK_EINVAL, "gemm_nt_swiglu_bwd: operands exceed 32-bit buffer offsets");
+  launch_nt_w4m16<bf16_t, 2>(p, (hipStream_t)stream);
+  return unok::check_launch("gemm_nt_swiglu_bwd");
 }
 
 UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,

@@ -8,6 +8,8 @@
 // reduces with 64-lane wavefront shuffles.
 #include "common.h"
 
+#include <type_traits>
+
 template <typename T> struct Vec { static constexpr int N = 16 / sizeof(T); };
 
 template <typename T>
@@ -320,10 +322,13 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ d
     load_vec(dout + row * F + c, d);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-      const float sg = sigmoidf_(g[e]);
-      const float silu = Elem<T>::round(g[e] * sg);
-      du[e] = d[e] * silu;
-      dg[e] = d[e] * u[e] * sg * (1.f + g[e] * (1.f - sg));
+      if constexpr (std::is_same<T, bf16_t>::value) {
+        swiglu_grad(d[e], g[e], u[e], dg[e], du[e]);
+      } else {
+        const float sg = sigmoidf_(g[e]);
+        du[e] = d[e] * (g[e] * sg);
+        dg[e] = d[e] * u[e] * sg * (1.f + g[e] * (1.f - sg));
+      }
     }
     store_vec(dgu + row * ldd + c, dg);
     store_vec(dgu + row * ldd + F + c, du);

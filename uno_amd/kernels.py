@@ -230,6 +230,40 @@ def gemm_nt_swiglu(a: torch.Tensor, b_interleaved: torch.Tensor, out: torch.Tens
     return out
 
 
+def gemm_nt_swiglu_bwd(a: torch.Tensor, b: torch.Tensor, a2: torch.Tensor | None, b2: torch.Tensor | None,
+                       gu: torch.Tensor, dgu: torch.Tensor | None = None) -> torch.Tensor:
+    """dgu = SwiGLU backward of dS = a @ b.T (+ a2 @ b2.T) against gu = [gate | up]; dS is never
+    stored. bf16; M and F = b.shape[0] multiples of 256."""
+    for t, n in ((a, "a"), (b, "b"), (gu, "gu")):
+        _rowmajor(t, n)
+    M, K = a.shape
+    F = b.shape[0]
+    if b.shape[1] != K or tuple(gu.shape) != (M, 2 * F):
+        raise RuntimeError("gemm_nt_swiglu_bwd: a [M,K], b [F,K] and gu [M,2F] required")
+    K2 = 0
+    if a2 is not None:
+        _rowmajor(a2, "a2")
+        _rowmajor(b2, "b2")
+        K2 = b2.shape[1]
+        if b2.shape[0] != F or a2.shape[0] != M or a2.shape[1] < K2:
+            raise RuntimeError("gemm_nt_swiglu_bwd: a2 [M,>=K2] and b2 [F,K2] required")
+    dgu = dgu if dgu is not None else torch.empty((M, 2 * F), device=a.device, dtype=a.dtype)
+    _rowmajor(dgu, "dgu")
+    rec = _recorder
+    if rec is not None and rec.predicate(a.dtype, M, F, K, K2, [F]):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    else:
+        rec = None
+    N.call("unok_gemm_nt_swiglu_bwd", M, F, K, N.ptr(a), _ld(a), N.ptr(b), _ld(b), N.ptr(a2),
+           _ld(a2) if a2 is not None else 0, N.ptr(b2), _ld(b2) if b2 is not None else 0, K2, N.ptr(gu), _ld(gu),
+           N.ptr(dgu), _ld(dgu), N.stream())
+    if rec is not None:
+        ev1.record()
+        rec.records.append((ev0, ev1, 2.0 * M * F * (K + K2)))
+    return dgu
+
+
 def swiglu_fused_ok(M: int, F: int, K: int) -> bool:
     """Shapes the fused gate/up + SwiGLU product accepts."""
     return M % 256 == 0 and (2 * F) % 256 == 0 and K % 64 == 0 and K > 0

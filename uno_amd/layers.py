@@ -131,10 +131,14 @@ class NoisyLayer(torch.autograd.Function):
         # ---- down projection ----------------------------------------------------------
         g_d = K.gemm_nt(dh2, lora.sb_t(li, "d"))                              # [M, r]
         K.gemm_tn(dh2, h_d, out=gb(li, "d"), alpha=sc_l, beta=1.0)            # dB_d
-        ds = K.gemm_nt(dh2, lw.w_d_t, a2=g_d, b2=lora.a_t(li, "d"))           # [M, F]
+        if dh2.dtype == torch.bfloat16 and M % 256 == 0 and g.F % 256 == 0 and g.H % 64 == 0 and r % 64 == 0:
+            # dS = dh2 W_d + g_d A_d never leaves the GEMM: its epilogue applies the SwiGLU backward
+            dgu = K.gemm_nt_swiglu_bwd(dh2, lw.w_d_t, g_d, lora.a_t(li, "d"), gu)
+        else:
+            ds = K.gemm_nt(dh2, lw.w_d_t, a2=g_d, b2=lora.a_t(li, "d"))       # [M, F]
+            dgu = K.swiglu_bwd(ds, gu, g.F)
+            del ds
         K.gemm_tn(g_d, s, out=ga(li, "d"), beta=1.0)                          # dA_d
-        dgu = K.swiglu_bwd(ds, gu, g.F)
-        del ds
         # ---- gate | up -----------------------------------------------------------------
         g_gu = torch.empty((M, 2 * r), device=dh2.device, dtype=dh2.dtype)
         sbt = lora.sb_t(li, "gu")
