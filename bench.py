@@ -299,7 +299,7 @@ def main() -> int:
         "mfu": round(mfu, 4), "algorithmic_tflop_per_step": round(flops["total"] / 1e12, 2),
         "flops_breakdown_tflop": {k: round(v / 1e12, 2) for k, v in flops.items() if k != "total"},
         "roofline": {"kernel": "gemm_nt_bf16_w4m16_kernel (256x256 tiles, 16x16x32 MFMA; fused LoRA linears, "
-                                "clean-stream gate/up + SwiGLU, LM head)",
+                                "SwiGLU forward and backward epilogues, LM head)",
                      "bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic() if args.workload == "qwen3_8b" else None,
