@@ -45,14 +45,17 @@ int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
                  void* C, int64_t ldc, const void* R, int64_t ldr,
                  const uint8_t* gate, float alpha, void* stream);
 
-/* C[M, N/2] = silu(G) (.) U of the gate/up product A[M,K] B[N,K]^T, bf16, for B with 64-row
- * interleaved gate/up rows (rows 128 b + [0, 64): gate features 64 b + [0, 64); rows
- * 128 b + [64, 128): the same up features); rounded exactly as unok_gemm_nt followed by
- * unok_swiglu_fwd. M and N multiples of 256, K of 64. Clean-stream (forward-only) MLP of the
- * remote Qwen3 decoder: down_proj input act_fn(gate_proj(x)) * up_proj(x)
- * (modeling_qwen3.py:81-82). */
+/* C[M, N/2] = silu(G) (.) U of the gate/up product A[M,K] B[N,K]^T (+ A2[M,K2] B2[N,K2]^T, the
+ * LoRA extension), bf16, for B (and B2) with 64-row interleaved gate/up rows (rows 128 b + [0, 64):
+ * gate features 64 b + [0, 64); rows 128 b + [64, 128): the same up features); rounded exactly as
+ * unok_gemm_nt followed by unok_swiglu_fwd. With gu non-null, also stores the product itself as
+ * gu[M, N] = [gate | up] (the layout of the plain product, for the backward). M and N multiples of
+ * 256, K and K2 of 64; A2 may be null (K2 ignored). The remote Qwen3 decoder's MLP input to
+ * down_proj, act_fn(gate_proj(x)) * up_proj(x) (modeling_qwen3.py:81-82), with the LoRA terms of
+ * gate_proj and up_proj (peft 0.15.2 lora.Linear; training/lora.py:136-179). */
 int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
-                        void* C, int64_t ldc, void* stream);
+                        const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,
+                        void* C, int64_t ldc, void* gu, int64_t ldgu, void* stream);
 
 /* dgu[M, 2F] = SwiGLU backward of dS = A[M,K] B[F,K]^T + A2[M,K2] B2[F,K2]^T against
  * gu[M, 2F] = [gate | up] (dS is never stored); bf16, rounded exactly as unok_gemm_nt followed by

@@ -178,6 +178,48 @@ def test_gemm_nt_swiglu_matches_unfused(dev, M, F, Kd):
     assert torch.equal(fused, ref)
 
 
+def _interleave_lora_b(sb_gu, F, r):
+    """[sB_gate; sB_up] [2F, r] -> [2F, 2r] in the interleaved row order, zero off-diagonal halves."""
+    out = torch.zeros(F // 64, 2, 64, 2 * r, device=sb_gu.device, dtype=sb_gu.dtype)
+    out[:, 0, :, :r] = sb_gu[:F].view(F // 64, 64, r)
+    out[:, 1, :, r:] = sb_gu[F:].view(F // 64, 64, r)
+    return out.view(2 * F, 2 * r)
+
+
+@pytest.mark.parametrize("M,F,Kd,r", [(512, 512, 256, 32), (1024, 1536, 512, 64), (256, 256, 128, 64)])
+def test_gemm_nt_swiglu_lora_and_gate_up_store(dev, M, F, Kd, r):
+    """With the gate/up LoRA terms as one K = 2r extension on interleaved rows, and the [gate | up]
+    product stored for the backward: both outputs equal the segmented LoRA product followed by the
+    SwiGLU kernel, bit for bit."""
+    torch.manual_seed(M + F + r)
+    x = (torch.randn(M, Kd, device=dev) * 0.5).bfloat16()
+    w = (torch.randn(2 * F, Kd, device=dev) * 0.1).bfloat16()
+    h = (torch.randn(M, 2 * r, device=dev) * 0.5).bfloat16()
+    sb = (torch.randn(2 * F, r, device=dev) * 0.1).bfloat16()
+    gu_ref = K.gemm_nt(x, w, a2=h, b2=sb, segments=[(F, 0), (2 * F, r)])
+    ref = K.swiglu_fwd(gu_ref, F)
+    gu = torch.full((M, 2 * F), float("nan"), device=dev, dtype=torch.bfloat16)
+    fused = K.gemm_nt_swiglu(x, K.interleave_gate_up(w, F), a2=h, b2_interleaved=_interleave_lora_b(sb, F, r), gu=gu)
+    torch.cuda.synchronize()
+    assert torch.equal(gu, gu_ref)
+    assert torch.equal(fused, ref)
+
+
+def test_lora_state_keeps_interleaved_gate_up_b(dev):
+    """The LoRA state's interleaved gate/up sB follows the compute copy after every refresh."""
+    from types import SimpleNamespace
+    from uno_amd.adapter import LoraState
+    cfg = SimpleNamespace(hidden_size=128, head_dim=64, num_attention_heads=2, num_key_value_heads=1,
+                          intermediate_size=256, num_hidden_layers=3)
+    st = LoraState(cfg, 32, 64.0, dev, torch.bfloat16)
+    for it in range(2):
+        st.master.normal_()
+        st.refresh_copies()
+        torch.cuda.synchronize()
+        for li in range(3):
+            assert torch.equal(st.sb_gu_i(li), _interleave_lora_b(st.sb_c(li, "gu"), 256, 32)), (it, li)
+
+
 def test_gemm_nt_swiglu_rejects_unaligned_shapes(dev):
     x = torch.randn(300, 64, device=dev).bfloat16()
     w = torch.randn(256, 64, device=dev).bfloat16()

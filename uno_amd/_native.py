@@ -26,7 +26,7 @@ SIGNATURES: dict[str, tuple] = {
     "unok_last_error": (C.c_char_p, []),
     "unok_gemm_nt": (_i, [_i, _i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i,
                           _i, _ip, _ip, _p, _i64, _p, _i64, _p, _f, _p]),
-    "unok_gemm_nt_swiglu": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p]),
+    "unok_gemm_nt_swiglu": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i, _p, _i64, _p, _i64, _p]),
     "unok_gemm_nt_swiglu_bwd": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i, _p, _i64, _p, _i64,
                                      _p]),
     "unok_gemm_tn_workspace": (_i64, [_i, _i, _i]),

@@ -11,7 +11,10 @@ so that each fused projection's adapters are contiguous (A_qkv = [A_q; A_k; A_v]
 matrix; B_qkv = [B_q; B_k; B_v] is [q+2kv, r]), the optimizer is one flat pass, and the
 compute copy (B scaled by alpha/r) is refreshed by that same pass. Transposed compute copies
 (A^T per group, (sB)^T per group) feed the data-gradient GEMMs and are rebuilt by one batched
-transpose launch after every update.
+transpose launch after every update. For the gate/up product with the SwiGLU epilogue, whose
+weight rows alternate in blocks of 64 (64 gate rows, then the same features' up rows), sB of
+gate/up is also kept in that row order with K = 2r columns: [sB_gate, 0] on gate rows and
+[0, sB_up] on up rows, so one LoRA extension over h = x [A_gate; A_up]^T serves both.
 """
 from __future__ import annotations
 
@@ -83,6 +86,7 @@ class LoraState:
         self.copy_t = torch.empty(self.numel, device=self.device, dtype=compute_dtype)
         self.step = 0
         self._build_transpose_jobs()
+        self._build_gate_up_interleaved()
         # autograd anchor: the decoder's stream Functions take it as an input so that backward
         # runs; the LoRA gradients are accumulated straight into ``grad`` by the kernels.
         self.anchor = torch.zeros(1, **f32).requires_grad_(True)
@@ -128,6 +132,34 @@ class LoraState:
         self._jobs = torch.tensor(jobs, dtype=torch.int64, device=self.device)
         self._tiles = tile
 
+    def _build_gate_up_interleaved(self):
+        F, r, L = self.slots[0]["gate_proj"].out, self.rank, len(self.slots)
+        self._sb_gu_i = None
+        if F % 64 or L == 0:
+            return
+        # zero once; the refresh writes only the gate half of gate rows and the up half of up rows
+        self._sb_gu_i = torch.zeros((L, F // 64, 2, 64, 2 * r), device=self.device, dtype=self.compute_dtype)
+        lstride = self.slots[1]["gate_proj"].b_off - self.slots[0]["gate_proj"].b_off if L > 1 else 0
+        for li in range(1, L):
+            assert self.slots[li]["gate_proj"].b_off - self.slots[li - 1]["gate_proj"].b_off == lstride
+        # sB_gate / sB_up of every layer as [L, 2, F/64, 64, r] (gate rows then up rows per layer)
+        self._sb_gu_src = self.copy.as_strided((L, 2, F // 64, 64, r), (lstride, F * r, 64 * r, r, 1),
+                                               self.copy.storage_offset() + self.slots[0]["gate_proj"].b_off)
+
+    def _refresh_gate_up_interleaved(self) -> None:
+        if self._sb_gu_i is None:
+            return
+        r = self.rank
+        self._sb_gu_i[:, :, 0, :, :r].copy_(self._sb_gu_src[:, 0])
+        self._sb_gu_i[:, :, 1, :, r:].copy_(self._sb_gu_src[:, 1])
+
+    def sb_gu_i(self, layer: int) -> torch.Tensor | None:
+        """sB of gate/up as [2F, 2r] in the interleaved row order (see the module docstring)."""
+        if self._sb_gu_i is None:
+            return None
+        t = self._sb_gu_i[layer]
+        return t.view(-1, t.shape[-1])
+
     def a_t(self, layer: int, group: str) -> torch.Tensor:
         """A_group^T [in, rows] compute copy."""
         return self._t_views[layer][(group, "a")]
@@ -157,6 +189,7 @@ class LoraState:
     def refresh_transposes(self) -> None:
         N.call("unok_transpose_jobs", N.dtype_code(self.compute_dtype), N.ptr(self._jobs), self._jobs.shape[0],
                self._tiles, N.ptr(self.copy), N.ptr(self.copy_t), N.stream())
+        self._refresh_gate_up_interleaved()
 
     def zero_grad(self) -> None:
         self.grad.zero_()

@@ -29,6 +29,7 @@ struct GemmNT {
   void* C; int64_t ldc;
   const void* R; int64_t ldr;
   const uint8_t* gate;
+  void* C2; int64_t ldc2;          // second output of the SwiGLU forward epilogue (gate | up), or null
   int M, N, K, K2;
   int nseg;
   int seg_end[4];
@@ -1302,22 +1303,67 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     // 64 b + [0, 64), rows 128 b + [64, 128) = the same up features): the wave's 128 columns are
     // one such pair, accumulator j < 4 the gate and j + 4 the up value of the same feature. Writes
     // C[row][64 b + c] = bf16(bf16(silu(g)) u) with g, u rounded to bf16 first, as a bf16 GEMM
-    // followed by the SwiGLU kernel computes it. Interior tiles only (checked by the caller).
+    // followed by the SwiGLU kernel computes it. With C2, also stores the rounded gate and up
+    // values as C2[row][f] and C2[row][N/2 + f] (the [gate | up] layout of the plain product):
+    // then each wave rounds its 128 x (64 gate | 64 up) block into a private 32 KB of the idle
+    // LDS stages (16-byte chunks XOR-swizzled by row, as in the backward epilogue) and stores
+    // both outputs by rows, 16 lanes per row: gate and up as 128-byte runs, C as one.
+    // Interior tiles only (checked by the caller).
     const int f0 = (n0 + wn * 128) / 2;
+    if (p.C2 == nullptr) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        OutT* crow = C + (int64_t)(m0 + wm * 128 + i * 16 + lr) * p.ldc;
+#pragma unroll
+        for (int j = 0; j < TN / 2; ++j) {
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gv = bf16_to_f32(f32_to_bf16(acc[i][j][q] * p.alpha));
+            const float uv = bf16_to_f32(f32_to_bf16(acc[i][j + TN / 2][q] * p.alpha));
+            v[q] = bf16_to_f32(f32_to_bf16(gv * sigmoidf_(gv))) * uv;
+          }
+          store4(crow + f0 + j * 16 + lk * 4, nullptr, v);
+        }
+      }
+      return;
+    }
+    asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed (waited above)
+    bf16_t* q = smem + wid * 128 * 128;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      OutT* crow = C + (int64_t)(m0 + wm * 128 + i * 16 + lr) * p.ldc;
 #pragma unroll
-      for (int j = 0; j < TN / 2; ++j) {
-        float v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float gv = bf16_to_f32(f32_to_bf16(acc[i][j][q] * p.alpha));
-          const float uv = bf16_to_f32(f32_to_bf16(acc[i][j + TN / 2][q] * p.alpha));
-          v[q] = bf16_to_f32(f32_to_bf16(gv * sigmoidf_(gv))) * uv;
-        }
-        store4(crow + f0 + j * 16 + lk * 4, nullptr, v);
+      for (int j = 0; j < TN; ++j) {
+        uint2 w;
+        w.x = (uint32_t)f32_to_bf16(acc[i][j][0] * p.alpha) | ((uint32_t)f32_to_bf16(acc[i][j][1] * p.alpha) << 16);
+        w.y = (uint32_t)f32_to_bf16(acc[i][j][2] * p.alpha) | ((uint32_t)f32_to_bf16(acc[i][j][3] * p.alpha) << 16);
+        *(uint2*)&q[(i * 16 + lr) * 128 + (((2 * j + (lk >> 1)) ^ lr) << 3) + (lk & 1) * 4] = w;
       }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    const int rsub = lane >> 4, c16 = lane & 15;
+    const int F = p.N / 2;
+    const int64_t row0 = m0 + wm * 128 + rsub;
+    bf16_t* gdst = (bf16_t*)p.C2 + row0 * p.ldc2 + (c16 < 8 ? f0 + 8 * c16 : F + f0 + 8 * (c16 - 8));
+    OutT* sdst = C + row0 * p.ldc + f0 + 4 * c16;
+#pragma unroll 8
+    for (int it = 0; it < 32; ++it) {
+      const int r = it * 4 + rsub;
+      const bf16_t* qr = q + r * 128;
+      const uint4 vw = *(const uint4*)&qr[(c16 ^ (r & 15)) << 3];
+      const uint2 gw = *(const uint2*)&qr[(((c16 >> 1) ^ (r & 15)) << 3) + (c16 & 1) * 4];
+      const uint2 uw = *(const uint2*)&qr[(((8 + (c16 >> 1)) ^ (r & 15)) << 3) + (c16 & 1) * 4];
+      *(uint4*)(gdst + (int64_t)(it * 4) * p.ldc2) = vw;
+      const bf16_t* gv = (const bf16_t*)&gw;
+      const bf16_t* uv = (const bf16_t*)&uw;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float g = bf16_to_f32(gv[e]);
+        v[e] = bf16_to_f32(f32_to_bf16(g * sigmoidf_(g))) * bf16_to_f32(uv[e]);
+      }
+      store4(sdst + (int64_t)(it * 4) * p.ldc, nullptr, v);
     }
     return;
   }
@@ -1452,17 +1498,23 @@ static void launch_nt_dma(const GemmNT& p, int out_dtype, hipStream_t st) {
 // 128 b + [0, 64) gate, 128 b + [64, 128) up of features 64 b + [0, 64)), bf16, rounded as the
 // unfused product followed by unok_swiglu_fwd. M and N multiples of 256, K of 64.
 UNOK_EXPORT int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
-                                    void* C, int64_t ldc, void* stream) {
-  UNOK_REQUIRE(M >= 0 && N >= 0 && K >= 0, UNOK_EINVAL, "gemm_nt_swiglu: negative size M=%d N=%d K=%d", M, N, K);
+                                    const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,
+                                    void* C, int64_t ldc, void* gu, int64_t ldgu, void* stream) {
+  UNOK_REQUIRE(M >= 0 && N >= 0 && K >= 0 && K2 >= 0, UNOK_EINVAL, "gemm_nt_swiglu: negative size M=%d N=%d K=%d",
+               M, N, K);
   if (M == 0 || N == 0) return 0;
-  UNOK_REQUIRE(M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && K > 0, UNOK_EINVAL,
-               "gemm_nt_swiglu: M=%d and N=%d must be multiples of 256, K=%d of 64", M, N, K);
-  UNOK_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldc % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(C),
+  const bool ext = A2 != nullptr && K2 > 0;
+  UNOK_REQUIRE(M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && K > 0 && (!ext || K2 % 64 == 0), UNOK_EINVAL,
+               "gemm_nt_swiglu: M=%d and N=%d must be multiples of 256, K=%d and K2=%d of 64", M, N, K, K2);
+  UNOK_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldc % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(C) &&
+                   (!ext || (lda2 % 8 == 0 && ldb2 % 8 == 0 && aligned16(A2) && aligned16(B2))) &&
+                   (gu == nullptr || (ldgu % 8 == 0 && aligned16(gu))),
                UNOK_EALIGN, "gemm_nt_swiglu: row strides must be multiples of 8 and rows 16-byte aligned");
   GemmNT p{};
   p.A = A; p.lda = lda; p.B = B; p.ldb = ldb;
-  p.C = C; p.ldc = ldc;
-  p.M = M; p.N = N; p.K = K; p.alpha = 1.f; p.nseg = 1;
+  p.A2 = ext ? A2 : nullptr; p.lda2 = lda2; p.B2 = B2; p.ldb2 = ldb2;
+  p.C = C; p.ldc = ldc; p.C2 = gu; p.ldc2 = ldgu;
+  p.M = M; p.N = N; p.K = K; p.K2 = ext ? K2 : 0; p.alpha = 1.f; p.nseg = 1;
   for (int i = 0; i < 4; ++i) { p.seg_end[i] = N; p.seg_col[i] = 0; }
   UNOK_REQUIRE(buffer_ranges_ok(p), UNOK_EINVAL, "gemm_nt_swiglu: operands exceed 32-bit buffer offsets");
   launch_nt_w4m16<bf16_t, 1>(p, (hipStream_t)stream);

@@ -205,28 +205,44 @@ def qknorm_rope_bwd(dq, dk, qkv, nq, nk, d, wq, wk, pos, inv_freq, rstd, dqkv):
     return dqkv
 
 
-def gemm_nt_swiglu(a: torch.Tensor, b_interleaved: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """silu(gate) * up of a @ b.T for gate/up weight rows interleaved in blocks of 64
-    (``interleave_gate_up``); bf16, M and the row count of b multiples of 256."""
+def gemm_nt_swiglu(a: torch.Tensor, b_interleaved: torch.Tensor, *, a2: torch.Tensor | None = None,
+                   b2_interleaved: torch.Tensor | None = None, gu: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up of a @ b.T (+ a2 @ b2.T) for gate/up weight rows interleaved in blocks of 64
+    (``interleave_gate_up``; b2 likewise); bf16, M and the row count of b multiples of 256, K and
+    K2 = b2.shape[1] of 64. With ``gu`` ([M, rows]), also stores the product as [gate | up]."""
     _rowmajor(a, "a")
     _rowmajor(b_interleaved, "b")
     M, K = a.shape
     rows = b_interleaved.shape[0]
     if b_interleaved.shape[1] != K or a.dtype != torch.bfloat16 or b_interleaved.dtype != torch.bfloat16:
         raise RuntimeError("gemm_nt_swiglu: bf16 a [M,K] and b [N,K] required")
+    K2 = 0
+    if a2 is not None:
+        _rowmajor(a2, "a2")
+        _rowmajor(b2_interleaved, "b2")
+        K2 = b2_interleaved.shape[1]
+        if b2_interleaved.shape[0] != rows or a2.shape[0] != M or a2.shape[1] < K2:
+            raise RuntimeError("gemm_nt_swiglu: a2 [M,>=K2] and b2 [N,K2] required")
+    if gu is not None:
+        _rowmajor(gu, "gu")
+        if tuple(gu.shape) != (M, rows) or gu.dtype != a.dtype:
+            raise RuntimeError("gemm_nt_swiglu: gu must be [M, N] in the dtype of a")
     out = out if out is not None else torch.empty((M, rows // 2), device=a.device, dtype=a.dtype)
     _rowmajor(out, "out")
     rec = _recorder
-    if rec is not None and rec.predicate(a.dtype, M, rows, K, 0, [rows]):
+    if rec is not None and rec.predicate(a.dtype, M, rows, K, K2, [rows]):
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
     else:
         rec = None
     N.call("unok_gemm_nt_swiglu", M, rows, K, N.ptr(a), _ld(a), N.ptr(b_interleaved), _ld(b_interleaved),
-           N.ptr(out), _ld(out), N.stream())
+           N.ptr(a2), _ld(a2) if a2 is not None else 0, N.ptr(b2_interleaved),
+           _ld(b2_interleaved) if b2_interleaved is not None else 0, K2,
+           N.ptr(out), _ld(out), N.ptr(gu), _ld(gu) if gu is not None else 0, N.stream())
     if rec is not None:
         ev1.record()
-        rec.records.append((ev0, ev1, 2.0 * M * rows * K))
+        rec.records.append((ev0, ev1, 2.0 * M * rows * (K + K2)))
     return out
 
 

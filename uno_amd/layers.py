@@ -110,8 +110,14 @@ class NoisyLayer(torch.autograd.Function):
         h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o"), residual=h0)
         x2, rstd2 = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
         h_gu = K.gemm_nt(x2, lora.a_c(li, "gu"))
-        gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu"), segments=[(g.F, 0), (2 * g.F, r)])
-        s = K.swiglu_fwd(gu, g.F)
+        sb_gu_i = lora.sb_gu_i(li) if lw.w_gu_i is not None and x2.dtype == torch.bfloat16 else None
+        if sb_gu_i is not None and (2 * r) % 64 == 0 and K.swiglu_fused_ok(x2.shape[0], g.F, x2.shape[1]):
+            # gate/up product with its LoRA terms, SwiGLU in the epilogue; [gate | up] kept for backward
+            gu = torch.empty((x2.shape[0], 2 * g.F), device=x2.device, dtype=x2.dtype)
+            s = K.gemm_nt_swiglu(x2, lw.w_gu_i, a2=h_gu, b2_interleaved=sb_gu_i, gu=gu)
+        else:
+            gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu"), segments=[(g.F, 0), (2 * g.F, r)])
+            s = K.swiglu_fwd(gu, g.F)
         h_d = K.gemm_nt(s, lora.a_c(li, "d"))
         h2 = K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d"), residual=h1)
         ctx.lw, ctx.lora, ctx.li, ctx.g, ctx.sc = lw, lora, li, g, sc
