@@ -22,10 +22,14 @@ from ..optim import FusedLoraAdamW
 from .config import UnoObjectiveConfig
 from .constants import IGNORE_INDEX
 from .curriculum import BlockCurriculumPlan, set_model_block_size
-from .lora import TokenwiseLoraRouter, make_saved_adapter_portable, save_adapter
+from .lora import TokenwiseLoraRouter, load_adapter, make_saved_adapter_portable, save_adapter
 from .losses import shift_labels_for_next_token
 from .modeling import (extract_uno_regions, prepare_uno_layout, run_prepared_uno_forward, unwrap_base_model,
                        validate_uno_model)
+
+
+# AdamW moments of a curriculum-boundary checkpoint (flat fp32 buffers, safetensors).
+OPTIMIZER_STATE = "uno_optimizer_state.safetensors"
 
 
 def combine_objective_losses(ce_loss, kl_loss, tv_loss, objective: UnoObjectiveConfig):
@@ -196,15 +200,52 @@ class UnoTrainer:
         return loss
 
     def save_checkpoint(self, output_dir) -> Path:
-        """Adapter checkpoint; at curriculum boundaries also the resume state file."""
+        """Adapter checkpoint (PEFT format); at curriculum boundaries the complete resume state
+        too (training/trainer.py:89-128 saves full state there): the AdamW moments and update
+        count, the position of the model's noise stream (what the reference's RNG state restores),
+        then the curriculum state file, which is written last so that its presence marks a
+        complete checkpoint."""
+        from safetensors.torch import save_file
+
         ckpt = Path(output_dir) / f"checkpoint-{self.state.global_step}"
         save_adapter(_unwrap_wrappers(self.model), ckpt)
         make_saved_adapter_portable(ckpt)
         reason = self.curriculum.checkpoint_reasons.get(self.state.global_step)
         if reason:
+            st = self.optimizer.state
+            save_file({"exp_avg": st.exp_avg.detach().cpu(), "exp_avg_sq": st.exp_avg_sq.detach().cpu()},
+                      str(ckpt / OPTIMIZER_STATE))
+            base = unwrap_base_model(_unwrap_wrappers(self.model))
             payload = {"version": 1, "global_step": self.state.global_step, "reason": reason,
-                       "curriculum_sha256": self.curriculum.sha256()}
+                       "curriculum_sha256": self.curriculum.sha256(), "adamw_updates": st.step,
+                       "noise_draws": int(getattr(base, "_bd_step", 0))}
             tmp = ckpt / "uno_curriculum_state.json.tmp"
             tmp.write_text(json.dumps(payload, indent=2, sort_keys=True) + "\n")
             tmp.replace(ckpt / "uno_curriculum_state.json")
         return ckpt
+
+    def resume_from_checkpoint(self, checkpoint) -> None:
+        """Restores a curriculum-boundary checkpoint (validate_curriculum_resume, then adapters,
+        AdamW moments, update count, noise-stream position and global step): the next train_step
+        continues the run exactly."""
+        from safetensors.torch import load_file
+
+        checkpoint = Path(checkpoint)
+        validate_curriculum_resume(checkpoint, self.curriculum)
+        payload = json.loads((checkpoint / "uno_curriculum_state.json").read_text())
+        moments_path = checkpoint / OPTIMIZER_STATE
+        if not moments_path.is_file() or "adamw_updates" not in payload:
+            raise FileNotFoundError(f"{checkpoint} holds no optimizer state ({OPTIMIZER_STATE}).")
+        moments = load_file(str(moments_path))
+        st = self.optimizer.state
+        for name in ("exp_avg", "exp_avg_sq"):
+            if tuple(moments[name].shape) != (st.numel,):
+                raise ValueError(f"{name} in {moments_path} has {moments[name].numel()} values, expected {st.numel}.")
+        load_adapter(_unwrap_wrappers(self.model), checkpoint)
+        st.exp_avg.copy_(moments["exp_avg"])
+        st.exp_avg_sq.copy_(moments["exp_avg_sq"])
+        st.step = int(payload["adamw_updates"])
+        base = unwrap_base_model(_unwrap_wrappers(self.model))
+        if hasattr(base, "_bd_step"):
+            base._bd_step = int(payload.get("noise_draws", payload["global_step"]))
+        self.state.global_step = int(payload["global_step"])
