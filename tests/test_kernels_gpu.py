@@ -230,6 +230,7 @@ class _Head:
 
 @pytest.mark.parametrize("keep", [True, False], ids=["kept_logits", "recomputed_logits"])
 @pytest.mark.parametrize("dtype,R,H,V,chunk", [(torch.float32, 50, 64, 5000, 2048),
+                                               (torch.float32, 50, 64, 5003, 2048),
                                                (torch.bfloat16, 300, 256, 8192, 3000),
                                                (torch.bfloat16, 1000, 512, 151936, 16384)])
 def test_chunked_weighted_ce(dev, dtype, R, H, V, chunk, keep, monkeypatch):

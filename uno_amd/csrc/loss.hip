@@ -12,6 +12,8 @@
 // math; TV's gradient is p * (sign(p - q) - sum sign * p) with sign(0) = 0.
 #include "common.h"
 
+#include <type_traits>
+
 // Floating-point contraction is off in this file: TV must see d = p - q == 0 exactly when
 // p == q (sign(0) = 0), which a fused multiply-add of p's scaling into the subtraction breaks.
 #pragma clang fp contract(off)
@@ -19,6 +21,8 @@
 template <typename T> __device__ __forceinline__ float ldf(const T* p) { return Elem<T>::load(p); }
 
 // Running softmax statistics of a logits chunk z[R, Vc] (columns c0..c0+Vc of the vocab).
+// One pass over the row: each thread keeps its own (max, sum-exp), rescaled when its max grows,
+// with 16-byte loads for fp32 rows that allow them; the block then merges the pairs.
 template <typename T>
 __global__ __launch_bounds__(256) void row_lse_update_kernel(const T* __restrict__ z, int64_t ldz, int Vc, int c0,
                                                              const int64_t* __restrict__ tgt, float* run_max,
@@ -26,12 +30,28 @@ __global__ __launch_bounds__(256) void row_lse_update_kernel(const T* __restrict
   __shared__ float red[32];
   const int row = blockIdx.x;
   const T* zr = z + (int64_t)row * ldz;
-  float m = -INFINITY;
-  for (int j = threadIdx.x; j < Vc; j += 256) m = fmaxf(m, ldf(zr + j));
-  m = block_max(m, red);
-  float s = 0.f;
-  for (int j = threadIdx.x; j < Vc; j += 256) s += expf(ldf(zr + j) - m);
-  s = block_sum(s, red);
+  float m = -INFINITY, s = 0.f;
+  auto add = [&](float v) {
+    if (v > m) { s = s * expf(m - v) + 1.f; m = v; }   // expf(-inf) = 0 on the first value
+    else s += expf(v - m);
+  };
+  int j0 = 0;
+  if constexpr (std::is_same<T, float>::value) {
+    if (((uintptr_t)zr & 15) == 0) {
+      const int nv = Vc / 4;
+      for (int q = threadIdx.x; q < nv; q += 256) {
+        const float4 v = *(const float4*)(zr + 4 * q);
+        const float mv = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+        if (mv > m) { s *= expf(m - mv); m = mv; }
+        s += expf(v.x - m) + expf(v.y - m) + expf(v.z - m) + expf(v.w - m);
+      }
+      j0 = 4 * nv;
+    }
+  }
+  for (int j = j0 + threadIdx.x; j < Vc; j += 256) add(ldf(zr + j));
+  const float mb = block_max(m, red);
+  s = block_sum(m == -INFINITY ? 0.f : s * expf(m - mb), red);
+  m = mb;
   if (threadIdx.x == 0) {
     float M0 = first ? -INFINITY : run_max[row];
     float S0 = first ? 0.f : run_sum[row];
@@ -108,7 +128,20 @@ __global__ __launch_bounds__(256) void ce_grad_chunk_kernel(const float* __restr
   const int64_t t = tgt[row] - c0;
   const float* zr = z + (int64_t)row * ldz;
   TO* dr = dz + (int64_t)row * lddz;
-  for (int j = threadIdx.x; j < Vc; j += 256) {
+  int j0 = 0;
+  if constexpr (std::is_same<TO, bf16_t>::value) {
+    if (((uintptr_t)zr & 15) == 0 && ((uintptr_t)dr & 7) == 0) {   // 4 logits in, 4 gradients out per load
+      const int nv = Vc / 4;
+      for (int q = threadIdx.x; q < nv; q += 256) {
+        const float4 v = *(const float4*)(zr + 4 * q);
+        float p[4] = {expf(v.x - l), expf(v.y - l), expf(v.z - l), expf(v.w - l)};
+        if (t >= 4 * q && t < 4 * q + 4) p[t - 4 * q] -= 1.f;
+        *(uint2*)(dr + 4 * q) = make_uint2(pack2_bf16(c * p[0], c * p[1]), pack2_bf16(c * p[2], c * p[3]));
+      }
+      j0 = 4 * nv;
+    }
+  }
+  for (int j = j0 + threadIdx.x; j < Vc; j += 256) {
     float p = expf(zr[j] - l);
     if (j == t) p -= 1.f;
     Elem<TO>::store(dr + j, c * p);
