@@ -1033,17 +1033,47 @@ __global__ __launch_bounds__(512) void gemm_tn_skinny_kernel(const GemmTNSkinny 
   }
 }
 
-// C[P,Q] (row stride ldc, fp32) = beta * C + sum_z WS[z]
+// C[P,Q] (row stride ldc, fp32) = beta * C + sum_z WS[z], partials summed in z order. With Q and
+// ldc multiples of 4 and 16-byte aligned buffers each thread takes 4 consecutive elements, and
+// the partial loads are unrolled so several are in flight at once.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, float* C, int64_t ldc,
                                                              int P, int Q, int nsplit, float beta) {
   const int64_t total = (int64_t)P * Q;
+  const bool vec = (Q & 3) == 0 && (ldc & 3) == 0 && (((uintptr_t)ws | (uintptr_t)C) & 15) == 0;
+  if (vec) {
+    for (int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x); i < total;
+         i += 4 * (int64_t)gridDim.x * blockDim.x) {
+      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+      for (int z = 0; z < nsplit; ++z) {
+        const float4 v = *(const float4*)(ws + z * total + i);
+        s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+      }
+      const int64_t r = i / Q, c = i % Q;
+      float4* dst = (float4*)(C + r * ldc + c);
+      if (beta != 0.f) {
+        const float4 o = *dst;
+        s.x += beta * o.x; s.y += beta * o.y; s.z += beta * o.z; s.w += beta * o.w;
+      }
+      *dst = s;
+    }
+    return;
+  }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.f;
+#pragma unroll 4
     for (int z = 0; z < nsplit; ++z) s += ws[z * total + i];
     const int64_t r = i / Q, c = i % Q;
     float* dst = C + r * ldc + c;
     *dst = (beta != 0.f ? beta * *dst : 0.f) + s;
   }
+}
+
+// Workgroups of the split-K reduction: one element per thread, four when rows allow vectors.
+static int reduce_blocks(int P, int Q) {
+  const int64_t per = (Q % 4 == 0) ? 1024 : 256;
+  const int64_t b = ((int64_t)P * Q + per - 1) / per;
+  return (int)(b < 4096 ? (b > 0 ? b : 1) : 4096);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1871,8 +1901,7 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
       launch_tn_skinny(q, nz, !a_small, st);
       int rc = unok::check_launch("gemm_tn_skinny");
       if (rc) return rc;
-      const int64_t total = (int64_t)NS * NX;
-      const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+      const int blocks = reduce_blocks(P, Q);
       hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, (const float*)workspace, C, ldc,
                          P, Q, nz, beta);
       return unok::check_launch("gemm_tn_reduce");
@@ -1901,8 +1930,7 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
   }
   int rc = unok::check_launch("gemm_tn");
   if (rc) return rc;
-  const int64_t total = (int64_t)P * Q;
-  const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+  const int blocks = reduce_blocks(P, Q);
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, (const float*)workspace, C, ldc, P, Q, nz, beta);
   return unok::check_launch("gemm_tn_reduce");
 }
