@@ -78,8 +78,7 @@ def clean_layer(h: torch.Tensor, lw: LayerWeights, g: Geometry, sc: StreamContex
     x1, _ = K.rmsnorm_fwd(h, lw.ln_in, g.eps)
     qkv = K.gemm_nt(x1, lw.w_qkv)
     q, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
-    v = torch.empty((M, g.kv), device=h.device, dtype=h.dtype)
-    K.rows_copy(qkv[:, g.q + g.kv:], v, M)
+    v = qkv[:, g.q + g.kv:]   # a strided view: the attention kernels take V's row stride, no copy
     o, _ = K.attn_fwd(q, k, v, sc.iv_clean, g.nq, g.nk, g.d)
     h1 = K.gemm_nt(o, lw.w_o, residual=h)
     x2, _ = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
