@@ -51,10 +51,10 @@ WORKLOADS = {
 
 
 WORKLOAD_NAMES = {
-    "qwen3_8b": "Qwen3-8B-shape cond-LoRA block-diffusion step (config 3)",
-    "dense_1b": "1B-class (16 layers, hidden 2048, 16q/8kv) cond-LoRA step, rank 32 (config 2)",
-    "mha_7b": "7B MHA (no q/k-norm, vocab 32000) cond-LoRA step, block curriculum 4/8/16/32 (config 4)",
-    "packed_16k": "Qwen3-8B-shape step on one 16384-token row of packed segments, block 32 (config 5)",
+    "qwen3_8b": "Qwen3-8B-shape cond-LoRA block-diffusion step (36 layers, 4 x 4096 tokens, block 16, LoRA r64)",
+    "dense_1b": "1B-class (16 layers, hidden 2048, 16q/8kv) cond-LoRA step, rank 32",
+    "mha_7b": "7B MHA (no q/k-norm, vocab 32000) cond-LoRA step, block curriculum 4/8/16/32",
+    "packed_16k": "Qwen3-8B-shape step on one 16384-token row of packed segments, block 32",
 }
 
 
