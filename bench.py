@@ -223,7 +223,7 @@ def main() -> int:
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported in this build "
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
               "(the step is data-parallel across GPUs with only the LoRA gradients exchanged).", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():

@@ -1,6 +1,6 @@
 """CPU oracle of Uno's conditional-LoRA block-diffusion training step.
 
-TEST INFRASTRUCTURE ONLY. This package is the parity checker: a plain restatement of the
+TEST INFRASTRUCTURE ONLY. This package is the parity reference: a plain restatement of the
 reference algorithm (fp32 PyTorch on the CPU, numpy for the integer hashing). Only the
 test-suite, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import
 it, and only to check or to time the reference algorithm -- never as the product path.

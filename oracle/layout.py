@@ -15,7 +15,7 @@ IGNORE_INDEX = -100
 
 
 def modify_padded_position_ids_2d(position_ids: torch.Tensor) -> torch.Tensor:
-    """Contract: positions are returned unchanged (no padding markers in this build's data)."""
+    """Contract: positions are returned unchanged (rows carry no padding markers in the training data)."""
     return position_ids.clone()
 
 

@@ -71,7 +71,7 @@ class UnoQwen3Config:
 # Module-level helpers looked up by training/modeling.py:47-62
 # ------------------------------------------------------------------------------------------
 def modify_padded_position_ids_2d(position_ids: torch.Tensor) -> torch.Tensor:
-    """Positions pass through unchanged (rows carry no padding markers in this build's data)."""
+    """Positions pass through unchanged (rows carry no padding markers in the training data)."""
     return position_ids.clone()
 
 
