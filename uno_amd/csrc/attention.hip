@@ -867,72 +867,31 @@ static int check_geom(int dtype, int D, int Hq, int Hkv) {
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Queries per wave in the forward: 32 (QG = 1, two workgroups per CU) or 64 (QG = 2, one).
-// UNOK_ATTN_QG selects, for tuning.
-static int attn_qg() {
-  static int q = [] {
-    const char* e = getenv("UNOK_ATTN_QG");
-    return (e && atoi(e) == 2) ? 2 : 1;
-  }();
-  return q;
-}
-
-template <int D, int QG>
-static void launch_fwd_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
+// Forward: 32 queries per wave, 128 per workgroup, two workgroups per CU.
+template <int D>
+static void launch_fwd(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
   constexpr size_t lds = 4 * ATT_BK * D * sizeof(bf16_t);
-  static bool configured = false;
-  if (!configured) {
-    hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<D, QG>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    configured = true;
-  }
-  const unsigned blocks = (unsigned)(((Mq + 128 * QG - 1) / (128 * QG)) * Hq);
-  hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, QG>), dim3(blocks), dim3(256), lds, st, a);
+  UNOK_SET_LDS_ONCE((attn_fwd_bf16_kernel<D, 1>), lds);
+  const unsigned blocks = (unsigned)(((Mq + 127) / 128) * Hq);
+  hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 1>), dim3(blocks), dim3(256), lds, st, a);
 }
 
-// Waves per dQ workgroup: 4 (128 queries, two independent workgroups per CU, whose phases
-// interleave on each SIMD; the default) or 8 (256 queries, one workgroup per CU: the two waves of
-// a SIMD then pass the same per-tile barrier and stall together). UNOK_ATTN_DQ_WAVES selects.
-static int attn_dq_waves() {
-  static int w = [] {
-    const char* e = getenv("UNOK_ATTN_DQ_WAVES");
-    return (e && atoi(e) == 8) ? 8 : 4;
-  }();
-  return w;
-}
-
-template <int D, int NW>
-static void launch_dq_t(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
-  constexpr size_t lds = 4 * ATT_BK * D * sizeof(bf16_t);
-  static bool configured = false;
-  if (!configured) {
-    hipFuncSetAttribute((const void*)attn_dq_bf16_kernel<D, NW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    configured = true;
-  }
-  const unsigned blocks = (unsigned)(((Mq + 32 * NW - 1) / (32 * NW)) * Hq);
-  hipLaunchKernelGGL((attn_dq_bf16_kernel<D, NW>), dim3(blocks), dim3(NW * 64), lds, st, a);
-}
-
+// dQ: 4 waves of 32 queries per workgroup, two independent workgroups per CU (their phases
+// interleave on each SIMD; with one 8-wave workgroup the two waves of a SIMD pass the same per-tile
+// barrier and stall together).
 template <int D>
 static void launch_dq(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
-  if (attn_dq_waves() == 4) launch_dq_t<D, 4>(Mq, Hq, st, a);
-  else launch_dq_t<D, 8>(Mq, Hq, st, a);
+  constexpr size_t lds = 4 * ATT_BK * D * sizeof(bf16_t);
+  UNOK_SET_LDS_ONCE((attn_dq_bf16_kernel<D, 4>), lds);
+  const unsigned blocks = (unsigned)(((Mq + 127) / 128) * Hq);
+  hipLaunchKernelGGL((attn_dq_bf16_kernel<D, 4>), dim3(blocks), dim3(256), lds, st, a);
 }
 
 template <int D>
 static void launch_dkv(unsigned blocks, hipStream_t st, const AttnArgs& a) {
   constexpr size_t lds = 4 * 2 * 32 * D * sizeof(bf16_t);
-  static bool configured = false;
-  if (!configured) {
-    hipFuncSetAttribute((const void*)attn_dkv_bf16_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    configured = true;
-  }
+  UNOK_SET_LDS_ONCE(attn_dkv_bf16_kernel<D>, lds);
   hipLaunchKernelGGL(attn_dkv_bf16_kernel<D>, dim3(blocks), dim3(256), lds, st, a);
-}
-
-template <int D>
-static void launch_fwd(int Mq, int Hq, hipStream_t st, const AttnArgs& a) {
-  if (attn_qg() == 2) launch_fwd_t<D, 2>(Mq, Hq, st, a);
-  else launch_fwd_t<D, 1>(Mq, Hq, st, a);
 }
 
 // Forward. K2/V2 may be null (single source). Strides in elements.

@@ -41,6 +41,18 @@ int check_launch(const char* what);
     if (!(cond)) return unok::set_error((code), __VA_ARGS__); \
   } while (0)
 
+// Raises a kernel's dynamic-LDS limit once per process. The function-local static is initialised
+// under the C++ runtime's guard, so concurrent first launches from the autograd worker thread and
+// the main thread are safe.
+#define UNOK_SET_LDS_ONCE(kernel, bytes)                                                                \
+  do {                                                                                                  \
+    static const bool lds_set_ = [] {                                                                   \
+      hipFuncSetAttribute((const void*)(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)(bytes)); \
+      return true;                                                                                      \
+    }();                                                                                                \
+    (void)lds_set_;                                                                                     \
+  } while (0)
+
 // ---------------------------------------------------------------------------------------
 // bf16 helpers. bf16 values travel as uint16_t bit patterns; conversions use
 // round-to-nearest-even, the rounding torch uses for float -> bfloat16.

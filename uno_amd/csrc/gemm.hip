@@ -359,13 +359,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT 
 }
 
 // ---------------------------------------------------------------------------------------
-// 256x256 bf16 NT kernel with four waves, each owning a 128x128 block of C (16 accumulator
-// tiles of 32x32 in AGPRs). Per MFMA this halves the LDS operand traffic of the 8-wave layout
-// (8 fragment reads per 16 MFMAs instead of 6 per 8), which is what bounds the 8-wave kernel:
-// LDS reads + direct-to-LDS writes of a K tile equal its MFMA time there. Operand fragments are
-// double-buffered in VGPRs: the reads for step ks+1 are issued before the MFMAs of step ks, and
-// the first fragments of the next K tile are read right after the per-tile barrier, so the MFMA
-// pipe is never waiting on LDS latency. K tiles stream in through two direct-to-LDS stages.
+// Helpers of the 256x256 direct-to-LDS kernel below: buffer resources and 4-wide epilogue stores.
 // ---------------------------------------------------------------------------------------
 // Buffer resource over `bytes` bytes from `base` (raw buffer: stride 0, dword 3 = data format).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -393,290 +387,6 @@ __device__ __forceinline__ void store4(float* dst, const float* res, const float
     o.x += r.x; o.y += r.y; o.z += r.z; o.w += r.w;
   }
   *(float4*)dst = o;
-}
-
-template <int BK, int STAGES, typename OutT, int SCHED>
-__global__ __launch_bounds__(256) void gemm_nt_bf16_w4_kernel(const GemmNT p) {
-  constexpr int BM = 256, BN = 256, NW = 4;
-  constexpr int TM = 4, TN = 4;
-  constexpr int KS = BK / 16;                   // MFMA K steps per tile
-  constexpr int CPR = BK / 8;                   // 16-byte chunks per tile row
-  constexpr int RPI = 64 / CPR;                 // tile rows per load instruction
-  constexpr int INS = BM / (RPI * NW);          // load instructions per wave per operand
-  constexpr int LPT = 2 * INS;                  // loads per wave per tile
-  static_assert(KS % 2 == 0 && STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * LPT < 64, "bad config");
-  static_assert(SCHED == 0 || (STAGES == 2 && BK == 64), "the explicit schedules are written for 2 stages of BK 64");
-  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
-  bf16_t* As = smem;                            // [STAGES][BM*BK]
-  bf16_t* Bs = smem + STAGES * BM * BK;         // [STAGES][BN*BK]
-
-  const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
-  const int lin = xcd_remap(blockIdx.x, nM * nN);
-  constexpr int GROUP = 8;
-  const int group = lin / (GROUP * nN);
-  const int first_m = group * GROUP;
-  const int gsz = min(nM - first_m, GROUP);
-  const int ing = lin % (GROUP * nN);
-  const int m0 = (first_m + ing % gsz) * BM;
-  const int n0 = (ing / gsz) * BN;
-
-  const bool ext = p.A2 != nullptr && p.K2 > 0;
-  const int nk1 = p.K / BK;
-  const int nk = nk1 + (ext ? p.K2 / BK : 0);
-
-  // Direct-to-LDS sources: lane -> (row lane/CPR of an RPI-row group, 16-byte slot lane%CPR);
-  // the byte offsets of the rows this lane loads (clamped to the last row) are fixed per
-  // operand pair. Byte ranges were checked on the host to fit 32 bits.
-  const int lrowi = lane / CPR, slot = lane % CPR;
-  __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(((int64_t)(p.M - 1) * p.lda + p.K) * 2));
-  __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)(((int64_t)(p.N - 1) * p.ldb + p.K) * 2));
-  uint32_t a_vo[INS], b_vo[INS];
-  auto set_offsets = [&](int64_t lda, int64_t ldb) {
-#pragma unroll
-    for (int i = 0; i < INS; ++i) {
-      const int r = (i * NW + wid) * RPI + lrowi;
-      const int chunk = slot ^ dma_swz<BK>(r);
-      a_vo[i] = (uint32_t)(((int64_t)min(m0 + r, p.M - 1) * lda + chunk * 8) * 2);
-      b_vo[i] = (uint32_t)(((int64_t)min(n0 + r, p.N - 1) * ldb + chunk * 8) * 2);
-    }
-  };
-  set_offsets(p.lda, p.ldb);
-  int kbase = 0;
-  // Tiles are issued in order; tile nk1 switches to the LoRA operand pair (A2, B2).
-  auto issue = [&](int kt, int buf) {
-    if (kt == nk1) {
-      ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0), (uint32_t)(((int64_t)(p.M - 1) * p.lda2 + p.K2) * 2));
-      rb = make_rsrc(p.B2, (uint32_t)(((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2));
-      set_offsets(p.lda2, p.ldb2);
-      kbase = nk1;
-    }
-    bf16_t* as = As + buf * BM * BK + wid * RPI * BK;
-    bf16_t* bs = Bs + buf * BN * BK + wid * RPI * BK;
-    const uint32_t kb = (uint32_t)(kt - kbase) * BK * 2;
-#pragma unroll
-    for (int i = 0; i < INS; ++i) buf_lds16(ra, a_vo[i], kb, as + i * NW * RPI * BK);
-#pragma unroll
-    for (int i = 0; i < INS; ++i) buf_lds16(rb, b_vo[i], kb, bs + i * NW * RPI * BK);
-  };
-  // Wait until this wave's LDS reads have returned (unconditionally, so the compiler's wait
-  // tracking knows it) and its loads of tile t have landed, `later` tiles having been issued
-  // after tile t.
-  auto wait_tile = [&](int later) {
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
-    if (STAGES > 4 && later >= 3) wait_vm<(STAGES > 4 ? 3 * LPT : 0)>();
-    else if (STAGES > 3 && later >= 2) wait_vm<(STAGES > 3 ? 2 * LPT : 0)>();
-    else if (STAGES > 2 && later >= 1) wait_vm<(STAGES > 2 ? LPT : 0)>();
-    else wait_vm<0>();
-  };
-
-  // Fragment reads: rows wm*128 + 32i + lrow (A) / wn*128 + 32j + lrow (B); every such row has
-  // the same swizzle dma_swz(lrow), so only the chunk term varies with ks.
-  const int wm = wid >> 1, wn = wid & 1;
-  const int lrow = lane & 31, lg = lane >> 5;
-  const int sw = dma_swz<BK>(lrow);
-  const int a_row0 = (wm * 128 + lrow) * BK, b_row0 = (wn * 128 + lrow) * BK;
-  bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
-  auto load_frags = [&](bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN], int buf, int ks) {
-    const bf16_t* as = As + buf * BM * BK + a_row0;
-    const bf16_t* bs = Bs + buf * BN * BK + b_row0;
-    const int co = ((ks * 2 + lg) ^ sw) << 3;
-    // Read in the order the next step's MFMAs consume them: fa[0], all of fb, then fa[1..3].
-    fa[0] = *(const bf16x8_t*)&as[co];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[j] = *(const bf16x8_t*)&bs[j * 32 * BK + co];
-#pragma unroll
-    for (int i = 1; i < TM; ++i) fa[i] = *(const bf16x8_t*)&as[i * 32 * BK + co];
-  };
-
-  f32x16_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  // The product is formed transposed (B fragment as the MFMA's first operand), so that each lane
-  // ends up holding 4 consecutive output columns of one row: acc[i][j][4k + q] =
-  // C[wm*128 + 32i + lrow][wn*128 + 32j + 8k + 4lg + q], stored as one 8/16-byte vector.
-  auto mfmas = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[TN]) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-  };
-  // 8 fragment reads spread over the first 8 of 16 MFMAs, then the remaining 8 MFMAs.
-  auto interleave = [&]() {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 8, 0);
-  };
-
-  if constexpr (SCHED == 0) {
-    // All STAGES stages are filled up front; afterwards the stage of tile kt is refilled with tile
-    // kt + STAGES right after the barrier that ends its reads, so every load has a full tile of
-    // MFMA work per stage ahead of it to land.
-  #pragma unroll
-    for (int t = 0; t < STAGES; ++t)
-      if (t < nk) issue(t, t);
-    wait_tile(min(nk - 1, STAGES - 1));
-    asm volatile("s_barrier" ::: "memory");
-    load_frags(fa0, fb0, 0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt % STAGES;
-      const bool more = kt + 1 < nk;
-      __builtin_amdgcn_sched_barrier(0);
-  #pragma unroll
-      for (int ks = 0; ks + 1 < KS; ++ks) {
-        if (ks % 2 == 0) { load_frags(fa1, fb1, cur, ks + 1); mfmas(fa0, fb0); }
-        else { load_frags(fa0, fb0, cur, ks + 1); mfmas(fa1, fb1); }
-        interleave();
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // Every read of stage `cur` by this wave has been issued and has returned; once each wave is
-      // here with its loads of tile kt+1 landed, tile kt+1 is complete in LDS. Tiles up to
-      // kt + STAGES - 1 have been issued so far.
-      wait_tile(min(nk - 1, kt + STAGES - 1) - (kt + 1));
-      asm volatile("s_barrier" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      if (kt + STAGES < nk) issue(kt + STAGES, cur);
-      if (more) load_frags(fa0, fb0, (kt + 1) % STAGES, 0);
-      mfmas(fa1, fb1);
-      if (more) interleave();
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else {
-    // Fixed instruction order per step: 16 MFMAs; after every second one a fragment read for the
-    // next step (in the order that step consumes them: fa[0], fb[0..3], fa[1..3]); and the
-    // direct-to-LDS loads of the tile two ahead spread evenly over the step(s) that issue them
-    // (SCHED 1: all 16 in step 3; SCHED 2: its A half in step 3, its B half in step 0 of the next
-    // tile). A burst of loads fills the load queue and stalls the in-order issue of the MFMAs
-    // behind it. Tiles past the end are clamped to the last one, so the instruction stream has
-    // no branches; a clamped tile lands in a stage that is never read again.
-    const int co0 = lg ^ sw;
-    auto step = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[TN], bf16x8_t (&na)[TM], bf16x8_t (&nb)[TN],
-                    int rstage, int rks, auto dma_n, int dma_lo, uint32_t kb, int dstage) {
-      constexpr int ND = decltype(dma_n)::value;
-      constexpr int EVERY = ND ? TM * TN / ND : 1;
-      const bf16_t* fas = As + rstage * BM * BK + a_row0;
-      const bf16_t* fbs = Bs + rstage * BN * BK + b_row0;
-      const int co = ((rks * 2) ^ co0) << 3;    // chunk (2 rks + lg) ^ sw
-      bf16_t* das = As + dstage * BM * BK + wid * RPI * BK;
-      bf16_t* dbs = Bs + dstage * BN * BK + wid * RPI * BK;
-#pragma unroll
-      for (int idx = 0; idx < TM * TN; ++idx) {
-        const int i = idx / TN, j = idx % TN;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-        if (ND && idx % EVERY == 0) {
-          const int n = dma_lo + idx / EVERY;
-          if (n < INS) buf_lds16(ra, a_vo[n], kb, das + n * NW * RPI * BK);
-          else buf_lds16(rb, b_vo[n - INS], kb, dbs + (n - INS) * NW * RPI * BK);
-        }
-        if (idx % 2 == 0) {
-          const int r = idx / 2;
-          if (r == 0) na[0] = *(const bf16x8_t*)&fas[co];
-          else if (r <= TN) nb[r - 1] = *(const bf16x8_t*)&fbs[(r - 1) * 32 * BK + co];
-          else na[r - TN] = *(const bf16x8_t*)&fas[(r - TN) * 32 * BK + co];
-        }
-      }
-#pragma unroll
-      for (int idx = 0; idx < TM * TN; ++idx) {
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-        if (ND && idx % EVERY == 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
-        if (idx % 2 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    // Sets up the operand pair of tile t (switching to the LoRA pair at tile nk1; tiles are set
-    // up in order) and returns its k byte offset.
-    auto dma_tile = [&](int t) -> uint32_t {
-      if (t == nk1) {
-        ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0), (uint32_t)(((int64_t)(p.M - 1) * p.lda2 + p.K2) * 2));
-        rb = make_rsrc(p.B2, (uint32_t)(((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2));
-        set_offsets(p.lda2, p.ldb2);
-        kbase = nk1;
-      }
-      return (uint32_t)(t - kbase) * BK * 2;
-    };
-    using D0 = std::integral_constant<int, 0>;
-    using DH = std::integral_constant<int, INS>;
-    using DF = std::integral_constant<int, 2 * INS>;
-
-    // Prologue: tile 0 whole, tile 1 (clamped) whole (SCHED 1) or its A half (SCHED 2).
-    issue(0, 0);
-    uint32_t kb_next = dma_tile(min(1, nk - 1));
-    {
-      bf16_t* as = As + 1 * BM * BK + wid * RPI * BK;
-      bf16_t* bs = Bs + 1 * BN * BK + wid * RPI * BK;
-#pragma unroll
-      for (int i = 0; i < INS; ++i) buf_lds16(ra, a_vo[i], kb_next, as + i * NW * RPI * BK);
-      if constexpr (SCHED == 1) {
-#pragma unroll
-        for (int i = 0; i < INS; ++i) buf_lds16(rb, b_vo[i], kb_next, bs + i * NW * RPI * BK);
-      }
-    }
-    if constexpr (SCHED == 1) wait_vm<2 * INS>(); else wait_vm<INS>();   // tile 0 landed
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    asm volatile("s_barrier" ::: "memory");
-    load_frags(fa0, fb0, 0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1, nxt = cur ^ 1;
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (SCHED == 2) step(fa0, fb0, fa1, fb1, cur, 1, DH{}, INS, kb_next, nxt);  // B half of tile kt+1
-      else step(fa0, fb0, fa1, fb1, cur, 1, D0{}, 0, 0u, 0);
-      step(fa1, fb1, fa0, fb0, cur, 2, D0{}, 0, 0u, 0);
-      step(fa0, fb0, fa1, fb1, cur, 3, D0{}, 0, 0u, 0);
-      // Tile kt+1 is complete once every wave is here with all its loads landed (nothing after
-      // tile kt+1 has been issued yet) and its reads of stage cur returned.
-      __builtin_amdgcn_s_waitcnt(0x0070);
-      asm volatile("s_barrier" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      kb_next = dma_tile(min(kt + 2, nk - 1));
-      if constexpr (SCHED == 2) step(fa1, fb1, fa0, fb0, nxt, 0, DH{}, 0, kb_next, cur);   // A half of tile kt+2
-      else step(fa1, fb1, fa0, fb0, nxt, 0, DF{}, 0, kb_next, cur);
-    }
-    __builtin_amdgcn_s_waitcnt(0x0070);       // clamped loads still write LDS
-  }
-
-  // Epilogue: 4 consecutive columns per lane and row -> one 8-byte (bf16) / 16-byte (fp32)
-  // store, residual read the same way. Columns come in groups of 4 (N % 4 == 0 on the host).
-  // Interior tiles without a gate take a branch-free path.
-  OutT* C = (OutT*)p.C;
-  const OutT* R = (const OutT*)p.R;
-  auto epilogue = [&](auto has_res, auto checked) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int row = m0 + wm * 128 + i * 32 + lrow;
-      if (checked && row >= p.M) continue;
-      const float sc = (!checked || p.gate == nullptr || p.gate[row] != 0) ? p.alpha : 0.f;
-      OutT* crow = C + (int64_t)row * p.ldc;
-      const OutT* rrow = has_res ? R + (int64_t)row * p.ldr : nullptr;
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int col = n0 + wn * 128 + j * 32 + k * 8 + lg * 4;
-          if (checked && col >= p.N) continue;
-          float v[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * k + q] * sc;
-          store4(crow + col, has_res ? rrow + col : nullptr, v);
-        }
-      }
-    }
-  };
-  const bool interior = m0 + BM <= p.M && n0 + BN <= p.N && p.gate == nullptr;
-  if (R) {
-    if (interior) epilogue(std::true_type{}, std::false_type{}); else epilogue(std::true_type{}, std::true_type{});
-  } else {
-    if (interior) epilogue(std::false_type{}, std::false_type{}); else epilogue(std::false_type{}, std::true_type{});
-  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1409,42 +1119,17 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
 // Row tiles per tile group (tiles are walked group by group, column by column inside a group; an
 // XCD's 32 concurrent workgroups then cover group x 32/group tiles). Long-K products run faster
 // with groups of 4 (measured: 16384 x 4096 x 12288 1.25 -> 1.21 ms, x 24576 2.47 -> 2.42 ms),
-// the others with 8. UNOK_GEMM_GROUP overrides, for tuning.
-static int w4m16_group(int K) {
-  static const int g = [] { const char* e = getenv("UNOK_GEMM_GROUP"); return e ? atoi(e) : 0; }();
-  return g > 0 ? g : (K >= 8192 ? 4 : 8);
-}
+// the others with 8.
+static int w4m16_group(int K) { return K >= 8192 ? 4 : 8; }
 
 template <typename OutT, int EPI = 0>
 static void launch_nt_w4m16(const GemmNT& p0, hipStream_t st) {
   GemmNT p = p0;
   p.group = w4m16_group(p.K + p.K2);
   constexpr size_t lds = 2 * (256 + 256) * 64 * sizeof(bf16_t);
-  static bool configured = false;
-  if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4m16_kernel<OutT, EPI>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    configured = true;
-  }
+  UNOK_SET_LDS_ONCE((gemm_nt_bf16_w4m16_kernel<OutT, EPI>), lds);
   const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
   hipLaunchKernelGGL((gemm_nt_bf16_w4m16_kernel<OutT, EPI>), dim3(nb), dim3(256), lds, st, p);
-}
-
-// Configuration of the 256x256 direct-to-LDS kernel (UNOK_GEMM_CFG selects one, for tuning):
-//   0: 8 waves, BK 64, 2 stages   1: 8 waves, BK 32, 4 stages   2: 8 waves, BK 32, 5 stages
-//   3: 4 waves, BK 32, 4 stages   4: 4 waves, BK 64, 2 stages
-//   5/6/7: 4 waves of 128x128, VGPR double-buffered fragments; BK 64 x 2 stages / BK 32 x 4 / BK 32 x 5
-//      (5: each tile's direct-to-LDS loads spread over two MFMA steps, A half then B half)
-//   8: as 5, with the next tiles' loads issued as one burst and fragment reads bunched per step
-//   9: as 5, with all 16 loads of a tile spread over one MFMA step
-//  10: 4 waves of 128x128 with 16x16x32 MFMAs (BK 64 x 2 stages); the default
-static int dma_cfg() {
-  static int c = [] {
-    const char* e = getenv("UNOK_GEMM_CFG");
-    const int v = e ? atoi(e) : 10;
-    return (v >= 0 && v <= 10) ? v : 10;
-  }();
-  return c;
 }
 
 // The 4-wave kernel addresses operands through buffer resources with 32-bit byte offsets and
@@ -1458,79 +1143,29 @@ static bool buffer_ranges_ok(const GemmNT& p) {
   return true;
 }
 
-template <int BK, int STAGES, typename OutT, int SCHED>
-static void launch_nt_w4(const GemmNT& p, hipStream_t st) {
-  constexpr size_t lds = (size_t)STAGES * (256 + 256) * BK * sizeof(bf16_t);
-  static bool configured = false;
-  if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SCHED>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    configured = true;
-  }
-  const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
-  hipLaunchKernelGGL((gemm_nt_bf16_w4_kernel<BK, STAGES, OutT, SCHED>), dim3(nb), dim3(256), lds, st, p);
-}
-
 template <int BM, int BN, int NW, int BK, int STAGES, typename OutT, bool ROT = false>
 static void launch_nt_dma_t(const GemmNT& p, hipStream_t st) {
   constexpr size_t lds = (size_t)STAGES * (BM + BN) * BK * sizeof(bf16_t);
-  static bool configured = false;
-  if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT, ROT>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    configured = true;
-  }
+  UNOK_SET_LDS_ONCE((gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT, ROT>), lds);
   const int nb = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   hipLaunchKernelGGL((gemm_nt_bf16_dma_kernel<BM, BN, NW, BK, STAGES, OutT, ROT>), dim3(nb), dim3(NW * 64), lds, st, p);
 }
 
+// Large products: the 256x256 16x16x32-MFMA kernel; operands beyond its 32-bit buffer offsets
+// take the 8-wave direct-to-LDS kernel, which addresses them with 64-bit pointers.
 template <typename OutT>
-static void launch_nt_dma_o(const GemmNT& p, hipStream_t st) {
-  switch (dma_cfg()) {
-    case 1: launch_nt_dma_t<256, 256, 8, 32, 4, OutT>(p, st); break;
-    case 2: launch_nt_dma_t<256, 256, 8, 32, 5, OutT>(p, st); break;
-    case 3: launch_nt_dma_t<256, 256, 4, 32, 4, OutT>(p, st); break;
-    case 4: launch_nt_dma_t<256, 256, 4, 64, 2, OutT>(p, st); break;
-    case 5:
-    case 6:
-    case 7:
-    case 8:
-    case 9:
-    case 10:
-      if (!buffer_ranges_ok(p)) { launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break; }
-      if (dma_cfg() == 5) launch_nt_w4<64, 2, OutT, 2>(p, st);
-      else if (dma_cfg() == 8) launch_nt_w4<64, 2, OutT, 0>(p, st);
-      else if (dma_cfg() == 9) launch_nt_w4<64, 2, OutT, 1>(p, st);
-      else if (dma_cfg() == 10) launch_nt_w4m16<OutT>(p, st);
-      else if (dma_cfg() == 6) launch_nt_w4<32, 4, OutT, 0>(p, st);
-      else launch_nt_w4<32, 5, OutT, 0>(p, st);
-      break;
-    default: launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st); break;
-  }
+static void launch_nt_large(const GemmNT& p, hipStream_t st) {
+  if (buffer_ranges_ok(p)) launch_nt_w4m16<OutT>(p, st);
+  else launch_nt_dma_t<256, 256, 8, 64, 2, OutT>(p, st);
 }
 
-template <int BM, int BN, int NW, int BK, int STAGES, bool ROT = false>
-static void launch_nt_dma_o2(const GemmNT& p, int out_dtype, hipStream_t st) {
-  if (out_dtype == UNOK_F32) launch_nt_dma_t<BM, BN, NW, BK, STAGES, float, ROT>(p, st);
-  else launch_nt_dma_t<BM, BN, NW, BK, STAGES, bf16_t, ROT>(p, st);
-}
-
-// Skinny NT path (N <= 192): 1 = 64xN tiles with 4 LDS stages for N <= 128 and 3 for N <= 192,
-// 2 = 2 stages, 3 = 4 stages, 4 = 5 stages, 5 = 8 / 6 / 4 stages, 6 = as 1 with each workgroup's
-// K walk rotated (default; the concurrent reads then spread over the rows' column offsets instead
-// of all hitting the same one), 0 = off (register-staged 128x64 / 128x128 tiles).
-// UNOK_SKINNY_CFG selects one, for tuning.
-static int skinny_cfg() {
-  static int c = [] {
-    const char* e = getenv("UNOK_SKINNY_CFG");
-    const int v = e ? atoi(e) : 6;
-    return (v >= 0 && v <= 6) ? v : 6;
-  }();
-  return c;
-}
-
-static void launch_nt_dma(const GemmNT& p, int out_dtype, hipStream_t st) {
-  if (out_dtype == UNOK_F32) launch_nt_dma_o<float>(p, st); else launch_nt_dma_o<bf16_t>(p, st);
+// Skinny products (N <= 192): one 64 x N tile spans every output column, 4 LDS stages for
+// N <= 128 and 3 for N <= 192, each workgroup's K walk rotated so that the concurrent reads
+// spread over the rows' column offsets instead of all hitting the same one.
+template <int BN, int STAGES>
+static void launch_nt_skinny_t(const GemmNT& p, int out_dtype, hipStream_t st) {
+  if (out_dtype == UNOK_F32) launch_nt_dma_t<64, BN, 4, 64, STAGES, float, true>(p, st);
+  else launch_nt_dma_t<64, BN, 4, 64, STAGES, bf16_t, true>(p, st);
 }
 
 // C = alpha * gate (.) (A B^T + A2[:, seg_col] B2^T) + R.
@@ -1640,36 +1275,12 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
     return true;
   };
   const long long big_tiles = (long long)((M + 255) / 256) * ((N + 255) / 256);
-  const int sk = skinny_cfg();
-  if (sk > 0 && N <= 192 && !p.A2 && K % 64 == 0 && M >= 4096) {
-    // Skinny products (LoRA x·Aᵀ and dY·B, N = r .. 3r): one 64-row tile spans all N columns, so
-    // every activation row is read from HBM once; 4 waves, direct-to-LDS loads, 3-4 stages.
+  if (N <= 192 && !p.A2 && K % 64 == 0 && M >= 4096) {
+    // Skinny products (LoRA x·Aᵀ and dY·B, N = r .. 3r): every activation row is read from HBM once.
     const int bn = (N + 63) / 64 * 64;
-    if (sk == 1) {
-      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 4>(p, out_dtype, st);
-      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 4>(p, out_dtype, st);
-      else launch_nt_dma_o2<64, 192, 4, 64, 3>(p, out_dtype, st);
-    } else if (sk == 3) {
-      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 4>(p, out_dtype, st);
-      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 4>(p, out_dtype, st);
-      else launch_nt_dma_o2<64, 192, 4, 64, 4>(p, out_dtype, st);
-    } else if (sk == 6) {
-      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 4, true>(p, out_dtype, st);
-      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 4, true>(p, out_dtype, st);
-      else launch_nt_dma_o2<64, 192, 4, 64, 3, true>(p, out_dtype, st);
-    } else if (sk == 5) {
-      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 8>(p, out_dtype, st);
-      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 6>(p, out_dtype, st);
-      else launch_nt_dma_o2<64, 192, 4, 64, 4>(p, out_dtype, st);
-    } else if (sk == 4) {
-      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 5>(p, out_dtype, st);
-      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 5>(p, out_dtype, st);
-      else launch_nt_dma_o2<64, 192, 4, 64, 5>(p, out_dtype, st);
-    } else {
-      if (bn == 64) launch_nt_dma_o2<64, 64, 4, 64, 2>(p, out_dtype, st);
-      else if (bn == 128) launch_nt_dma_o2<64, 128, 4, 64, 2>(p, out_dtype, st);
-      else launch_nt_dma_o2<64, 192, 4, 64, 2>(p, out_dtype, st);
-    }
+    if (bn == 64) launch_nt_skinny_t<64, 4>(p, out_dtype, st);
+    else if (bn == 128) launch_nt_skinny_t<128, 4>(p, out_dtype, st);
+    else launch_nt_skinny_t<192, 3>(p, out_dtype, st);
   } else if (N <= 64 || !segs_ok(128)) {
     UNOK_REQUIRE(segs_ok(64), UNOK_EINVAL, "gemm_nt(bf16): segment ends must be multiples of 64");
     launch_nt_bf16<128, 64>(p, out_dtype, st);
@@ -1677,7 +1288,7 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
     if ((long long)((M + 127) / 128) * ((N + 127) / 128) < 256) launch_nt_bf16<64, 128>(p, out_dtype, st);
     else launch_nt_bf16<128, 128>(p, out_dtype, st);
   } else if (K % 64 == 0 && (!p.A2 || p.K2 % 64 == 0)) {
-    launch_nt_dma(p, out_dtype, st);
+    if (out_dtype == UNOK_F32) launch_nt_large<float>(p, st); else launch_nt_large<bf16_t>(p, st);
   } else {
     launch_nt_bf16<256, 256>(p, out_dtype, st);
   }
@@ -1694,15 +1305,8 @@ static int tn_general_splits(int Mrows, int P, int Q) {
   return nsplit < 1 ? 1 : (int)nsplit;
 }
 
-// Workgroups the skinny TN kernel aims for (UNOK_TN_WORKGROUPS overrides, for tuning).
-static int tn_skinny_target() {
-  static int t = [] {
-    const char* e = getenv("UNOK_TN_WORKGROUPS");
-    const int v = e ? atoi(e) : 256;
-    return v < 16 ? 16 : (v > 4096 ? 4096 : v);
-  }();
-  return t;
-}
+// Workgroups the register-transposing skinny TN kernel aims for: one per CU.
+static int tn_skinny_target() { return 256; }
 
 static int tn_skinny_splits(int Mrows, int NX) {
   const int nstrip = (NX + TNS_QB - 1) / TNS_QB;
@@ -1811,25 +1415,11 @@ __global__ __launch_bounds__(256, NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const
   }
 }
 
-// Skinny TN kernel choice: 1 = transpose-load kernel for NS in {64, 128} (default), 0 = the
-// register-transposing kernel for every NS. UNOK_TN_CFG selects, for tuning.
-static int tn_cfg() {
-  static int c = [] {
-    const char* e = getenv("UNOK_TN_CFG");
-    return (e && atoi(e) == 0) ? 0 : 1;
-  }();
-  return c;
-}
-
 template <int NS>
 static void launch_tn_tr_t(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
   constexpr size_t lds = 2 * 64 * (128 + NS) * sizeof(bf16_t);
-  static bool configured = false;
-  if (!configured) {
-    hipFuncSetAttribute((const void*)gemm_tn_tr_kernel<NS, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipFuncSetAttribute((const void*)gemm_tn_tr_kernel<NS, false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    configured = true;
-  }
+  UNOK_SET_LDS_ONCE((gemm_tn_tr_kernel<NS, true>), lds);
+  UNOK_SET_LDS_ONCE((gemm_tn_tr_kernel<NS, false>), lds);
   const int nstrip = (p.NX + 127) / 128;
   if (tout)
     hipLaunchKernelGGL((gemm_tn_tr_kernel<NS, true>), dim3(nstrip * nz), dim3(256), lds, st, p);
@@ -1870,9 +1460,10 @@ static void launch_tn_skinny_t(const GemmTNSkinny& p, int nz, bool tout, hipStre
     hipLaunchKernelGGL((gemm_tn_skinny_kernel<NS, false>), dim3(nstrip * nz), dim3(512), 0, st, p);
 }
 
+// NS = 64 and 128 take the transpose-load kernel; other rank widths the register-transposing one.
 static void launch_tn_skinny(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
-  if (tn_cfg() == 1 && p.NS == 64) { launch_tn_tr_t<64>(p, nz, tout, st); return; }
-  if (tn_cfg() == 1 && p.NS == 128) { launch_tn_tr_t<128>(p, nz, tout, st); return; }
+  if (p.NS == 64) { launch_tn_tr_t<64>(p, nz, tout, st); return; }
+  if (p.NS == 128) { launch_tn_tr_t<128>(p, nz, tout, st); return; }
   switch (p.NS) {
     case 32: launch_tn_skinny_t<32>(p, nz, tout, st); break;
     case 64: launch_tn_skinny_t<64>(p, nz, tout, st); break;
@@ -1904,7 +1495,7 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
     const void* X = a_small ? B : A;
     if (NS % 32 == 0 && NS <= 256 && NX >= TNS_QB && NX % 8 == 0 && lds_ % 8 == 0 && ldx % 8 == 0 &&
         aligned16(S) && aligned16(X)) {
-      const bool tr = tn_cfg() == 1 && (NS == 64 || NS == 128);
+      const bool tr = NS == 64 || NS == 128;
       const int nz0 = tr ? tn_tr_splits(Mrows, NX, NS) : tn_skinny_splits(Mrows, NX);
       int rps = (Mrows + nz0 - 1) / nz0;
       rps = ((rps + TNS_BK - 1) / TNS_BK) * TNS_BK;
