@@ -75,6 +75,17 @@ int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* A, int64_t l
                  const void* B, int64_t ldb, float* C, int64_t ldc, float alpha, float beta,
                  void* workspace, int64_t ws_bytes, void* stream);
 
+/* unok_gemm_tn without a workspace argument and without any device allocation: the split-K
+ * partials live in a 64 MiB array the library holds on each GPU it runs on (resolved on the first
+ * call on that device; the stream must belong to the current device). No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Problems whose partials exceed 64 MiB
+ * (unok_gemm_tn_workspace(Mrows, P, Q) > 67108864) are rejected with -1. All calls on one GPU
+ * share the array: calls that overlap on that GPU race. */
+int unok_gemm_tn_noalloc(int in_dtype, int Mrows, int P, int Q, const void* A, int64_t lda,
+                         const void* B, int64_t ldb, float* C, int64_t ldc, float alpha, float beta,
+                         void* stream);
+
 /* ---- Row-wise decoder ops ----------------------------------------------------------------- */
 
 /* y = w * round(x * rsqrt(mean(x^2) + eps)), rstd[M] saved. Qwen3RMSNorm

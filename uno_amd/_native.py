@@ -31,6 +31,7 @@ SIGNATURES: dict[str, tuple] = {
                                      _p]),
     "unok_gemm_tn_workspace": (_i64, [_i, _i, _i]),
     "unok_gemm_tn": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _f, _f, _p, _i64, _p]),
+    "unok_gemm_tn_noalloc": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _f, _f, _p]),
     "unok_rmsnorm_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _p, _i64, _p, _f, _p]),
     "unok_rmsnorm_bwd": (_i, [_i, _i, _i, _p, _p, _p, _p, _p, _p, _p]),
     "unok_qknorm_rope_fwd": (_i, [_i, _i, _i, _i, _i, _p, _i64, _p, _p, _p, _p, _f, _p, _p, _p, _p]),

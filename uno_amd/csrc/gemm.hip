@@ -1537,3 +1537,58 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, (const float*)workspace, C, ldc, P, Q, nz, beta);
   return unok::check_launch("gemm_tn_reduce");
 }
+
+// ---------------------------------------------------------------------------------------
+// unok_gemm_tn_noalloc: unok_gemm_tn with its split-K partials in a library-held device array
+// instead of a caller workspace, for callers that cannot allocate device memory. The array is a
+// file-scope __device__ object, so every GPU the library runs on holds its own copy (64 MiB)
+// until the process ends. Its device address is resolved once per device, with that device
+// current, by hipGetSymbolAddress on the first call there; the host-side name `scratch` is never
+// passed to a kernel. Every split writes all of its partials before the reduction reads them, so
+// nothing has to be cleared between calls; calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------------------
+#include <mutex>
+
+#define UNOK_TN_SCRATCH_BYTES ((int64_t)64 << 20)
+static __device__ __align__(256) float scratch[UNOK_TN_SCRATCH_BYTES / 4];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices];   // device address of `scratch`, per device (null: not yet resolved)
+}  // namespace
+
+static int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return unok::set_error((int)e, "gemm_tn_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  UNOK_REQUIRE(dev >= 0 && dev < kScratchDevices, UNOK_EUNSUPPORTED, "gemm_tn_noalloc: device %d beyond the %d supported",
+               dev, kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return unok::set_error(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol,
+                             "gemm_tn_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                             hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+UNOK_EXPORT int unok_gemm_tn_noalloc(int in_dtype, int Mrows, int P, int Q, const void* A, int64_t lda,
+                                     const void* B, int64_t ldb, float* C, int64_t ldc, float alpha, float beta,
+                                     void* stream) {
+  UNOK_REQUIRE(Mrows >= 0 && P >= 0 && Q >= 0, UNOK_EINVAL, "gemm_tn_noalloc: negative size");
+  if (P == 0 || Q == 0) return 0;
+  const int64_t need = unok_gemm_tn_workspace(Mrows, P, Q);
+  UNOK_REQUIRE(need <= UNOK_TN_SCRATCH_BYTES, UNOK_EINVAL,
+               "gemm_tn_noalloc: Mrows=%d P=%d Q=%d needs %lld bytes of split-K scratch; the library holds %lld",
+               Mrows, P, Q, (long long)need, (long long)UNOK_TN_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws);
+  if (rc) return rc;
+  return unok_gemm_tn(in_dtype, Mrows, P, Q, A, lda, B, ldb, C, ldc, alpha, beta, ws, UNOK_TN_SCRATCH_BYTES, stream);
+}

@@ -146,6 +146,24 @@ def gemm_tn(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None
     return out
 
 
+def gemm_tn_noalloc(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, *, alpha: float = 1.0,
+                    beta: float = 0.0) -> torch.Tensor:
+    """As ``gemm_tn`` into an existing fp32 ``out``, with the split-K partials in the library's own
+    per-device scratch array: nothing is allocated, by torch or by the library."""
+    _rowmajor(a, "a")
+    _rowmajor(b, "b")
+    _rowmajor(out, "out")
+    if a.shape[0] != b.shape[0] or a.dtype != b.dtype:
+        raise RuntimeError("gemm_tn_noalloc: operands must share rows and dtype")
+    Mr, P = a.shape
+    Q = b.shape[1]
+    if out.dtype != torch.float32 or tuple(out.shape) != (P, Q):
+        raise RuntimeError("gemm_tn_noalloc: out must be fp32 [P,Q]")
+    N.call("unok_gemm_tn_noalloc", N.dtype_code(a.dtype), Mr, P, Q, N.ptr(a), _ld(a), N.ptr(b), _ld(b),
+           N.ptr(out), _ld(out), float(alpha), float(beta), N.stream())
+    return out
+
+
 # ------------------------------------------------------------------------------------------
 # Row-wise kernels
 # ------------------------------------------------------------------------------------------
