@@ -116,8 +116,10 @@ def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813, total_
 def algorithmic_flops(cfg: dict, wl: dict, mask, ce_rows: int, r: int) -> dict:
     """Algorithmically necessary FLOPs of one step from realised counts (recompute excluded):
     base linears forward on both streams + data gradient of the noisy stream, LoRA forward /
-    dgrad / wgrad on noisy rows, attention over allowed pairs only (forward for both streams,
-    dQ for noisy queries and dK/dV for intra-block pairs), LM head forward + dgrad of CE rows."""
+    dgrad / wgrad on noisy rows, attention over allowed pairs only (forward QK^T and PV for both
+    streams: 4d per pair; backward dP = dO V^T and dQ = dS K for noisy queries: 4d per pair, dK and dV
+    for intra-block pairs: 4d per pair; the kernels' recomputation of S in the backward is not
+    counted), LM head forward + dgrad of CE rows."""
     H, F, d = cfg["hidden_size"], cfg["intermediate_size"], cfg["head_dim"]
     q, kv, Lyr, V = cfg["num_attention_heads"] * d, cfg["num_key_value_heads"] * d, cfg["num_hidden_layers"], cfg["vocab_size"]
     Hq = cfg["num_attention_heads"]
@@ -133,7 +135,7 @@ def algorithmic_flops(cfg: dict, wl: dict, mask, ce_rows: int, r: int) -> dict:
         "linear_dgrad": 2 * n_lin * T,
         "lora": 6 * n_lora * T,
         "attn_fwd": 4 * d * Hq * Lyr * (p_clean + p_noisy),
-        "attn_bwd": (6 * d * Hq * p_noisy + 4 * d * Hq * p_intra) * Lyr,
+        "attn_bwd": (4 * d * Hq * p_noisy + 4 * d * Hq * p_intra) * Lyr,
         "lm_head": 2 * H * V * ce_rows * 2,
     }
     f["total"] = sum(f.values())
@@ -259,6 +261,7 @@ def main() -> int:
     blocks = [plan.stage_for_step(min(trainer.state.global_step + i, plan.max_steps - 1)).block_size
               for i in range(args.steps)]
     per_block = {}
+    draws = base._bd_step          # the accounting draw must not move the timed steps' noise stream
     for b in sorted(set(blocks)):
         base.config.block_size = b
         pos, mpos, _ = prepare_uno_layout(base, batch["input_ids"], batch.get("position_ids"))
@@ -267,6 +270,7 @@ def main() -> int:
         shifted = shift_labels_for_next_token(batch["labels"], pos)
         ce_rows = int((noised & (shifted != -100)).sum())
         per_block[b] = algorithmic_flops(cfg, wl, mask, ce_rows, wl["lora_rank"])
+    base._bd_step = draws
     flops = {k: sum(per_block[b][k] for b in blocks) / len(blocks) for k in per_block[blocks[0]]}
 
     rec = K.LaunchRecorder(lambda dt, M, N, Kd, K2, segs: dt == torch.bfloat16 and K.nt_uses_256_tiles(M, N, segs))

@@ -154,6 +154,11 @@ int unok_bd_prepare(int B, int L, const int64_t* ids, const int64_t* pos, const 
                     uint8_t* noised, float* tfull, int32_t* noisy_src, int32_t* clean_src,
                     int32_t* noisy_iv, int32_t* clean_iv, int64_t* noisy_ids,
                     int64_t* clean_ids, void* stream);
+/* region[B, 2L] = the [noisy | clean] per-segment layout mask alone (1 on noisy rows), from the
+ * model positions: segments start at t = 0 and wherever pos[t-1] >= pos[t]. Replaces
+ * calculate_token_nums + _build_noisy_region_mask of prepare_uno_layout
+ * (training/modeling.py:65-81,84-98). */
+int unok_bd_region(int B, int L, const int64_t* pos, uint8_t* region, void* stream);
 /* p_mask = noise level of every noised token in row-major order (training/trainer.py:278). */
 int unok_bd_compact(int64_t n, const uint8_t* noised, const float* tfull, float* p_mask,
                     int32_t* count, void* stream);

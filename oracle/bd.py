@@ -118,7 +118,7 @@ def dense_mask(model_pos: torch.Tensor, block_size: int, intra_block: str = "bid
     return same & (clean_clean | noisy_clean | noisy_noisy)
 
 
-def dense_mask_bruteforce(model_pos: torch.Tensor, block_size: int) -> torch.Tensor:
+def dense_mask_bruteforce(model_pos: torch.Tensor, block_size: int, intra_block: str = "bidirectional") -> torch.Tensor:
     """Pure-Python loop over all pairs (spec restated literally; tiny inputs only)."""
     seg, noisy, j = concat_descriptors(model_pos)
     B, L2 = seg.shape
@@ -135,6 +135,8 @@ def dense_mask_bruteforce(model_pos: torch.Tensor, block_size: int) -> torch.Ten
                     ok = ik // block_size < iq // block_size
                 else:
                     ok = ik // block_size == iq // block_size
+                    if intra_block == "causal":
+                        ok = ok and ik <= iq
                 out[b, q, k] = ok
     return out
 

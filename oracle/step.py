@@ -88,5 +88,5 @@ def train_steps(params, lora, cfg: Cfg, batch: dict, objective: Objective, *, bl
             first_grads = {k: v.grad.detach().clone() for k, v in leaves.items()}
         torch.nn.utils.clip_grad_norm_(list(leaves.values()), max_grad_norm)
         opt.step()
-        hist.append(float(loss))
+        hist.append(float(loss.detach()))
     return hist, first_grads, {k: v.detach() for k, v in leaves.items()}

@@ -161,6 +161,54 @@ def test_bd_prepare_bit_exact(dev, L, bs, packed, noise):
         assert torch.equal(mask.to_dense(), ref[2])
 
 
+def _lognormal_row(total, seed, median=3000, sigma=0.6, lo=512):
+    """Segment lengths of one packed row: log-normal (median, sigma) clipped to [lo, total]."""
+    g = torch.Generator().manual_seed(seed)
+    out, left = [], total
+    while left > 0:
+        n = int(math.exp(math.log(median) + sigma * torch.randn((), generator=g).item()))
+        n = min(max(n, lo), left)
+        out.append(n)
+        left -= n
+    return out
+
+
+@pytest.mark.parametrize("B,L,kind", [(3, 64, "single"), (2, 96, "packed"), (4, 4096, "single"),
+                                      (1, 16384, "lognormal"), (2, 3000, "ones")])
+def test_region_kernel_matches_oracle(dev, B, L, kind):
+    """prepare_uno_layout's region mask (one device kernel) against the oracle's per-segment loop
+    (training/modeling.py:65-81): single rows, packed rows, 16384-token rows of log-normal
+    segments, and rows of length-1 segments (the position never increases)."""
+    if kind == "packed":
+        _, _, pos = _batch(B, L, 512, 8, seed=3, packed=True)
+    elif kind == "lognormal":
+        segs = _lognormal_row(L, seed=11)
+        pos = torch.cat([torch.arange(n) for n in segs]).view(1, L).repeat(B, 1)
+    elif kind == "ones":
+        pos = torch.zeros(B, L, dtype=torch.int64)
+    else:
+        pos = torch.arange(L).view(1, L).repeat(B, 1)
+    from uno_amd.model import noisy_region_mask
+    mine = noisy_region_mask(pos.to(dev)).cpu()
+    ids = torch.zeros(B, L, dtype=torch.int64)
+    _, _, ref = olay.prepare_uno_layout(ids, pos)
+    assert torch.equal(mine, ref)
+
+
+def test_extract_regions_split_any_tensor(dev):
+    """extract_uno_regions on a tensor the decoder did not produce: the device row split equals
+    the reference's boolean indexing (training/modeling.py:101-113)."""
+    from uno_amd.model import noisy_region_mask
+    from uno_amd.training.modeling import extract_uno_regions
+    B, L, H = 2, 96, 64
+    _, _, pos = _batch(B, L, 512, 8, seed=5, packed=True)
+    region = noisy_region_mask(pos.to(dev))
+    hidden = torch.randn(B, 2 * L, H, device=dev).bfloat16()
+    noisy, clean = extract_uno_regions(hidden, region, L)
+    assert torch.equal(noisy, hidden[region].reshape(B, L, H))
+    assert torch.equal(clean, hidden[~region].reshape(B, L, H))
+
+
 # ------------------------------------------------------------------------------------------
 # Attention: two-stream kernels against dense attention over the oracle's mask
 # ------------------------------------------------------------------------------------------
@@ -177,18 +225,25 @@ def _dense_attn(q, k, v, allow, D):
     return o, lse2
 
 
-@pytest.mark.parametrize("dtype,D,L,bs,packed", [(torch.bfloat16, 128, 256, 16, False),
-                                                 (torch.bfloat16, 128, 320, 6, True),
-                                                 (torch.bfloat16, 64, 192, 12, True),
-                                                 (torch.float32, 64, 128, 4, True)])
-def test_block_diffusion_attention(dev, dtype, D, L, bs, packed):
+@pytest.mark.parametrize("dtype,D,L,bs,packed,intra", [(torch.bfloat16, 128, 256, 16, False, "bidirectional"),
+                                                       (torch.bfloat16, 128, 320, 6, True, "bidirectional"),
+                                                       (torch.bfloat16, 64, 192, 12, True, "bidirectional"),
+                                                       (torch.float32, 64, 128, 4, True, "bidirectional"),
+                                                       (torch.bfloat16, 128, 320, 16, True, "causal"),
+                                                       (torch.float32, 64, 128, 6, True, "causal")])
+def test_block_diffusion_attention(dev, dtype, D, L, bs, packed, intra):
+    """Both streams' forward and the noisy stream's dQ/dK/dV against dense attention over the
+    oracle's mask. ``causal`` is the in-block variant the inference draft uses
+    (nano_vllm_uno/layers/attention.py:658-666): noisy token j sees noisy tokens <= j of its block."""
     torch.manual_seed(4)
     B, Hq, Hkv = 2, 4, 2
     ids, labels, pos = _batch(B, L, 512, 8, seed=7, packed=packed)
     _, _, mask, _, _, _ = bd_prepare(ids.to(dev), pos.to(dev), (labels == -100).to(dev), block_size=bs,
-                                     mask_token_id=511)
+                                     mask_token_id=511, intra_block=intra)
     M = B * L
-    dense = obd.dense_mask(pos, bs)                       # oracle mask over the concat layout
+    dense = obd.dense_mask(pos, bs, intra)                # oracle mask over the concat layout
+    if L <= 256:
+        assert torch.equal(mask.to_dense(), dense)
     ns, cs = mask.noisy_src.long().cpu(), mask.clean_src.long().cpu()
     full = torch.zeros(B * 2 * L, B * 2 * L, dtype=torch.bool)
     for b in range(B):

@@ -60,10 +60,29 @@ def test_extract_regions_order():
     assert clean[0, :, 0].tolist() == [4, 6, 10]
 
 
+@pytest.mark.parametrize("intra", ["bidirectional", "causal"])
 @pytest.mark.parametrize("b", [1, 2, 3, 4, 6])
-def test_dense_mask_matches_bruteforce(b):
+def test_dense_mask_matches_bruteforce(b, intra):
     pos = torch.tensor([[0, 1, 2, 3, 4, 5, 6, 0, 1, 2, 3, 4], list(range(12))])
-    assert torch.equal(bd.dense_mask(pos, b), bd.dense_mask_bruteforce(pos, b))
+    assert torch.equal(bd.dense_mask(pos, b, intra), bd.dense_mask_bruteforce(pos, b, intra))
+
+
+@pytest.mark.parametrize("L,b", [(64, 4), (60, 6), (40, 16)])
+def test_causal_intra_block_pair_counts(L, b):
+    """Causal in-block variant: a noisy query at in-block offset o sees o + 1 noisy keys, so a
+    block of size n contributes n(n+1)/2 noisy-noisy pairs instead of n^2; the clean pairs are
+    unchanged; with block size 1 both variants coincide."""
+    pos = torch.arange(L)[None]
+    _, noisy, _ = bd.concat_descriptors(pos)
+    noisy = noisy[0]
+    bi, ca = bd.dense_mask(pos, b)[0], bd.dense_mask(pos, b, "causal")[0]
+    assert torch.equal(bi[~noisy], ca[~noisy])
+    nn_bi = int(bi[noisy][:, noisy].sum())
+    nn_ca = int(ca[noisy][:, noisy].sum())
+    sizes = [min(b, L - s) for s in range(0, L, b)]
+    assert nn_bi == sum(n * n for n in sizes)
+    assert nn_ca == sum(n * (n + 1) // 2 for n in sizes)
+    assert torch.equal(bd.dense_mask(pos, 1), bd.dense_mask(pos, 1, "causal"))
 
 
 @pytest.mark.parametrize("L,b", [(64, 4), (96, 16), (60, 6), (48, 12), (40, 32)])

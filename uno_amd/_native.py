@@ -46,6 +46,7 @@ SIGNATURES: dict[str, tuple] = {
                            _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _f, _p]),
     "unok_bd_prepare": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _u64, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                              _p, _p, _p]),
+    "unok_bd_region": (_i, [_i, _i, _p, _p, _p]),
     "unok_bd_compact": (_i, [_i64, _p, _p, _p, _p, _p]),
     "unok_row_lse_update": (_i, [_i, _i, _i, _p, _i64, _i, _p, _p, _p, _p, _i, _p]),
     "unok_row_argmax_update": (_i, [_i, _i, _i, _p, _i64, _i, _p, _p, _i, _p]),

@@ -85,6 +85,10 @@ class LoraState:
         self.copy = torch.empty(self.numel, device=self.device, dtype=compute_dtype)
         self.copy_t = torch.empty(self.numel, device=self.device, dtype=compute_dtype)
         self.step = 0
+        # master._version at the last refresh of the compute copies (None: never refreshed)
+        self._copies_version = None
+        # (parameter, gradient view, master address) of every lora_A / lora_B tensor
+        self._bindings: list[tuple[torch.nn.Parameter, torch.Tensor, int]] = []
         self._build_transpose_jobs()
         self._build_gate_up_interleaved()
         # autograd anchor: the decoder's stream Functions take it as an input so that backward
@@ -181,10 +185,53 @@ class LoraState:
         return self.group_b(self.grad, layer, group)
 
     def refresh_copies(self) -> None:
-        """Rebuilds the compute copies from the master weights (after init/load)."""
+        """Rebuilds the compute copies from the master weights."""
         N.call("unok_cast_copy", N.dtype_code(self.compute_dtype), self.numel, self.n_a, float(self.scale),
                N.ptr(self.master), N.ptr(self.copy), N.stream())
         self.refresh_transposes()
+        self._copies_version = self.master._version
+
+    def bind_parameter(self, param: torch.nn.Parameter, grad_view: torch.Tensor) -> None:
+        """Registers a lora_A / lora_B parameter (a view of ``master``) and its gradient view."""
+        param.grad = grad_view
+        self._bindings.append((param, grad_view, param.data_ptr()))
+
+    def sync_for_forward(self) -> None:
+        """Makes the adapters consistent whatever updated them since the last forward.
+
+        * Weights: any in-place update of the parameters (torch optimizers, ``copy_``, init)
+          advances the version counter that all views of ``master`` share; the compute copies
+          are rebuilt when it moved. (Writes through ``param.data`` bypass the counter: call
+          ``refresh_copies`` after them.) A parameter whose storage was replaced is an error,
+          since the kernels read ``master``.
+        * Gradients: the kernels accumulate into the flat ``grad`` buffer. A parameter whose
+          ``.grad`` was set to None (``zero_grad(set_to_none=True)``) gets its view back, zeroed;
+          one whose ``.grad`` was replaced by another tensor has that tensor's values copied in.
+        """
+        for param, _, addr in self._bindings:
+            if param.data_ptr() != addr:
+                raise RuntimeError("A LoRA parameter no longer views the adapter storage (its .data was "
+                                   "replaced); update adapters in place instead.")
+        if self.master._version != self._copies_version:
+            self.refresh_copies()
+        unbound = [(p, g) for p, g, _ in self._bindings if p.grad is not g]
+        if not unbound:
+            return
+        if len(unbound) == len(self._bindings) and all(p.grad is None for p, _ in unbound):
+            self.grad.zero_()
+            for p, g in unbound:
+                p.grad = g
+            return
+        with torch.no_grad():
+            for p, g in unbound:
+                if p.grad is None:
+                    g.zero_()
+                else:
+                    if tuple(p.grad.shape) != tuple(g.shape):
+                        raise RuntimeError(f"gradient of shape {tuple(p.grad.shape)} set on a LoRA tensor of "
+                                           f"shape {tuple(g.shape)}")
+                    g.copy_(p.grad)
+                p.grad = g
 
     def refresh_transposes(self) -> None:
         N.call("unok_transpose_jobs", N.dtype_code(self.compute_dtype), N.ptr(self._jobs), self._jobs.shape[0],

@@ -65,6 +65,14 @@ __global__ __launch_bounds__(256) void row_lse_update_kernel(const T* __restrict
   }
 }
 
+// (v, i) beats (bv, bi) under torch.argmax's order: NaN above every number, then larger values,
+// then the smaller index among equal values (first occurrence).
+__device__ __forceinline__ bool argmax_beats(float v, int64_t i, float bv, int64_t bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
 // First-index argmax merge over a chunk: best (value, index) per row.
 template <typename T>
 __global__ __launch_bounds__(256) void row_argmax_update_kernel(const T* __restrict__ z, int64_t ldz, int Vc, int c0,
@@ -74,10 +82,10 @@ __global__ __launch_bounds__(256) void row_argmax_update_kernel(const T* __restr
   const int row = blockIdx.x;
   const T* zr = z + (int64_t)row * ldz;
   float bv = -INFINITY;
-  int bi = INT_MAX;
+  int bi = INT_MAX;                      // INT_MAX: this thread has seen no element
   for (int j = threadIdx.x; j < Vc; j += 256) {
     const float v = ldf(zr + j);
-    if (v > bv) { bv = v; bi = j; }   // j increases per thread: strict > keeps the first index
+    if (bi == INT_MAX || argmax_beats(v, j, bv, bi)) { bv = v; bi = j; }
   }
   sv[threadIdx.x] = bv;
   si[threadIdx.x] = bi;
@@ -86,17 +94,18 @@ __global__ __launch_bounds__(256) void row_argmax_update_kernel(const T* __restr
     if (threadIdx.x < o) {
       const float v2 = sv[threadIdx.x + o];
       const int i2 = si[threadIdx.x + o];
-      if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
+      if (i2 != INT_MAX && (si[threadIdx.x] == INT_MAX || argmax_beats(v2, i2, sv[threadIdx.x], si[threadIdx.x]))) {
         sv[threadIdx.x] = v2;
         si[threadIdx.x] = i2;
       }
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0 && si[0] != INT_MAX) {
     const float v = sv[0];
     const int64_t idx = (int64_t)si[0] + c0;
-    if (first || v > best_val[row]) { best_val[row] = v; best_idx[row] = idx; }
+    // chunks arrive in increasing column order, so an equal value of a later chunk never wins
+    if (first || argmax_beats(v, idx, best_val[row], best_idx[row])) { best_val[row] = v; best_idx[row] = idx; }
   }
 }
 

@@ -50,7 +50,9 @@ struct BdArgs {
   int64_t* noisy_ids; int64_t* clean_ids;                      // [B*L] token ids per stream row
 };
 
-// One workgroup per batch row. Segment starts/ends come from a chunked scan.
+// One workgroup per batch row. Segment starts/ends come from a chunked scan. REGION_ONLY writes
+// just the [noisy | clean] region mask (the layout step that precedes noising).
+template <bool REGION_ONLY>
 __global__ __launch_bounds__(1024) void bd_prepare_kernel(const BdArgs a) {
   __shared__ int carry_start[1024];
   __shared__ int carry_end[1024];
@@ -84,6 +86,12 @@ __global__ __launch_bounds__(1024) void bd_prepare_kernel(const BdArgs a) {
     int e = next_start;
     for (int u = t + 1; u < c1; ++u)
       if (pos[u - 1] >= pos[u]) { e = u; break; }
+    const int64_t base2 = (int64_t)b * 2 * L;
+    if (REGION_ONLY) {
+      a.region[base2 + seg_s + t] = 1;
+      a.region[base2 + e + t] = 0;
+      continue;
+    }
     const int s = seg_s, len = e - s, j = t - s, blk = j / a.bs;
     const int bstart = s + blk * a.bs;
     const int bend = min(bstart + a.bs, e);
@@ -100,7 +108,6 @@ __global__ __launch_bounds__(1024) void bd_prepare_kernel(const BdArgs a) {
     }
     a.noised[gi] = noised ? 1 : 0;
     a.tfull[gi] = tb;
-    const int64_t base2 = (int64_t)b * 2 * L;
     const int64_t nidx = base2 + s + t, cidx = base2 + e + t;
     a.concat_ids[nidx] = nid;
     a.concat_ids[cidx] = id;
@@ -166,8 +173,18 @@ UNOK_EXPORT int unok_bd_prepare(int B, int L, const int64_t* ids, const int64_t*
   BdArgs a{ids, pos, prompt, B, L, block_size, mask_id, noise_mask_mode, intra_causal, key,
            concat_ids, concat_pos, region, noised, tfull, noisy_src, clean_src, noisy_iv, clean_iv, noisy_ids,
            clean_ids};
-  hipLaunchKernelGGL(bd_prepare_kernel, dim3(B), dim3(1024), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(bd_prepare_kernel<false>, dim3(B), dim3(1024), 0, (hipStream_t)stream, a);
   return unok::check_launch("bd_prepare");
+}
+
+UNOK_EXPORT int unok_bd_region(int B, int L, const int64_t* pos, uint8_t* region, void* stream) {
+  UNOK_REQUIRE(B >= 0 && L >= 0, UNOK_EINVAL, "bd_region: negative shape");
+  if (B == 0 || L == 0) return 0;
+  UNOK_REQUIRE((int64_t)B * 2 * L < INT32_MAX, UNOK_EINVAL, "bd_region: batch too large");
+  BdArgs a{};
+  a.pos = pos; a.B = B; a.L = L; a.bs = 1; a.region = region;
+  hipLaunchKernelGGL(bd_prepare_kernel<true>, dim3(B), dim3(1024), 0, (hipStream_t)stream, a);
+  return unok::check_launch("bd_region");
 }
 
 UNOK_EXPORT int unok_bd_compact(int64_t n, const uint8_t* noised, const float* tfull, float* p_mask, int32_t* count,

@@ -15,6 +15,7 @@ large product of forward and backward is a K-contiguous MFMA GEMM. The per-proje
 """
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass, field
 
 import torch
@@ -88,6 +89,18 @@ def calculate_token_nums(position_ids: torch.Tensor) -> list[torch.Tensor]:
     return out
 
 
+def noisy_region_mask(model_position_ids: torch.Tensor) -> torch.Tensor:
+    """[B, 2L] bool: the per-segment [noisy | clean] layout of the concatenated batch (True on the
+    noisy copies), segments as in ``calculate_token_nums``; one device kernel, no host work."""
+    if model_position_ids.dim() != 2:
+        raise RuntimeError(f"model positions must be [B, L], got {tuple(model_position_ids.shape)}")
+    B, L = model_position_ids.shape
+    pos = model_position_ids.to(torch.int64).contiguous()
+    region = torch.empty((B, 2 * L), device=pos.device, dtype=torch.bool)
+    N.call("unok_bd_region", B, L, N.ptr(pos), N.ptr(region), N.stream())
+    return region
+
+
 # ------------------------------------------------------------------------------------------
 # Attention-mask object returned by prepare_for_bd_training
 # ------------------------------------------------------------------------------------------
@@ -136,7 +149,7 @@ class BlockDiffusionMask:
 
 def bd_prepare(input_ids, model_position_ids, prompt_mask, *, block_size: int, mask_token_id: int,
                noise: str = "uniform", intra_block: str = "bidirectional", seed: int = 20260813, step: int = 0,
-               device=None):
+               device=None, region: torch.Tensor | None = None):
     """Device-side block-diffusion preparation; returns (concat_ids [B,2L], concat_pos [B,2L],
     BlockDiffusionMask, noised [B,L] bool, noise level per token [B,L] fp32, p_mask [n_noised])."""
     if noise not in ("uniform", "mask"):
@@ -155,7 +168,10 @@ def bd_prepare(input_ids, model_position_ids, prompt_mask, *, block_size: int, m
     i32 = dict(device=dev, dtype=torch.int32)
     concat_ids = torch.empty((B, 2 * L), **i64)
     concat_pos = torch.empty((B, 2 * L), **i64)
-    region = torch.empty((B, 2 * L), device=dev, dtype=torch.bool)
+    if region is None:
+        region = torch.empty((B, 2 * L), device=dev, dtype=torch.bool)
+    elif tuple(region.shape) != (B, 2 * L) or region.dtype != torch.bool or not region.is_contiguous():
+        raise RuntimeError("prepare_for_bd_training: region buffer must be a contiguous [B, 2L] bool tensor")
     noised = torch.empty((B, L), device=dev, dtype=torch.bool)
     tfull = torch.empty((B, L), device=dev, dtype=torch.float32)
     noisy_src, clean_src = torch.empty(B * L, **i32), torch.empty(B * L, **i32)
@@ -203,10 +219,10 @@ class UnoRMSNorm(_Frozen):
 
 
 class _LoraWeight(nn.Module):
-    def __init__(self, view: torch.Tensor, grad_view: torch.Tensor):
+    def __init__(self, view: torch.Tensor, grad_view: torch.Tensor, state: LoraState):
         super().__init__()
         self.weight = nn.Parameter(view, requires_grad=True)
-        self.weight.grad = grad_view
+        state.bind_parameter(self.weight, grad_view)
 
 
 class UnoProjection(nn.Module):
@@ -328,12 +344,15 @@ class UnoQwen3Model(nn.Module):
             raise RuntimeError(f"input_ids shape {tuple(input_ids.shape)} does not match the mask ({B}, {2 * L}).")
         lora = self._uno_lora
         if lora is not None:
+            lora.sync_for_forward()
             gate = lora.token_mask
             if gate is None:
                 raise RuntimeError("Set the Uno LoRA token mask before the model forward.")
             if tuple(gate.shape) != (B, 2 * L):
                 raise RuntimeError("Uno LoRA mask and activation shapes differ: "
                                    f"mask={tuple(gate.shape)}, output={(B, 2 * L)}.")
+            # The layout step hands the same region tensor to the router and to the mask, so the
+            # identity test settles the usual case without a device comparison.
             if gate is not mask.region and not torch.equal(gate.to(mask.region.device), mask.region):
                 raise RuntimeError("The two-stream decoder requires the LoRA token mask to be the noisy region "
                                    "of the block-diffusion layout.")
@@ -356,7 +375,11 @@ class UnoQwen3Model(nn.Module):
             hn = Lyr.NoisyLayer.apply(hn, lora.anchor, lw, lora, li, g, sc)
         noisy_final = Lyr.FinalNorm.apply(hn, self.norm.weight, g.eps, lora.anchor)
         hidden = Lyr.ScatterStreams.apply(noisy_final, clean_final, mask.noisy_src, mask.clean_src)
-        return UnoModelOutput(hidden.view(B, 2 * L, g.H))
+        out = hidden.view(B, 2 * L, g.H)
+        # The two streams themselves, for extract_uno_regions: the same rows as out[region] and
+        # out[~region], and the gradient then reaches the decoder without a scatter and a gather.
+        out._uno_streams = (noisy_final, clean_final, mask.region)
+        return UnoModelOutput(out)
 
 
 class UnoQwen3ForCausalLM(nn.Module):
@@ -370,6 +393,8 @@ class UnoQwen3ForCausalLM(nn.Module):
         w = torch.zeros(cfg.vocab_size, cfg.hidden_size, **e)
         self.lm_head = UnoLMHead(w, torch.zeros(cfg.hidden_size, cfg.vocab_size, **e))
         self._bd_step = 0
+        self._layout = None      # (model positions, region mask) of the last prepare_uno_layout
+        self._staged = None      # prepared batch for the next forward (stage_prepared_batch)
 
     @property
     def device(self):
@@ -407,6 +432,12 @@ class UnoQwen3ForCausalLM(nn.Module):
         self.refresh_transposed()
 
     # ---- the reference's model-side call contract ---------------------------------------------
+    def remember_layout(self, model_position_ids: torch.Tensor, region: torch.Tensor) -> None:
+        """Called by prepare_uno_layout: a later prepare_for_bd_training on the same positions
+        writes its region into this tensor, so the router's mask and the attention mask are one
+        object."""
+        self._layout = (model_position_ids, region)
+
     def prepare_for_bd_training(self, input_ids, model_position_ids, prompt_mask, *, step: int | None = None):
         """Noises non-prompt tokens per block, builds the [noisy | clean] concatenation and the
         block-diffusion attention mask (call contract: training/trainer.py:198-209)."""
@@ -414,14 +445,36 @@ class UnoQwen3ForCausalLM(nn.Module):
         if step is None:
             step = self._bd_step
         self._bd_step = step + 1
+        region = None
+        if self._layout is not None and self._layout[0] is model_position_ids:
+            region = self._layout[1]
+        self._layout = None
         return bd_prepare(input_ids, model_position_ids, prompt_mask, block_size=int(cfg.block_size),
                           mask_token_id=cfg.resolved_mask_token_id, noise=cfg.noise or "uniform",
-                          intra_block=cfg.intra_block, seed=cfg.noise_seed, step=step, device=self.device)
+                          intra_block=cfg.intra_block, seed=cfg.noise_seed, step=step, device=self.device,
+                          region=region)
+
+    @contextlib.contextmanager
+    def stage_prepared_batch(self, concatenated_input_ids, concatenated_position_ids, attention_mask):
+        """Within the block, a forward of this model (through any wrapper) runs the decoder on the
+        prepared [noisy | clean] batch and returns {"hidden_states": (last_hidden_state,)}."""
+        if self._staged is not None:
+            raise RuntimeError("a prepared batch is already staged on this model")
+        self._staged = (concatenated_input_ids, concatenated_position_ids, attention_mask)
+        try:
+            yield
+        finally:
+            self._staged = None
 
     def forward(self, *args, **kwargs):
-        raise NotImplementedError(
-            "UnoQwen3ForCausalLM is driven through prepare_for_bd_training + .model (the Uno step "
-            "patches forward per call, training/modeling.py:116-147).")
+        if self._staged is None:
+            raise NotImplementedError(
+                "UnoQwen3ForCausalLM runs the Uno step only: stage a prepared block-diffusion batch "
+                "(run_prepared_uno_forward) before calling it.")
+        ids, pos, mask = self._staged
+        out = self.model(input_ids=ids, attention_mask=mask, position_ids=pos, output_attentions=False,
+                         output_hidden_states=False, return_dict=True, use_cache=False)
+        return {"hidden_states": (out.last_hidden_state,)}
 
 
 # ------------------------------------------------------------------------------------------
@@ -435,7 +488,7 @@ class LoraAdapterModel(nn.Module):
         self.model = model
 
     def forward(self, *args, **kwargs):
-        return self.model.forward(*args, **kwargs)
+        return self.model(*args, **kwargs)
 
 
 class UnoLoraModel(nn.Module):
@@ -456,9 +509,9 @@ class UnoLoraModel(nn.Module):
             for name in MODULES:
                 mod = getattr(layer.self_attn if name in ("q_proj", "k_proj", "v_proj", "o_proj") else layer.mlp, name)
                 mod.lora_A = nn.ModuleDict({"default": _LoraWeight(st.a_view(st.master, li, name),
-                                                                   st.a_view(st.grad, li, name))})
+                                                                   st.a_view(st.grad, li, name), st)})
                 mod.lora_B = nn.ModuleDict({"default": _LoraWeight(st.b_view(st.master, li, name),
-                                                                   st.b_view(st.grad, li, name))})
+                                                                   st.b_view(st.grad, li, name), st)})
                 mod.use_dora = {"default": False}
                 mod.scaling = {"default": st.scale}
                 mod.r = {"default": st.rank}
@@ -485,16 +538,29 @@ class UnoLoraModel(nn.Module):
 
     @torch.no_grad()
     def load_lora(self, tensors: dict) -> None:
-        """Loads {'model.layers.N....X_proj.lora_A.weight': tensor} (PEFT adapter names)."""
-        own = {}
-        for n, p in self.named_parameters():
-            if p.requires_grad:
-                own[n.replace("base_model.model.", "", 1).replace(".default", "")] = p
+        """Loads {'model.layers.N....X_proj.lora_A.weight': tensor} (PEFT adapter names). The set
+        must be complete: every adapter tensor exactly once, with its exact shape; a partial or
+        mismatched file raises before anything is written."""
+        def key(name: str) -> str:
+            return name.replace("base_model.model.", "", 1).replace(".default", "")
+
+        own = {key(n): p for n, p in self.named_parameters() if p.requires_grad}
+        given = {}
         for k, v in tensors.items():
-            key = k.replace("base_model.model.", "", 1).replace(".default", "")
-            if key not in own:
+            kk = key(k)
+            if kk not in own:
                 raise KeyError(f"unknown LoRA tensor {k}")
-            own[key].copy_(v.to(own[key].dtype))
+            if kk in given:
+                raise ValueError(f"LoRA tensor {kk} given twice")
+            if tuple(v.shape) != tuple(own[kk].shape):
+                raise ValueError(f"LoRA tensor {k} has shape {tuple(v.shape)}, expected {tuple(own[kk].shape)}")
+            given[kk] = v
+        missing = sorted(set(own) - set(given))
+        if missing:
+            raise ValueError(f"adapter is incomplete: {len(missing)} of {len(own)} LoRA tensors missing "
+                             f"(first: {missing[0]})")
+        for kk, v in given.items():
+            own[kk].copy_(v.to(own[kk].dtype))
         self.state.refresh_copies()
 
     def lora_tensors(self) -> dict:
@@ -504,7 +570,7 @@ class UnoLoraModel(nn.Module):
         return self.base_model.model
 
     def forward(self, *args, **kwargs):
-        return self.get_base_model().forward(*args, **kwargs)
+        return self.base_model(*args, **kwargs)
 
     def __getattr__(self, name):
         try:

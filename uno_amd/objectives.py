@@ -122,6 +122,22 @@ def teacher_argmax(lm_head, h_rows: torch.Tensor, chunk: int = DEFAULT_CE_CHUNK)
     return best_idx
 
 
+@torch.no_grad()
+def logits_argmax(z: torch.Tensor) -> torch.Tensor:
+    """First-index argmax of each row of given [R, V] logits (fp32 or bf16) on the argmax kernel."""
+    if z.dim() != 2:
+        raise RuntimeError(f"logits must be [rows, vocab], got {tuple(z.shape)}")
+    if z.shape[1] > 1 and z.stride(1) != 1:
+        z = z.contiguous()
+    R, V = z.shape
+    best_val = torch.empty(R, device=z.device, dtype=torch.float32)
+    best_idx = torch.empty(R, device=z.device, dtype=torch.int64)
+    if R:
+        N.call("unok_row_argmax_update", N.dtype_code(z.dtype), R, V, N.ptr(z), z.stride(0) if R > 1 else V, 0,
+               N.ptr(best_val), N.ptr(best_idx), 1, N.stream())
+    return best_idx
+
+
 class DistributionLoss(torch.autograd.Function):
     """kind 'tv': sum |p_s - p_t| * inv_n;  kind 'kl': sum p_s (log p_s - log p_t) * inv_n.
     Student logits are computed from h_s (differentiable), teacher logits from h_t (detached)."""

@@ -7,6 +7,7 @@ token mask it is given gates the low-rank update per row, which the fused GEMMs 
 from __future__ import annotations
 
 import json
+from collections import Counter
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Iterable
@@ -16,39 +17,40 @@ import torch
 from .config import LoraSettings
 from .constants import DEFAULT_MODEL_ID, DEFAULT_MODEL_REVISION, SUPPORTED_LORA_MODULES
 
-_SHORTHAND = {"q": "q_proj", "k": "k_proj", "v": "v_proj", "o": "o_proj"}
+# One-letter names of the attention projections, usable as a compact target string ("qkvo").
+_LETTER_TARGETS = {"q": "q_proj", "k": "k_proj", "v": "v_proj", "o": "o_proj"}
 
 
 def resolve_lora_targets(specification: str) -> tuple[str, ...]:
-    spec = specification.strip().lower()
-    if spec == "all":
-        return SUPPORTED_LORA_MODULES
-    if spec and set(spec) <= set(_SHORTHAND):
-        if len(set(spec)) != len(spec):
-            raise ValueError(f"LoRA target shorthand contains duplicates: {specification!r}.")
-        return tuple(_SHORTHAND[c] for c in spec)
-    targets = tuple(p.strip() for p in specification.split(",") if p.strip())
-    if not targets:
-        raise ValueError("LoRA targets cannot be empty.")
-    bad = sorted(set(targets) - set(SUPPORTED_LORA_MODULES))
-    if bad:
-        raise ValueError(f"Unsupported LoRA target(s): {bad}. Supported projection names are "
-                         f"{list(SUPPORTED_LORA_MODULES)}.")
-    if len(set(targets)) != len(targets):
-        raise ValueError(f"LoRA target list contains duplicates: {specification!r}.")
-    return targets
+    """Projection names from a target specification: "all", a string of attention letters
+    ("qv", "qkvo"), or a comma-separated list of projection names."""
+    text = specification.strip().lower()
+    if text == "all":
+        return tuple(SUPPORTED_LORA_MODULES)
+    if text and set(text) <= _LETTER_TARGETS.keys():
+        names = [_LETTER_TARGETS[c] for c in text]
+    else:
+        names = [part.strip() for part in specification.split(",") if part.strip()]
+        if not names:
+            raise ValueError(f"No LoRA targets in {specification!r}.")
+        unknown = [n for n in names if n not in SUPPORTED_LORA_MODULES]
+        if unknown:
+            raise ValueError(f"Unknown LoRA target(s) {unknown}; choose from {list(SUPPORTED_LORA_MODULES)}.")
+    if len(names) != len(set(names)):
+        raise ValueError(f"LoRA targets repeat in {specification!r}.")
+    return tuple(names)
 
 
 def validate_target_modules(model, targets: Iterable[str]) -> dict[str, int]:
-    targets = tuple(targets)
-    n_layers = getattr(model.config, "num_hidden_layers", None)
-    if not isinstance(n_layers, int) or n_layers <= 0:
-        raise RuntimeError("The base model must declare config.num_hidden_layers.")
-    counts = {t: sum(name.endswith(f".{t}") for name, _ in model.named_modules()) for t in targets}
-    wrong = {t: c for t, c in counts.items() if c != n_layers}
-    if wrong:
-        raise RuntimeError("Requested LoRA projections are not present exactly once per transformer layer "
-                           f"(expected {n_layers} each): {wrong}.")
+    """Every target must name exactly one module per decoder layer; returns the counts."""
+    layers = getattr(getattr(model, "config", None), "num_hidden_layers", None)
+    if type(layers) is not int or layers <= 0:
+        raise RuntimeError("The base model config must give a positive num_hidden_layers.")
+    leaf_names = Counter(name.rsplit(".", 1)[-1] for name, _ in model.named_modules() if name)
+    counts = {t: leaf_names.get(t, 0) for t in targets}
+    off = {t: c for t, c in counts.items() if c != layers}
+    if off:
+        raise RuntimeError(f"LoRA targets must occur once in each of the {layers} layers; found {off}.")
     return counts
 
 
@@ -67,35 +69,32 @@ def create_lora_model(model, settings: LoraSettings, *, init: str = "gaussian_b"
 
 
 def validate_only_lora_trainable(model) -> tuple[int, int]:
-    trainable, n_train, n_total = [], 0, 0
-    for name, p in model.named_parameters():
-        n_total += p.numel()
-        if p.requires_grad:
-            trainable.append(name)
-            n_train += p.numel()
+    """Only lora_A / lora_B tensors may train; returns (trainable, total) parameter counts."""
+    params = list(model.named_parameters())
+    trainable = [(n, p) for n, p in params if p.requires_grad]
     if not trainable:
-        raise RuntimeError("No trainable LoRA tensors were found.")
-    bad = [n for n in trainable if "lora_A" not in n and "lora_B" not in n]
-    if bad:
-        raise RuntimeError(f"Only LoRA A/B tensors may be trainable; found {bad[:5]}.")
-    return n_train, n_total
+        raise RuntimeError("The model has no trainable LoRA tensors.")
+    other = [n for n, _ in trainable if "lora_A" not in n and "lora_B" not in n]
+    if other:
+        raise RuntimeError(f"Only LoRA A/B tensors may be trainable; also trainable: {other[:5]}.")
+    return sum(p.numel() for _, p in trainable), sum(p.numel() for _, p in params)
 
 
 def make_saved_adapter_portable(adapter_dir) -> None:
+    """Points a saved adapter's metadata at the pinned Hub base model (adapter_config.json and,
+    when present, the model card's base_model line) instead of a local cache path."""
     adapter_dir = Path(adapter_dir)
     cfg_path = adapter_dir / "adapter_config.json"
     cfg = json.loads(cfg_path.read_text())
-    cfg["base_model_name_or_path"] = DEFAULT_MODEL_ID
-    cfg["revision"] = DEFAULT_MODEL_REVISION
+    cfg.update(base_model_name_or_path=DEFAULT_MODEL_ID, revision=DEFAULT_MODEL_REVISION)
     cfg_path.write_text(json.dumps(cfg, indent=2, sort_keys=True) + "\n")
-    readme = adapter_dir / "README.md"
-    if readme.is_file():
-        lines = readme.read_text().splitlines()
-        for i, line in enumerate(lines):
-            if line.startswith("base_model:"):
-                lines[i] = f"base_model: {DEFAULT_MODEL_ID}"
-                readme.write_text("\n".join(lines) + "\n")
-                break
+    card = adapter_dir / "README.md"
+    if card.is_file():
+        text = card.read_text().splitlines()
+        hit = next((i for i, line in enumerate(text) if line.startswith("base_model:")), None)
+        if hit is not None:
+            text[hit] = f"base_model: {DEFAULT_MODEL_ID}"
+            card.write_text("\n".join(text) + "\n")
 
 
 def save_adapter(lora_model, adapter_dir) -> Path:

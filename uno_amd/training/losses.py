@@ -8,7 +8,8 @@ from __future__ import annotations
 
 import torch
 
-from ..objectives import LogitsDistributionLoss, lm_head_logits
+from ..layers import GatherRows
+from ..objectives import LogitsDistributionLoss, lm_head_logits, logits_argmax
 from .constants import IGNORE_INDEX
 
 
@@ -21,20 +22,31 @@ def shift_labels_for_next_token(labels: torch.Tensor, position_ids: torch.Tensor
 
 
 def project_hidden_states(lm_head, hidden_states: torch.Tensor, masks: dict[str, torch.Tensor]):
-    """LM head applied once to the union of the masked rows, then re-selected per mask."""
-    union = torch.zeros_like(next(iter(masks.values())), dtype=torch.bool)
+    """LM head applied once to the union of the masked rows, then re-selected per mask
+    (training/losses.py:21-35); row gathers and the GEMM run on the HIP kernels."""
+    first = next(iter(masks.values()))
+    union = torch.zeros_like(first, dtype=torch.bool)
     for m in masks.values():
         union |= m
-    if not union.any():
+    hdim = hidden_states.shape[-1]
+    flat = hidden_states.reshape(-1, hdim)
+    rows = torch.nonzero(union.reshape(-1)).flatten().to(torch.int32)
+    if rows.numel() == 0:
         empty = hidden_states.new_empty((0, lm_head.weight.shape[0]))
         return {k: empty for k in masks}
-    logits = lm_head(hidden_states[union])
-    pos_in_union = union.reshape(-1).long().cumsum(0) - 1
-    return {k: logits[pos_in_union[m.reshape(-1)]] for k, m in masks.items()}
+    logits = lm_head(GatherRows.apply(flat, rows))
+    pos_in_union = (union.reshape(-1).to(torch.int32).cumsum(0) - 1).to(torch.int32)
+    out = {}
+    for k, m in masks.items():
+        sel = pos_in_union[m.reshape(-1)]
+        out[k] = GatherRows.apply(logits, sel) if sel.numel() else logits[:0]
+    return out
 
 
 def resolve_ce_targets(target_source: str, shifted_labels: torch.Tensor, ce_mask: torch.Tensor,
                        clean_teacher_logits: torch.Tensor | None) -> torch.Tensor:
+    """CE targets (training/losses.py:38-56): the shifted labels of the CE rows ("data"), or the
+    first-index argmax of the teacher's logits ("clean_argmax", the row-argmax kernel)."""
     if target_source == "data":
         return shifted_labels[ce_mask]
     if target_source != "clean_argmax":
@@ -45,7 +57,7 @@ def resolve_ce_targets(target_source: str, shifted_labels: torch.Tensor, ce_mask
     if clean_teacher_logits.size(0) != expected:
         raise RuntimeError("Teacher logits do not align with noised CE positions: "
                            f"{clean_teacher_logits.size(0)} rows for {expected} positions.")
-    return clean_teacher_logits.detach().argmax(dim=-1)
+    return logits_argmax(clean_teacher_logits.detach())
 
 
 def _inv_n(t: torch.Tensor, num_tokens: int) -> torch.Tensor:

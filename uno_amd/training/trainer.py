@@ -1,114 +1,194 @@
-"""Uno training step (counterpart of training/trainer.py in the reference).
+"""Uno training step as an HF Trainer (counterpart of training/trainer.py in the reference).
 
-``UnoTrainer.compute_loss(model, inputs, return_outputs=False, num_items_in_batch=None)`` keeps
-the reference's call surface and control flow (trainer.py:174-308): curriculum block size ->
-layout -> noising/concatenation -> gated forward -> region split -> objectives -> combine ->
-log. Underneath, the decoder runs the two-stream HIP path and the objectives are the fused
-LM-head kernels (CE never materialises [rows x vocab] logits). The trainer is standalone: the
-HF Trainer loop around compute_loss (backward, clip, AdamW, LR schedule) is provided by
-``training_step`` / ``optimizer_step`` with the reference's optimizer settings.
+``UnoTrainer(*, objective, curriculum, **trainer_kwargs)`` takes the reference's constructor
+(training/trainer.py:152-168, called as in training/train.py:307-315) and is a
+``transformers.Trainer``: ``train()``, callbacks, LR scheduling, clipping and checkpointing are
+HF's. What it changes is underneath ``compute_loss`` (same signature and control flow,
+training/trainer.py:174-308): the decoder runs the two-stream HIP path, and the objectives are the
+fused LM-head kernels. Its default optimizer is ``FusedLoraAdamW`` (torch AdamW semantics over the
+adapter's flat buffers); any torch optimizer over ``model.parameters()`` works too, since the
+adapters follow their fp32 parameters whatever updates them.
+
+``train_step(inputs)`` runs one optimizer step outside HF's loop (loss, backward, global-norm clip,
+AdamW, LR schedule): the unit the benchmark times.
 """
 from __future__ import annotations
 
 import json
+import os
+import tempfile
+import warnings
 from dataclasses import dataclass, field
 from pathlib import Path
 
 import torch
+from transformers import Trainer, TrainerCallback, TrainingArguments
 
 from ..layers import GatherRows
 from ..objectives import distribution_loss, fused_weighted_ce, teacher_argmax
 from ..optim import FusedLoraAdamW
 from .config import UnoObjectiveConfig
-from .constants import IGNORE_INDEX
+from .constants import DEFAULT_LEARNING_RATE, IGNORE_INDEX
 from .curriculum import BlockCurriculumPlan, set_model_block_size
 from .lora import TokenwiseLoraRouter, load_adapter, make_saved_adapter_portable, save_adapter
 from .losses import shift_labels_for_next_token
 from .modeling import (extract_uno_regions, prepare_uno_layout, run_prepared_uno_forward, unwrap_base_model,
                        validate_uno_model)
 
-
-# AdamW moments of a curriculum-boundary checkpoint (flat fp32 buffers, safetensors).
+# AdamW moments of a curriculum-boundary checkpoint written by save_checkpoint (flat fp32 buffers).
 OPTIMIZER_STATE = "uno_optimizer_state.safetensors"
+CURRICULUM_STATE = "uno_curriculum_state.json"
 
 
 def combine_objective_losses(ce_loss, kl_loss, tv_loss, objective: UnoObjectiveConfig):
-    """alpha * CE + beta * KL + gamma * TV."""
+    """alpha * CE + beta * KL + gamma * TV (training/trainer.py:34-46)."""
     objective.validate()
     return objective.ce_weight * ce_loss + objective.kl_weight * kl_loss + objective.tv_weight * tv_loss
 
 
+def sync_scheduler_param_groups(lr_scheduler) -> None:
+    """Re-aligns an LR scheduler with its optimizer's parameter groups when something (DeepSpeed
+    consolidation in the reference, training/trainer.py:49-79) changed their number after the
+    scheduler was built. Only a scheduler whose groups all share one base LR can be re-aligned."""
+    opt = getattr(lr_scheduler, "optimizer", None)
+    groups = getattr(opt, "param_groups", None)
+    base = getattr(lr_scheduler, "base_lrs", None)
+    if groups is None or base is None:
+        return
+    n = len(groups)
+    lambdas = getattr(lr_scheduler, "lr_lambdas", None)
+    if len(base) == n and (lambdas is None or len(lambdas) == n):
+        return
+    if len(set(map(float, base))) > 1:
+        raise RuntimeError(f"Optimizer groups changed, and the scheduler's base LRs differ ({base}); "
+                           "cannot re-align them.")
+    lr_scheduler.base_lrs = [g.get("initial_lr", g.get("lr", 0.0)) for g in groups]
+    if lambdas is not None:
+        if not lambdas:
+            raise RuntimeError("The scheduler has no LR lambda to extend.")
+        lr_scheduler.lr_lambdas = (list(lambdas) + [lambdas[-1]] * n)[:n]
+    if hasattr(lr_scheduler, "_last_lr"):
+        lr_scheduler._last_lr = [g["lr"] for g in groups]
+
+
+def _write_json(path: Path, payload: dict) -> None:
+    tmp = path.with_name(path.name + ".tmp")
+    tmp.write_text(json.dumps(payload, indent=2, sort_keys=True) + "\n")
+    tmp.replace(path)
+
+
+class SchedulerSyncCallback(TrainerCallback):
+    """Re-aligns the scheduler before every step (training/trainer.py:82-86)."""
+
+    def on_step_begin(self, args, state, control, **kwargs):
+        sync_scheduler_param_groups(kwargs.get("lr_scheduler"))
+        return control
+
+
+class CurriculumCheckpointCallback(TrainerCallback):
+    """Sets each step's block size and saves at every stage boundary (training/trainer.py:89-128)."""
+
+    def __init__(self, curriculum: BlockCurriculumPlan) -> None:
+        self.curriculum = curriculum
+
+    def on_step_begin(self, args, state, control, **kwargs):
+        if state.global_step < self.curriculum.max_steps:
+            set_model_block_size(kwargs["model"], self.curriculum.stage_for_step(state.global_step).block_size)
+        return control
+
+    def on_step_end(self, args, state, control, **kwargs):
+        if state.global_step in self.curriculum.checkpoint_reasons:
+            control.should_save = True
+        return control
+
+    def on_save(self, args, state, control, **kwargs):
+        if not state.is_world_process_zero:
+            return control
+        ckpt = Path(args.output_dir) / f"checkpoint-{state.global_step}"
+        make_saved_adapter_portable(ckpt)
+        reason = self.curriculum.checkpoint_reasons.get(state.global_step)
+        if reason:
+            _write_json(ckpt / CURRICULUM_STATE, {"version": 1, "global_step": state.global_step, "reason": reason,
+                                                  "curriculum_sha256": self.curriculum.sha256()})
+        return control
+
+
 def validate_curriculum_resume(checkpoint, curriculum: BlockCurriculumPlan) -> None:
-    state_path = Path(checkpoint) / "uno_curriculum_state.json"
-    if not state_path.is_file():
-        raise FileNotFoundError("Uno resumes are supported only from curriculum-boundary checkpoints; "
-                                f"missing {state_path}.")
-    state = json.loads(state_path.read_text())
+    """A resume must start from a boundary checkpoint of this very curriculum."""
+    path = Path(checkpoint) / CURRICULUM_STATE
+    if not path.is_file():
+        raise FileNotFoundError(f"Uno resumes only from curriculum-boundary checkpoints; {path} is missing.")
+    state = json.loads(path.read_text())
     if state.get("curriculum_sha256") != curriculum.sha256():
-        raise ValueError("Checkpoint curriculum does not match the current curriculum.")
+        raise ValueError(f"{checkpoint} was written under a different curriculum.")
     if state.get("global_step") not in curriculum.checkpoint_reasons:
-        raise ValueError(f"Checkpoint step {state.get('global_step')} is not a curriculum boundary.")
+        raise ValueError(f"Step {state.get('global_step')} of {checkpoint} is not a curriculum boundary.")
 
 
 @dataclass
-class TrainerState:
-    global_step: int = 0
-    log_history: list = field(default_factory=list)
+class UnoTrainingArguments(TrainingArguments):
+    """TrainingArguments with the reference run's settings as defaults (training/train.py:275-305):
+    torch AdamW, weight decay 0, clip 1.0, warmup-stable schedule without decay; no reporting and
+    no periodic saving (the curriculum callback saves at stage boundaries)."""
 
-
-@dataclass
-class UnoTrainingArguments:
-    learning_rate: float = 1e-5
-    weight_decay: float = 0.0
-    adam_beta1: float = 0.9
-    adam_beta2: float = 0.999
-    adam_epsilon: float = 1e-8
-    max_grad_norm: float = 1.0
-    warmup_steps: int = 0
-    output_dir: str | None = None
+    # HF creates the output directory when the Trainer is built: default to a scratch location
+    output_dir: str | None = field(default=os.path.join(tempfile.gettempdir(), "uno_trainer_output"))
+    learning_rate: float = field(default=DEFAULT_LEARNING_RATE)
+    weight_decay: float = field(default=0.0)
+    max_grad_norm: float = field(default=1.0)
+    optim: str = field(default="adamw_torch")
+    lr_scheduler_type: str = field(default="warmup_stable_decay")
+    lr_scheduler_kwargs: dict | str | None = field(default_factory=lambda: {"num_decay_steps": 0})
+    save_strategy: str = field(default="no")
+    remove_unused_columns: bool = field(default=False)
+    dataloader_drop_last: bool = field(default=True)
+    report_to: str | list[str] | None = field(default="none")
+    disable_tqdm: bool | None = field(default=True)
 
 
 def _unwrap_wrappers(model):
-    while hasattr(model, "module"):
+    while getattr(model, "module", None) is not None:
         model = model.module
     return model
 
 
-class UnoTrainer:
+class UnoTrainer(Trainer):
     """LoRA-only, single-forward Uno trainer on the MI355X kernels."""
 
-    def __init__(self, *, model, objective: UnoObjectiveConfig, curriculum: BlockCurriculumPlan,
-                 args: UnoTrainingArguments | None = None):
+    def __init__(self, *, objective: UnoObjectiveConfig, curriculum: BlockCurriculumPlan, **kwargs) -> None:
         objective.validate()
-        self.model = model
-        self.args = args or UnoTrainingArguments()
+        if kwargs.get("args") is None:
+            kwargs["args"] = UnoTrainingArguments()
+        super().__init__(**kwargs)
+        self.model_accepts_loss_kwargs = False
         self.objective = objective
         self.curriculum = curriculum
-        self.state = TrainerState()
-        validate_uno_model(model)
-        self._lora_router = TokenwiseLoraRouter(model)
-        lora_state = _unwrap_wrappers(model).state
-        self.optimizer = FusedLoraAdamW(lora_state, lr=self.args.learning_rate,
-                                        betas=(self.args.adam_beta1, self.args.adam_beta2),
-                                        eps=self.args.adam_epsilon, weight_decay=self.args.weight_decay,
-                                        max_grad_norm=self.args.max_grad_norm)
+        validate_uno_model(self.model)
+        self._lora_router = TokenwiseLoraRouter(self.model)
+        self._step_metrics: list[dict] = []
+        self.add_callback(SchedulerSyncCallback())
+        self.add_callback(CurriculumCheckpointCallback(curriculum))
 
-    # ---- logging ----------------------------------------------------------------------------
-    def log(self, logs: dict) -> None:
-        """Keeps device scalars as tensors; they are converted when the history is read."""
-        self.state.log_history.append(logs)
+    # ---- optimizer and schedule ---------------------------------------------------------------
+    def create_optimizer(self, model=None):
+        """FusedLoraAdamW for the torch AdamW settings of the run (the Trainer clips beforehand);
+        any other choice, or an optimizer passed in, is left to the Trainer."""
+        if self.optimizer is None and self.args.optim in ("adamw_torch", "adamw_torch_fused") \
+                and self.optimizer_cls_and_kwargs is None:
+            lora = getattr(_unwrap_wrappers(model if model is not None else self.model), "state", None)
+            if lora is not None:
+                a = self.args
+                self.optimizer = FusedLoraAdamW(lora, lr=a.learning_rate, betas=(a.adam_beta1, a.adam_beta2),
+                                                eps=a.adam_epsilon, weight_decay=a.weight_decay, max_grad_norm=None)
+                return self.optimizer
+        return super().create_optimizer(model)
 
-    def logged(self) -> list[dict]:
-        return [{k: (float(v) if torch.is_tensor(v) else v) for k, v in rec.items()} for rec in self.state.log_history]
+    def create_scheduler(self, num_training_steps, optimizer=None):
+        scheduler = super().create_scheduler(num_training_steps, optimizer)
+        sync_scheduler_param_groups(scheduler)
+        return scheduler
 
     # ---- the step -----------------------------------------------------------------------------
-    def learning_rate(self, step: int) -> float:
-        """Warmup-stable schedule with zero decay steps (training/train.py:282-284)."""
-        w = self.args.warmup_steps
-        if w > 0 and step < w:
-            return self.args.learning_rate * step / w
-        return self.args.learning_rate
-
     def compute_loss(self, model, inputs, return_outputs=False, num_items_in_batch=None):
         del num_items_in_batch
         step = min(self.state.global_step, self.curriculum.max_steps - 1)
@@ -118,7 +198,7 @@ class UnoTrainer:
         labels = inputs.get("labels")
         if labels is None:
             raise RuntimeError("Uno training batches must contain labels.")
-        unwrapped = _unwrap_wrappers(model)
+        unwrapped = self.accelerator.unwrap_model(model)
         base_model = unwrap_base_model(unwrapped)
         sequence_length = inputs["input_ids"].size(-1)
         original_positions, model_positions, noisy_region_mask = prepare_uno_layout(
@@ -134,6 +214,7 @@ class UnoTrainer:
         supervised_mask = labels != IGNORE_INDEX
         valid_next_token = shifted_labels != IGNORE_INDEX
         ce_mask = noised_positions & valid_next_token
+        # one host synchronisation for both counts (the CE row count sizes the LM-head GEMM)
         token_count, ce_count = (int(x) for x in torch.stack([supervised_mask.sum(), ce_mask.sum()]).tolist())
         dev = noisy_hidden.device
         inv_n = torch.full((), 1.0 / max(token_count, 1), device=dev, dtype=torch.float32)
@@ -170,7 +251,8 @@ class UnoTrainer:
             ce_loss = zero_loss
 
         combined_loss = combine_objective_losses(ce_loss, kl_loss, tv_loss, self.objective)
-        self.log({
+        # Kept as device scalars (no host synchronisation per step); ``logged()`` converts them.
+        self._step_metrics.append({
             "train/ce_loss": ce_loss.detach(), "train/reverse_kl_loss": kl_loss.detach(),
             "train/tv_loss": tv_loss.detach(), "train/combined_loss": combined_loss.detach(),
             "train/alpha": self.objective.ce_weight, "train/beta": self.objective.kl_weight,
@@ -182,29 +264,57 @@ class UnoTrainer:
                                    "tv_loss": tv_loss}
         return combined_loss
 
-    def training_step(self, model, inputs) -> torch.Tensor:
-        """Forward + backward of one micro-batch (gradients accumulate into the flat buffer)."""
-        loss = self.compute_loss(model, inputs)
-        loss.backward()
+    def logged(self) -> list[dict]:
+        """The per-step objective metrics of compute_loss, as floats."""
+        return [{k: (float(v) if torch.is_tensor(v) else v) for k, v in rec.items()} for rec in self._step_metrics]
+
+    # ---- one optimizer step outside HF's loop ---------------------------------------------------
+    def _ensure_optimizer(self) -> None:
+        if self.optimizer is None:
+            self.create_optimizer_and_scheduler(num_training_steps=self.curriculum.max_steps)
+
+    def train_step(self, inputs) -> torch.Tensor:
+        """compute_loss + backward + global-norm clip + AdamW + LR schedule for one micro-batch."""
+        self._ensure_optimizer()
+        self.model.train()
+        loss = self.compute_loss(self.model, self._prepare_inputs(inputs))
+        self.accelerator.backward(loss)
+        self.optimizer_step()
         return loss.detach()
 
     def optimizer_step(self) -> None:
-        """Global-norm clip + AdamW over the LoRA tensors, then zero the gradients."""
-        self.optimizer.step(lr=self.learning_rate(self.state.global_step))
-        self.optimizer.zero_grad()
+        """Clip to max_grad_norm, step the optimizer and the LR schedule, zero the gradients."""
+        self._ensure_optimizer()
+        opt = self.optimizer
+        if isinstance(opt, FusedLoraAdamW):
+            opt.step(max_grad_norm=self.args.max_grad_norm)
+        else:
+            if self.args.max_grad_norm:
+                torch.nn.utils.clip_grad_norm_([p for p in self.model.parameters() if p.grad is not None],
+                                               self.args.max_grad_norm)
+            opt.step()
+        if self.lr_scheduler is not None:
+            self.lr_scheduler.step()
+        opt.zero_grad(set_to_none=True)
         self.state.global_step += 1
 
-    def train_step(self, inputs) -> torch.Tensor:
-        loss = self.training_step(self.model, inputs)
-        self.optimizer_step()
-        return loss
+    # ---- saving ---------------------------------------------------------------------------------
+    def _save(self, output_dir: str | None = None, state_dict=None) -> None:
+        """Writes the adapter in PEFT format (the frozen base is never saved) plus the Trainer's
+        own files."""
+        del state_dict
+        out = Path(output_dir if output_dir is not None else self.args.output_dir)
+        save_adapter(_unwrap_wrappers(self.model), out)
+        if self.processing_class is not None:
+            self.processing_class.save_pretrained(str(out))
+        torch.save(self.args, out / "training_args.bin")
 
     def save_checkpoint(self, output_dir) -> Path:
-        """Adapter checkpoint (PEFT format); at curriculum boundaries the complete resume state
-        too (training/trainer.py:89-128 saves full state there): the AdamW moments and update
+        """Adapter checkpoint (PEFT format); at curriculum boundaries also the complete resume
+        state (training/trainer.py:89-128 saves full state there): the AdamW moments and update
         count, the position of the model's noise stream (what the reference's RNG state restores),
-        then the curriculum state file, which is written last so that its presence marks a
-        complete checkpoint."""
+        then the curriculum state file, written last so that its presence marks a complete
+        checkpoint."""
         from safetensors.torch import save_file
 
         ckpt = Path(output_dir) / f"checkpoint-{self.state.global_step}"
@@ -212,32 +322,31 @@ class UnoTrainer:
         make_saved_adapter_portable(ckpt)
         reason = self.curriculum.checkpoint_reasons.get(self.state.global_step)
         if reason:
-            st = self.optimizer.state
+            self._ensure_optimizer()
+            st = _unwrap_wrappers(self.model).state
             save_file({"exp_avg": st.exp_avg.detach().cpu(), "exp_avg_sq": st.exp_avg_sq.detach().cpu()},
                       str(ckpt / OPTIMIZER_STATE))
             base = unwrap_base_model(_unwrap_wrappers(self.model))
-            payload = {"version": 1, "global_step": self.state.global_step, "reason": reason,
-                       "curriculum_sha256": self.curriculum.sha256(), "adamw_updates": st.step,
-                       "noise_draws": int(getattr(base, "_bd_step", 0))}
-            tmp = ckpt / "uno_curriculum_state.json.tmp"
-            tmp.write_text(json.dumps(payload, indent=2, sort_keys=True) + "\n")
-            tmp.replace(ckpt / "uno_curriculum_state.json")
+            _write_json(ckpt / CURRICULUM_STATE, {
+                "version": 1, "global_step": self.state.global_step, "reason": reason,
+                "curriculum_sha256": self.curriculum.sha256(), "adamw_updates": st.step,
+                "noise_draws": int(getattr(base, "_bd_step", 0))})
         return ckpt
 
     def resume_from_checkpoint(self, checkpoint) -> None:
-        """Restores a curriculum-boundary checkpoint (validate_curriculum_resume, then adapters,
-        AdamW moments, update count, noise-stream position and global step): the next train_step
-        continues the run exactly."""
+        """Restores a save_checkpoint boundary checkpoint (adapters, AdamW moments, update count,
+        noise-stream position, global step): the next train_step continues the run exactly."""
         from safetensors.torch import load_file
 
         checkpoint = Path(checkpoint)
         validate_curriculum_resume(checkpoint, self.curriculum)
-        payload = json.loads((checkpoint / "uno_curriculum_state.json").read_text())
+        payload = json.loads((checkpoint / CURRICULUM_STATE).read_text())
         moments_path = checkpoint / OPTIMIZER_STATE
         if not moments_path.is_file() or "adamw_updates" not in payload:
             raise FileNotFoundError(f"{checkpoint} holds no optimizer state ({OPTIMIZER_STATE}).")
         moments = load_file(str(moments_path))
-        st = self.optimizer.state
+        self._ensure_optimizer()
+        st = _unwrap_wrappers(self.model).state
         for name in ("exp_avg", "exp_avg_sq"):
             if tuple(moments[name].shape) != (st.numel,):
                 raise ValueError(f"{name} in {moments_path} has {moments[name].numel()} values, expected {st.numel}.")
@@ -249,3 +358,8 @@ class UnoTrainer:
         if hasattr(base, "_bd_step"):
             base._bd_step = int(payload.get("noise_draws", payload["global_step"]))
         self.state.global_step = int(payload["global_step"])
+        if self.lr_scheduler is not None:
+            with warnings.catch_warnings():    # replaying the schedule, no optimizer step is due
+                warnings.simplefilter("ignore", UserWarning)
+                for _ in range(self.state.global_step):
+                    self.lr_scheduler.step()
