@@ -117,3 +117,30 @@ def test_resume_requires_a_boundary_checkpoint(dev, tmp_path):
     assert not (ckpt / OPTIMIZER_STATE).exists()
     with pytest.raises(FileNotFoundError, match="curriculum-boundary"):
         trainer.resume_from_checkpoint(ckpt)
+
+
+def test_incomplete_or_mismatched_adapter_is_rejected(dev, tmp_path):
+    """load_adapter refuses a partial or misshaped adapter file before writing anything."""
+    from safetensors.torch import save_file
+
+    from uno_amd.training.lora import load_adapter, save_adapter
+
+    lm, _, _ = _trainer(dev, lora_seed=1)
+    before = _weights(lm)
+    save_adapter(lm, tmp_path / "full")
+    tensors = load_file(str(tmp_path / "full" / "adapter_model.safetensors"))
+    names = sorted(tensors)
+    partial = dict(tensors)
+    del partial[names[3]]
+    (tmp_path / "partial").mkdir()
+    save_file(partial, str(tmp_path / "partial" / "adapter_model.safetensors"))
+    with pytest.raises(ValueError, match="incomplete"):
+        load_adapter(lm, tmp_path / "partial")
+    wrong = dict(tensors)
+    wrong[names[0]] = torch.zeros(wrong[names[0]].shape[0] + 1, wrong[names[0]].shape[1])
+    (tmp_path / "wrong").mkdir()
+    save_file(wrong, str(tmp_path / "wrong" / "adapter_model.safetensors"))
+    with pytest.raises(ValueError, match="shape"):
+        load_adapter(lm, tmp_path / "wrong")
+    for n, v in _weights(lm).items():
+        assert torch.equal(v, before[n]), n
