@@ -81,9 +81,19 @@ def lora_linear(x, W, A, B, gate, scale):
     return y + scale * (h @ B.T)
 
 
+def _keep(x, name):
+    return x
+
+
 def decoder(params: dict, lora: dict, cfg: Cfg, ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tensor,
-            gate: torch.Tensor | None) -> torch.Tensor:
-    """ids/pos [B,T]; mask [B,T,T] bool (query, key); gate [B,T] -> final-norm hidden [B,T,H]."""
+            gate: torch.Tensor | None, rnd=None) -> torch.Tensor:
+    """ids/pos [B,T]; mask [B,T,T] bool (query, key); gate [B,T] -> final-norm hidden [B,T,H].
+
+    ``rnd(x, point)``, when given, is applied to the activation stored at each named point (x1, qkv,
+    qk, o, resid, x2, gu, sw, final, and the LoRA weights/inner product lora_w, lora_h): a hook for
+    studying where the rounding of a bf16 implementation enters; the default leaves values as they
+    are."""
+    rnd = rnd or _keep
     Bsz, T = ids.shape
     Hq, Hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     s = cfg.lora_scale
@@ -96,33 +106,39 @@ def decoder(params: dict, lora: dict, cfg: Cfg, ids: torch.Tensor, pos: torch.Te
 
     def lin(i, name, x):
         p = module_path(i, name)
-        return lora_linear(x, params[p + ".weight"], lora.get(p + ".lora_A.weight"),
-                           lora.get(p + ".lora_B.weight"), gate, s)
+        A, B = lora.get(p + ".lora_A.weight"), lora.get(p + ".lora_B.weight")
+        if A is None or rnd is _keep:
+            return lora_linear(x, params[p + ".weight"], A, B, gate, s)
+        A, sB = rnd(A.to(x.dtype), "lora_w"), rnd(s * B.to(x.dtype), "lora_w")
+        hh = x @ A.T
+        if gate is not None:
+            hh = hh * gate.to(hh.dtype)[..., None]
+        return x @ params[p + ".weight"].T + rnd(hh, "lora_h") @ sB.T
 
     for i in range(cfg.num_hidden_layers):
         pre = f"model.layers.{i}."
-        x = rms_norm(h, params[pre + "input_layernorm.weight"], cfg.rms_norm_eps)
-        q = lin(i, "q_proj", x).view(Bsz, T, Hq, d)
-        k = lin(i, "k_proj", x).view(Bsz, T, Hkv, d)
-        v = lin(i, "v_proj", x).view(Bsz, T, Hkv, d)
+        x = rnd(rms_norm(h, params[pre + "input_layernorm.weight"], cfg.rms_norm_eps), "x1")
+        q = rnd(lin(i, "q_proj", x), "qkv").view(Bsz, T, Hq, d)
+        k = rnd(lin(i, "k_proj", x), "qkv").view(Bsz, T, Hkv, d)
+        v = rnd(lin(i, "v_proj", x), "qkv").view(Bsz, T, Hkv, d)
         if cfg.qk_norm:
             q = rms_norm(q, params[pre + "self_attn.q_norm.weight"], cfg.rms_norm_eps)
             k = rms_norm(k, params[pre + "self_attn.k_norm.weight"], cfg.rms_norm_eps)
         q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
-        q = q * cos + rotate_half(q) * sin
-        k = k * cos + rotate_half(k) * sin
+        q = rnd(q * cos + rotate_half(q) * sin, "qk")
+        k = rnd(k * cos + rotate_half(k) * sin, "qk")
         rep = Hq // Hkv
         k = k.repeat_interleave(rep, dim=1)
         v = v.repeat_interleave(rep, dim=1)
         scores = (q @ k.transpose(-1, -2)) * d ** -0.5 + bias
         # softmax in fp32 then back to the activation dtype (eager Qwen3 attention)
         attn = torch.softmax(scores.float() if scores.dtype != torch.float64 else scores, dim=-1).to(q.dtype) @ v
-        attn = attn.transpose(1, 2).reshape(Bsz, T, Hq * d)
-        h = h + lin(i, "o_proj", attn)
-        x = rms_norm(h, params[pre + "post_attention_layernorm.weight"], cfg.rms_norm_eps)
-        mlp = F.silu(lin(i, "gate_proj", x)) * lin(i, "up_proj", x)
-        h = h + lin(i, "down_proj", mlp)
-    return rms_norm(h, params["model.norm.weight"], cfg.rms_norm_eps)
+        attn = rnd(attn.transpose(1, 2).reshape(Bsz, T, Hq * d), "o")
+        h = rnd(h + lin(i, "o_proj", attn), "resid")
+        x = rnd(rms_norm(h, params[pre + "post_attention_layernorm.weight"], cfg.rms_norm_eps), "x2")
+        mlp = rnd(F.silu(rnd(lin(i, "gate_proj", x), "gu")) * rnd(lin(i, "up_proj", x), "gu"), "sw")
+        h = rnd(h + lin(i, "down_proj", mlp), "resid")
+    return rnd(rms_norm(h, params["model.norm.weight"], cfg.rms_norm_eps), "final")
 
 
 def init_params(cfg: Cfg, seed: int, std: float = 0.02, dtype=torch.float32) -> dict:

@@ -26,7 +26,7 @@ class Objective:
 
 
 def compute_loss(params, lora, cfg: Cfg, batch: dict, objective: Objective, *, block_size: int,
-                 mask_token_id: int, seed: int, step: int, noise: str = "uniform"):
+                 mask_token_id: int, seed: int, step: int, noise: str = "uniform", rnd=None):
     input_ids, labels = batch["input_ids"], batch["labels"]
     L = input_ids.shape[1]
     pos, model_pos, region = layout.prepare_uno_layout(input_ids, batch.get("position_ids"))
@@ -34,7 +34,7 @@ def compute_loss(params, lora, cfg: Cfg, batch: dict, objective: Objective, *, b
     cids, cpos, mask, noised, _, p_mask = bd.prepare_for_bd_training(
         input_ids, model_pos, labels == IGNORE_INDEX, block_size=block_size,
         mask_token_id=mask_token_id, seed=seed, step=step, noise=noise)
-    hidden = decoder(params, lora, cfg, cids, cpos, mask, region)
+    hidden = decoder(params, lora, cfg, cids, cpos, mask, region, rnd=rnd)
     noisy, clean = layout.extract_uno_regions(hidden, region, L)
     supervised = labels != IGNORE_INDEX
     valid_next = shifted != IGNORE_INDEX
