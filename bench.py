@@ -218,6 +218,10 @@ def main() -> int:
                     help="qwen3_8b is the headline; the others measure further model/batch shapes")
     ap.add_argument("--layers", type=int, default=None,
                     help="decoder layers (default: the workload's full depth)")
+    ap.add_argument("--batch", type=int, default=None,
+                    help="micro-batch rows (default: the workload's); larger batches may recompute layers")
+    ap.add_argument("--recompute", default="auto", choices=["auto", "on", "off"],
+                    help="noisy-stream activation recompute: auto = only the layers HBM cannot hold")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -235,6 +239,8 @@ def main() -> int:
 
     base_cfg, wl = WORKLOADS[args.workload]
     wl = dict(wl, warmup=args.warmup, steps_per_stage=max(1, args.steps // 4))
+    if args.batch is not None:
+        wl["batch"] = args.batch
     if args.layers is None:
         args.layers = base_cfg["num_hidden_layers"]
     cfg = dict(base_cfg, num_hidden_layers=args.layers)
@@ -247,6 +253,8 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     model, lm, trainer, batch = build_step(cfg, wl, dev)
+    from uno_amd.training.checkpointing import configure_gradient_checkpointing
+    configure_gradient_checkpointing(lm, {"auto": "auto", "on": True, "off": False}[args.recompute])
     print(f"[bench] model built: {args.layers} layers; warmup {args.warmup} steps", file=sys.stderr, flush=True)
     for i in range(args.warmup):
         trainer.train_step(batch)
@@ -311,6 +319,8 @@ def main() -> int:
     }
     if wl.get("segments"):
         out["config"]["segments"] = wl["segments"]
+    out["config"]["recompute_layers"] = sum(model.model.last_recompute_plan)
+    out["peak_hbm_gb"] = round(torch.cuda.max_memory_allocated() / 1e9, 1)
     if args.workload != "qwen3_8b":
         out["cpu_baseline"] = None            # the CPU oracle is timed on the headline workload only
     elif not args.no_cpu_baseline:

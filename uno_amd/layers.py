@@ -90,44 +90,66 @@ def clean_layer(h: torch.Tensor, lw: LayerWeights, g: Geometry, sc: StreamContex
     return h2, k, v
 
 
+def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: StreamContext, need_output: bool = True):
+    """Forward of one noisy-stream layer; returns (h2 or None, the activations its backward reads).
+    Deterministic: a second call on the same inputs reproduces every buffer bit for bit, which the
+    recompute policy relies on. ``need_output=False`` (recompute) skips the down projection's output."""
+    r = lora.rank
+    q_end, k_end = g.q, g.q + g.kv
+    x1, rstd1 = K.rmsnorm_fwd(h0, lw.ln_in, g.eps)
+    h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv"))
+    qkv = K.gemm_nt(x1, lw.w_qkv, a2=h_qkv, b2=lora.sb_c(li, "qkv"),
+                    segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)])
+    q, k, rstd_qk = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
+    v = qkv[:, k_end:]
+    o, lse = K.attn_fwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, g.nq, g.nk, g.d, k2=k, v2=v)
+    h_o = K.gemm_nt(o, lora.a_c(li, "o"))
+    h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o"), residual=h0)
+    x2, rstd2 = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
+    h_gu = K.gemm_nt(x2, lora.a_c(li, "gu"))
+    sb_gu_i = lora.sb_gu_i(li) if lw.w_gu_i is not None and x2.dtype == torch.bfloat16 else None
+    if sb_gu_i is not None and (2 * r) % 64 == 0 and K.swiglu_fused_ok(x2.shape[0], g.F, x2.shape[1]):
+        # gate/up product with its LoRA terms, SwiGLU in the epilogue; [gate | up] kept for backward
+        gu = torch.empty((x2.shape[0], 2 * g.F), device=x2.device, dtype=x2.dtype)
+        s = K.gemm_nt_swiglu(x2, lw.w_gu_i, a2=h_gu, b2_interleaved=sb_gu_i, gu=gu)
+    else:
+        gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu"), segments=[(g.F, 0), (2 * g.F, r)])
+        s = K.swiglu_fwd(gu, g.F)
+    h_d = K.gemm_nt(s, lora.a_c(li, "d"))
+    h2 = K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d"), residual=h1) if need_output else None
+    return h2, (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d)
+
+
+def saved_bytes_per_row(g: Geometry, rank: int, elem: int) -> int:
+    """Bytes of activations one noisy-stream layer keeps per token row for its backward."""
+    stored = 4 * g.H + (g.q + 2 * g.kv) + g.q + g.kv + g.q + 3 * g.F + 7 * rank
+    return stored * elem + 4 * (2 + g.nq + g.nk + g.nq)
+
+
 class NoisyLayer(torch.autograd.Function):
-    """One noisy-stream decoder layer with fused gated LoRA (forward and backward)."""
+    """One noisy-stream decoder layer with fused gated LoRA (forward and backward). With
+    ``recompute`` the layer keeps only its input and reruns its forward in the backward."""
 
     @staticmethod
-    def forward(ctx, h0, anchor, lw: LayerWeights, lora, li: int, g: Geometry, sc: StreamContext):
+    def forward(ctx, h0, anchor, lw: LayerWeights, lora, li: int, g: Geometry, sc: StreamContext,
+                recompute: bool = False):
         del anchor
-        r = lora.rank
-        q_end, k_end = g.q, g.q + g.kv
-        x1, rstd1 = K.rmsnorm_fwd(h0, lw.ln_in, g.eps)
-        h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv"))
-        qkv = K.gemm_nt(x1, lw.w_qkv, a2=h_qkv, b2=lora.sb_c(li, "qkv"),
-                        segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)])
-        q, k, rstd_qk = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
-        v = qkv[:, k_end:]
-        o, lse = K.attn_fwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, g.nq, g.nk, g.d, k2=k, v2=v)
-        h_o = K.gemm_nt(o, lora.a_c(li, "o"))
-        h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o"), residual=h0)
-        x2, rstd2 = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
-        h_gu = K.gemm_nt(x2, lora.a_c(li, "gu"))
-        sb_gu_i = lora.sb_gu_i(li) if lw.w_gu_i is not None and x2.dtype == torch.bfloat16 else None
-        if sb_gu_i is not None and (2 * r) % 64 == 0 and K.swiglu_fused_ok(x2.shape[0], g.F, x2.shape[1]):
-            # gate/up product with its LoRA terms, SwiGLU in the epilogue; [gate | up] kept for backward
-            gu = torch.empty((x2.shape[0], 2 * g.F), device=x2.device, dtype=x2.dtype)
-            s = K.gemm_nt_swiglu(x2, lw.w_gu_i, a2=h_gu, b2_interleaved=sb_gu_i, gu=gu)
-        else:
-            gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu"), segments=[(g.F, 0), (2 * g.F, r)])
-            s = K.swiglu_fwd(gu, g.F)
-        h_d = K.gemm_nt(s, lora.a_c(li, "d"))
-        h2 = K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d"), residual=h1)
+        h2, bufs = noisy_layer_forward(h0, lw, lora, li, g, sc)
         ctx.lw, ctx.lora, ctx.li, ctx.g, ctx.sc = lw, lora, li, g, sc
-        ctx.bufs = (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d)
+        if recompute:
+            ctx.bufs, ctx.h0 = None, h0
+        else:
+            ctx.bufs, ctx.h0 = bufs, None
         return h2
 
     @staticmethod
     def backward(ctx, dh2):
         lw, lora, li, g, sc = ctx.lw, ctx.lora, ctx.li, ctx.g, ctx.sc
-        (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d) = ctx.bufs
-        ctx.bufs = None
+        bufs = ctx.bufs
+        if bufs is None:
+            _, bufs = noisy_layer_forward(ctx.h0, lw, lora, li, g, sc, need_output=False)
+        (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d) = bufs
+        ctx.bufs = ctx.h0 = bufs = None
         dh2 = dh2.contiguous()
         M = dh2.shape[0]
         r, sc_l = lora.rank, lora.scale
@@ -181,7 +203,7 @@ class NoisyLayer(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx1 = K.gemm_nt(dqkv, lw.w_qkv_t, a2=g_qkv, b2=lora.a_t(li, "qkv"))
             dh0 = K.rmsnorm_bwd(dx1, h0, lw.ln_in, rstd1, dres=dh1)
-        return dh0, None, None, None, None, None, None
+        return dh0, None, None, None, None, None, None, None
 
 
 class FinalNorm(torch.autograd.Function):

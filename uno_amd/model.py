@@ -332,6 +332,51 @@ class UnoQwen3Model(nn.Module):
         inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))
         self.register_buffer("inv_freq", inv.to(device), persistent=False)
         self._uno_lora: LoraState | None = None
+        # Activation recompute of the noisy stream: False (keep every layer's activations), True
+        # (every layer reruns its forward in the backward), or "auto" (the fewest layers that make
+        # the kept activations fit the HBM budget).
+        self.recompute = "auto"
+        self.recompute_budget_bytes: int | None = None   # "auto": None = free HBM minus a reserve
+        self.recompute_reserve_bytes = 24 << 30
+        self.last_recompute_plan: list[bool] = []
+        self._auto_plan = None      # (shape/budget key, plan) of the last "auto" decision
+
+    def recompute_plan(self, rows: int, rank: int, elem: int) -> list[bool]:
+        """Which noisy-stream layers keep only their input for the backward (recompute) this step.
+        "auto" keeps as many layers' activations as the budget allows and recomputes the rest,
+        spread evenly over the depth."""
+        n = len(self.layers)
+        if self.recompute is True:
+            plan = [True] * n
+        elif not self.recompute:
+            plan = [False] * n
+        elif self.recompute == "auto":
+            key = (rows, rank, elem, self.recompute_budget_bytes, self.recompute_reserve_bytes)
+            if self._auto_plan is not None and self._auto_plan[0] == key:
+                self.last_recompute_plan = list(self._auto_plan[1])
+                return self.last_recompute_plan
+            per_layer = Lyr.saved_bytes_per_row(self.geo, rank, elem) * rows
+            input_only = self.geo.H * elem * rows
+            budget = self.recompute_budget_bytes
+            if budget is None:
+                # free HBM plus what torch's allocator holds unused (the previous step's activations)
+                dev = self.embed_tokens.weight.device
+                free, _ = torch.cuda.mem_get_info(dev)
+                cached = torch.cuda.memory_reserved(dev) - torch.cuda.memory_allocated(dev)
+                budget = free + cached - self.recompute_reserve_bytes
+            if budget >= n * per_layer:
+                keep = n
+            else:
+                keep = max(0, min(n, int((budget - n * input_only) // max(per_layer - input_only, 1))))
+            plan = [False] * n
+            drop = n - keep
+            for i in range(drop):                 # recompute `drop` layers spread over the depth
+                plan[(i * n) // drop] = True
+            self._auto_plan = (key, list(plan))
+        else:
+            raise ValueError(f"recompute must be True, False or 'auto', got {self.recompute!r}")
+        self.last_recompute_plan = plan
+        return plan
 
     def forward(self, input_ids=None, attention_mask=None, position_ids=None, output_attentions=False,
                 output_hidden_states=False, return_dict=True, use_cache=False, **kwargs):
@@ -371,8 +416,9 @@ class UnoQwen3Model(nn.Module):
         hn = K.embedding(mask.noisy_ids, emb)
         if lora is None:
             raise RuntimeError("The Uno decoder needs a LoRA adapter attached (create_lora_model).")
+        plan = self.recompute_plan(hn.shape[0], lora.rank, hn.element_size())
         for li, lw in enumerate(lws):
-            hn = Lyr.NoisyLayer.apply(hn, lora.anchor, lw, lora, li, g, sc)
+            hn = Lyr.NoisyLayer.apply(hn, lora.anchor, lw, lora, li, g, sc, plan[li])
         noisy_final = Lyr.FinalNorm.apply(hn, self.norm.weight, g.eps, lora.anchor)
         hidden = Lyr.ScatterStreams.apply(noisy_final, clean_final, mask.noisy_src, mask.clean_src)
         out = hidden.view(B, 2 * L, g.H)
