@@ -283,16 +283,23 @@ class _Head:
         self.weight_t = w.t().contiguous()
 
 
-@pytest.mark.parametrize("keep", [True, False], ids=["kept_logits", "recomputed_logits"])
+@pytest.mark.parametrize("path", ["gemm_epilogue", "chunk_buffer"])
 @pytest.mark.parametrize("dtype,R,H,V,chunk", [(torch.float32, 50, 64, 5000, 2048),
                                                (torch.float32, 50, 64, 5003, 2048),
                                                (torch.bfloat16, 300, 256, 8192, 3000),
-                                               (torch.bfloat16, 1000, 512, 151936, 16384)])
-def test_chunked_weighted_ce(dev, dtype, R, H, V, chunk, keep, monkeypatch):
+                                               (torch.bfloat16, 300, 256, 8200, 4096),
+                                               (torch.bfloat16, 1000, 512, 151936, 16384),
+                                               (torch.bfloat16, 777, 4096, 151936, 32768)])
+def test_chunked_weighted_ce(dev, dtype, R, H, V, chunk, path, monkeypatch):
+    """Weighted CE against fp32 torch: bf16 through the LM-head GEMM epilogues (softmax statistics
+    forward, recomputed-logit gradient backward; no [rows x vocab] buffer) and through the chunk
+    buffer with the row kernels (fp32 mode, and bf16 forced onto it)."""
     from uno_amd import objectives
     from uno_amd.objectives import fused_weighted_ce, teacher_argmax
-    # both backward paths: logits kept from the forward, or recomputed chunk by chunk
-    monkeypatch.setattr(objectives, "CE_KEEP_LOGITS_BYTES", (16 << 30) if keep else 0)
+    if path == "chunk_buffer":
+        monkeypatch.setattr(objectives, "_fused_ce_ok", lambda h, w: False)
+    elif dtype == torch.float32:
+        pytest.skip("the GEMM-epilogue path is bf16 only")
     torch.manual_seed(5)
     h = (torch.randn(R, H, device=dev) * 0.5).to(dtype)
     w = (torch.randn(V, H, device=dev) * 0.05).to(dtype)

@@ -36,6 +36,16 @@ struct GemmNT {
   int seg_end[4];
   int seg_col[4];
   float alpha;
+  // LM-head loss epilogues (EPI 3: softmax statistics, EPI 4: cross-entropy gradient) of logits
+  // Z = A B^T whose column n is vocabulary entry ce_vocab0 + n.
+  const int64_t* ce_tgt;           // [M] target vocabulary ids
+  int ce_vocab0;
+  float* ce_pmax; float* ce_psum;  // EPI 3: [M, ld ce_ldp] per 128-column block max / sum exp(z - max)
+  int64_t ce_ldp;
+  float* ce_zt;                    // EPI 3: [M] target logit (rows whose target lies in this product)
+  const float* ce_lse;             // EPI 4: [M] log-sum-exp over the whole vocabulary
+  const float* ce_w;               // EPI 4: [M] row weights; scaled by *ce_g * *ce_inv_n
+  const float* ce_g; const float* ce_inv_n;
 };
 
 template <typename T> __device__ __forceinline__ float ld_f(const T* p);
@@ -1039,6 +1049,80 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     }
     return;
   }
+  if constexpr (EPI == 3) {
+    // Softmax statistics of LM-head logits that are never stored: per row and 128-column block of
+    // this wave, the max and the sum of exp(z - max) over the block's columns below N (the four
+    // lanes of a row, lk = 0..3, hold 32 columns each and are merged through cross-lane shuffles),
+    // and the target logit of the rows whose target lies in the block.
+    const int cb = n0 + wn * 128;
+    const int part = cb >> 7;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm * 128 + i * 16 + lr;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (cb + j * 16 + lk * 4 + q < p.N) mx = fmaxf(mx, acc[i][j][q]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      float se = 0.f;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (cb + j * 16 + lk * 4 + q < p.N) se += expf(acc[i][j][q] - mx);
+      se += __shfl_xor(se, 16);
+      se += __shfl_xor(se, 32);
+      if (row < p.M && cb < p.N) {
+        if (lk == 0) {
+          p.ce_pmax[(int64_t)row * p.ce_ldp + part] = mx;
+          p.ce_psum[(int64_t)row * p.ce_ldp + part] = se;
+        }
+        const int64_t t = p.ce_tgt[row] - p.ce_vocab0 - cb;      // target column inside the block
+        if (t >= 0 && t < 128 && cb + t < p.N && ((t >> 2) & 3) == lk) {
+          float zt = 0.f;
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (j * 16 + q == (int)(t & ~12)) zt = acc[i][j][q];
+          p.ce_zt[row] = zt;
+        }
+      }
+    }
+    return;
+  }
+  if constexpr (EPI == 4) {
+    // Cross-entropy gradient of the recomputed logits: dz = bf16(w g inv_n (exp(z - lse) - onehot)),
+    // the same arithmetic as the separate gradient kernel over stored logits.
+    const float gs = p.ce_g[0] * p.ce_inv_n[0];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm * 128 + i * 16 + lr;
+      if (row >= p.M) continue;
+      const float lse = p.ce_lse[row], cf = p.ce_w[row] * gs;
+      const int64_t t = p.ce_tgt[row] - p.ce_vocab0;
+      bf16_t* crow = (bf16_t*)p.C + (int64_t)row * p.ldc;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * 128 + j * 16 + lk * 4;
+        if (col >= p.N) continue;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = cf * (expf(acc[i][j][q] - lse) - ((int64_t)(col + q) == t ? 1.f : 0.f));
+        if (col + 4 <= p.N) {
+          store4(crow + col, nullptr, v);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (col + q < p.N) crow[col + q] = f32_to_bf16(v[q]);
+        }
+      }
+    }
+    return;
+  }
   if constexpr (EPI == 1) {
     // Gate/up product with 64-row interleaved weights (rows 128 b + [0, 64) = gate features
     // 64 b + [0, 64), rows 128 b + [64, 128) = the same up features): the wave's 128 columns are
@@ -1222,6 +1306,56 @@ UNOK_EXPORT int unok_gemm_nt_swiglu_bwd(int M, int F, int K, const void* A, int6
   UNOK_REQUIRE(buffer_ranges_ok(p), UNOK_EINVAL, "gemm_nt_swiglu_bwd: operands exceed 32-bit buffer offsets");
   launch_nt_w4m16<bf16_t, 2>(p, (hipStream_t)stream);
   return unok::check_launch("gemm_nt_swiglu_bwd");
+}
+
+// Operand checks of the LM-head loss products (H[R,K] W[V,K]^T through the 256x256 kernel, which
+// addresses its operands with 32-bit buffer offsets).
+static int ce_operands_ok(const char* what, int R, int V, int K, const void* H, int64_t ldh, const void* W,
+                          int64_t ldw) {
+  UNOK_REQUIRE(R >= 0 && V > 0 && K > 0, UNOK_EINVAL, "%s: bad size R=%d V=%d K=%d", what, R, V, K);
+  UNOK_REQUIRE(K % 64 == 0 && ldh % 8 == 0 && ldw % 8 == 0 && aligned16(H) && aligned16(W), UNOK_EALIGN,
+               "%s: K=%d must be a multiple of 64, row strides multiples of 8, rows 16-byte aligned", what, K);
+  UNOK_REQUIRE(((int64_t)(R - 1) * ldh + K) * 2 <= 0xFFFFFFFFll && ((int64_t)(V - 1) * ldw + K) * 2 <= 0xFFFFFFFFll,
+               UNOK_EINVAL, "%s: operands exceed 32-bit buffer offsets", what);
+  return 0;
+}
+
+// Softmax statistics of the LM-head logits Z = H W^T (bf16 in, fp32 accumulate) without storing
+// them: pmax/psum[r, b] over columns [128 b, 128 b + 128) of Z, zt[r] = Z[r, tgt[r] - vocab0] for
+// targets inside [vocab0, vocab0 + V).
+UNOK_EXPORT int unok_lmhead_ce_stats(int R, int V, int K, const void* H, int64_t ldh, const void* W, int64_t ldw,
+                                     const int64_t* tgt, int vocab0, float* pmax, float* psum, int64_t ldp,
+                                     float* zt, void* stream) {
+  if (R == 0) return 0;
+  int rc = ce_operands_ok("lmhead_ce_stats", R, V, K, H, ldh, W, ldw);
+  if (rc) return rc;
+  UNOK_REQUIRE(ldp >= (V + 127) / 128, UNOK_EINVAL, "lmhead_ce_stats: ldp=%lld < %d blocks", (long long)ldp,
+               (V + 127) / 128);
+  GemmNT p{};
+  p.A = H; p.lda = ldh; p.B = W; p.ldb = ldw; p.M = R; p.N = V; p.K = K; p.alpha = 1.f; p.nseg = 1;
+  for (int i = 0; i < 4; ++i) { p.seg_end[i] = V; p.seg_col[i] = 0; }
+  p.ce_tgt = tgt; p.ce_vocab0 = vocab0; p.ce_pmax = pmax; p.ce_psum = psum; p.ce_ldp = ldp; p.ce_zt = zt;
+  launch_nt_w4m16<float, 3>(p, (hipStream_t)stream);
+  return unok::check_launch("lmhead_ce_stats");
+}
+
+// dz[r, v] = bf16(w[r] * g * inv_n * (exp(Z[r, v] - lse[r]) - [vocab0 + v == tgt[r]])) for the
+// recomputed logits Z = H W^T; Z itself is never stored.
+UNOK_EXPORT int unok_lmhead_ce_grad(int R, int V, int K, const void* H, int64_t ldh, const void* W, int64_t ldw,
+                                    const int64_t* tgt, int vocab0, const float* lse, const float* w,
+                                    const float* g, const float* inv_n, void* dz, int64_t lddz, void* stream) {
+  if (R == 0) return 0;
+  int rc = ce_operands_ok("lmhead_ce_grad", R, V, K, H, ldh, W, ldw);
+  if (rc) return rc;
+  UNOK_REQUIRE(lddz % 8 == 0 && lddz >= V && aligned16(dz), UNOK_EALIGN,
+               "lmhead_ce_grad: dz rows must be 16-byte aligned with a stride >= V, multiple of 8");
+  GemmNT p{};
+  p.A = H; p.lda = ldh; p.B = W; p.ldb = ldw; p.C = dz; p.ldc = lddz; p.M = R; p.N = V; p.K = K; p.alpha = 1.f;
+  p.nseg = 1;
+  for (int i = 0; i < 4; ++i) { p.seg_end[i] = V; p.seg_col[i] = 0; }
+  p.ce_tgt = tgt; p.ce_vocab0 = vocab0; p.ce_lse = lse; p.ce_w = w; p.ce_g = g; p.ce_inv_n = inv_n;
+  launch_nt_w4m16<bf16_t, 4>(p, (hipStream_t)stream);
+  return unok::check_launch("lmhead_ce_grad");
 }
 
 UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,

@@ -281,6 +281,33 @@ UNOK_EXPORT int unok_row_lse_update(int dtype, int R, int Vc, const void* z, int
   return unok::check_launch("row_lse_update");
 }
 
+// Merges the per-128-column-block softmax statistics of unok_lmhead_ce_stats into one (max,
+// sum-exp) per row; one workgroup per row, blocks merged in a fixed order.
+__global__ __launch_bounds__(256) void ce_parts_reduce_kernel(int nparts, const float* __restrict__ pmax,
+                                                              const float* __restrict__ psum, int64_t ldp,
+                                                              float* run_max, float* run_sum) {
+  __shared__ float red[32];
+  const int row = blockIdx.x;
+  const float* pm = pmax + (int64_t)row * ldp;
+  const float* ps = psum + (int64_t)row * ldp;
+  float m = -INFINITY;
+  for (int b = threadIdx.x; b < nparts; b += 256) m = fmaxf(m, pm[b]);
+  m = block_max(m, red);
+  float s = 0.f;
+  for (int b = threadIdx.x; b < nparts; b += 256) s += ps[b] > 0.f ? ps[b] * expf(pm[b] - m) : 0.f;
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) { run_max[row] = m; run_sum[row] = s; }
+}
+
+UNOK_EXPORT int unok_ce_parts_reduce(int R, int nparts, const float* pmax, const float* psum, int64_t ldp,
+                                     float* run_max, float* run_sum, void* stream) {
+  UNOK_REQUIRE(R >= 0 && nparts > 0 && ldp >= nparts, UNOK_EINVAL, "ce_parts_reduce: bad sizes");
+  if (R == 0) return 0;
+  hipLaunchKernelGGL(ce_parts_reduce_kernel, dim3(R), dim3(256), 0, (hipStream_t)stream, nparts, pmax, psum, ldp,
+                     run_max, run_sum);
+  return unok::check_launch("ce_parts_reduce");
+}
+
 UNOK_EXPORT int unok_row_argmax_update(int dtype, int R, int Vc, const void* z, int64_t ldz, int c0, float* best_val,
                                        int64_t* best_idx, int first, void* stream) {
   if (R == 0) return 0;

@@ -1,12 +1,10 @@
 """LM-head objectives of the Uno step on the HIP kernels.
 
-* ``fused_weighted_ce``: CE with the diffusion 1/t weighting (training/trainer.py:267-283),
-  evaluated over vocabulary chunks: each chunk's logits are produced by the MFMA GEMM and folded
-  into a running per-row log-sum-exp; the backward turns each chunk into dz = g w (softmax -
-  onehot) and feeds it straight into the data-gradient GEMM. When the fp32 logits of all rows fit
-  in CE_KEEP_LOGITS_BYTES (4.6 GB for the 7.6K supervised rows x 151936 vocabulary of the 4 x 4096
-  step) the vocabulary is one chunk and its logits are kept from the forward to the backward (no
-  recomputation); otherwise a chunk buffer is reused and the backward recomputes each chunk.
+* ``fused_weighted_ce``: CE with the diffusion 1/t weighting (training/trainer.py:267-283). In
+  bf16 the LM-head GEMM's epilogue reduces each 128-column block of logits to per-row softmax
+  statistics and picks the target logit, so the forward stores no logits; the backward recomputes
+  the logits one vocabulary chunk at a time in a GEMM whose epilogue emits dz = g w (softmax -
+  onehot) for the data-gradient GEMM. Only a [rows x chunk] bf16 buffer exists.
 * ``teacher_argmax``: first-index argmax of the clean-stream logits, chunked the same way
   (training/losses.py:38-56, target source "clean_argmax").
 * ``distribution_losses``: reverse KL and total variation (training/losses.py:59-183) over
@@ -19,9 +17,8 @@ import torch
 from . import _native as N
 from . import kernels as K
 
-DEFAULT_CE_CHUNK = 16384
-# Largest fp32 [rows x vocab] logits buffer kept between the CE forward and backward.
-CE_KEEP_LOGITS_BYTES = 16 << 30
+# Vocabulary columns per chunk of the CE backward (and of the fp32 / argmax chunk buffers).
+DEFAULT_CE_CHUNK = 32768
 
 
 def lm_head_logits(lm_head, x: torch.Tensor) -> torch.Tensor:
@@ -48,8 +45,22 @@ def _chunks(V: int, chunk: int):
         yield c0, min(V, c0 + chunk)
 
 
+def _fused_ce_ok(h: torch.Tensor, w_lm: torch.Tensor) -> bool:
+    """The GEMM-epilogue path: bf16, K a multiple of 64, and a vocabulary whose chunk ends keep the
+    data-gradient GEMM's 8-element K granularity."""
+    return (h.dtype == torch.bfloat16 and w_lm.dtype == torch.bfloat16 and h.shape[1] % 64 == 0
+            and w_lm.shape[0] % 8 == 0 and w_lm.stride(1) == 1)
+
+
 class ChunkedWeightedCE(torch.autograd.Function):
-    """loss = inv_n * sum_r w_r * CE(h_r W^T, y_r); inv_n is a device scalar."""
+    """loss = inv_n * sum_r w_r * CE(h_r W^T, y_r); inv_n is a device scalar.
+
+    bf16 (the step): the forward is one LM-head GEMM whose epilogue keeps only per-row softmax
+    statistics per 128 vocabulary columns and the target logit; the backward recomputes the
+    logits chunk by chunk inside a GEMM whose epilogue writes dz (bf16, one [rows x chunk]
+    buffer) and feeds it to the data-gradient GEMM. No [rows x vocab] tensor exists.
+    fp32 (parity mode) and other shapes: the logits of one vocabulary chunk at a time go through a
+    chunk buffer and the row kernels, recomputed in the backward."""
 
     @staticmethod
     def forward(ctx, h, w_lm, w_lm_t, targets, weights, inv_n, chunk):
@@ -60,39 +71,51 @@ class ChunkedWeightedCE(torch.autograd.Function):
         run_max, run_sum, zt = torch.empty(R, **f32), torch.empty(R, **f32), torch.zeros(R, **f32)
         lse = torch.empty(R, **f32)
         loss = torch.empty((), **f32)
-        keep = R * V * 4 <= CE_KEEP_LOGITS_BYTES
-        if keep:
-            chunk = V   # one GEMM over the whole vocabulary, no partial last wave of tiles per chunk
-        buf = torch.empty((R, V if keep else min(chunk, V)), **f32)
-        for i, (c0, c1) in enumerate(_chunks(V, chunk)):
-            z = buf[:, c0:c1] if keep else buf[:, :c1 - c0]
-            K.gemm_nt(h, w_lm[c0:c1], out=z)
-            N.call("unok_row_lse_update", N.F32, R, c1 - c0, N.ptr(z), buf.stride(0), c0, N.ptr(targets),
-                   N.ptr(run_max), N.ptr(run_sum), N.ptr(zt), int(i == 0), N.stream())
+        fused = _fused_ce_ok(h, w_lm)
+        if fused:
+            nparts = (V + 127) // 128
+            pmax, psum = torch.empty((R, nparts), **f32), torch.empty((R, nparts), **f32)
+            N.call("unok_lmhead_ce_stats", R, V, h.shape[1], N.ptr(h), h.stride(0), N.ptr(w_lm), w_lm.stride(0),
+                   N.ptr(targets), 0, N.ptr(pmax), N.ptr(psum), nparts, N.ptr(zt), N.stream())
+            N.call("unok_ce_parts_reduce", R, nparts, N.ptr(pmax), N.ptr(psum), nparts, N.ptr(run_max),
+                   N.ptr(run_sum), N.stream())
+            del pmax, psum
+        else:
+            buf = torch.empty((R, min(chunk, V)), **f32)
+            for i, (c0, c1) in enumerate(_chunks(V, chunk)):
+                z = buf[:, :c1 - c0]
+                K.gemm_nt(h, w_lm[c0:c1], out=z)
+                N.call("unok_row_lse_update", N.F32, R, c1 - c0, N.ptr(z), buf.stride(0), c0, N.ptr(targets),
+                       N.ptr(run_max), N.ptr(run_sum), N.ptr(zt), int(i == 0), N.stream())
+            del buf
         N.call("unok_ce_finish", R, N.ptr(run_max), N.ptr(run_sum), N.ptr(zt), N.ptr(weights), N.ptr(inv_n),
                N.ptr(lse), N.ptr(loss), N.stream())
-        ctx.save = (h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, buf if keep else None)
+        ctx.save = (h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, fused)
         return loss
 
     @staticmethod
     def backward(ctx, g):
-        h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, kept = ctx.save
+        h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, fused = ctx.save
         ctx.save = None
         R, V = h.shape[0], w_lm.shape[0]
         g = g.reshape(1).float().contiguous()
         f32 = dict(device=h.device, dtype=torch.float32)
-        buf = kept if kept is not None else torch.empty((R, min(chunk, V)), **f32)
-        dz = torch.empty((R, min(chunk, V)), device=h.device, dtype=h.dtype)
+        width = min(chunk, V)
+        dz = torch.empty((R, (width + 7) // 8 * 8), device=h.device, dtype=h.dtype)
         dh = torch.zeros(h.shape, **f32)
+        buf = None if fused else torch.empty((R, width), **f32)
         for c0, c1 in _chunks(V, chunk):
-            if kept is not None:
-                z = buf[:, c0:c1]
+            d = dz[:, :c1 - c0]
+            if fused:
+                N.call("unok_lmhead_ce_grad", R, c1 - c0, h.shape[1], N.ptr(h), h.stride(0), N.ptr(w_lm[c0:c1]),
+                       w_lm.stride(0), N.ptr(targets), c0, N.ptr(lse), N.ptr(weights), N.ptr(g), N.ptr(inv_n),
+                       N.ptr(dz), dz.stride(0), N.stream())
             else:
                 z = buf[:, :c1 - c0]
                 K.gemm_nt(h, w_lm[c0:c1], out=z)
-            d = dz[:, :c1 - c0]
-            N.call("unok_ce_grad_chunk", N.dtype_code(h.dtype), R, c1 - c0, N.ptr(z), buf.stride(0), c0, N.ptr(lse),
-                   N.ptr(targets), N.ptr(weights), N.ptr(g), N.ptr(inv_n), N.ptr(d), dz.stride(0), N.stream())
+                N.call("unok_ce_grad_chunk", N.dtype_code(h.dtype), R, c1 - c0, N.ptr(z), buf.stride(0), c0,
+                       N.ptr(lse), N.ptr(targets), N.ptr(weights), N.ptr(g), N.ptr(inv_n), N.ptr(d), dz.stride(0),
+                       N.stream())
             K.gemm_nt(d, w_lm_t[:, c0:c1], out=dh, residual=dh)
         return dh.to(h.dtype), None, None, None, None, None, None
 
