@@ -50,6 +50,20 @@ WORKLOADS = {
 }
 
 
+def objective(name: str):
+    """(UnoObjectiveConfig, description) of a benchmark objective."""
+    from uno_amd.training.config import UnoObjectiveConfig
+    table = {
+        "ce": (UnoObjectiveConfig(ce_target="ground_truth", ce_weight=1.0, kl_weight=0.0, tv_weight=0.0),
+               "CE (data targets, 1/t weights)"),
+        "tv": (UnoObjectiveConfig(ce_weight=0.0, kl_weight=0.0, tv_weight=1.0),
+               "TV against the clean-stream teacher (the released recipe)"),
+        "kl": (UnoObjectiveConfig(ce_weight=0.0, kl_weight=1.0, tv_weight=0.0),
+               "reverse KL against the clean-stream teacher"),
+    }
+    return table[name]
+
+
 WORKLOAD_NAMES = {
     "qwen3_8b": "Qwen3-8B-shape cond-LoRA block-diffusion step (36 layers, 4 x 4096 tokens, block 16, LoRA r64)",
     "dense_1b": "1B-class (16 layers, hidden 2048, 16q/8kv) cond-LoRA step, rank 32",
@@ -92,8 +106,7 @@ def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813, total_
                                               "seed": 0, "stages": stages})
     else:
         plan = BlockCurriculumPlan.fixed(wl["block_size"], total_steps, L, B)
-    trainer = UnoTrainer(model=lm, objective=UnoObjectiveConfig(ce_target="ground_truth", ce_weight=1.0,
-                                                                 kl_weight=0.0, tv_weight=0.0),
+    trainer = UnoTrainer(model=lm, objective=objective(wl.get("objective", "ce"))[0],
                          curriculum=plan, args=UnoTrainingArguments(learning_rate=1e-4))
     g = torch.Generator(device=device).manual_seed(seed + 2)
     ids = torch.randint(0, cfg.vocab_size - 1, (B, L), device=device, generator=g)
@@ -113,7 +126,7 @@ def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813, total_
     return model, lm, trainer, batch
 
 
-def algorithmic_flops(cfg: dict, wl: dict, mask, ce_rows: int, r: int) -> dict:
+def algorithmic_flops(cfg: dict, wl: dict, mask, head_rows: tuple[int, int], r: int) -> dict:
     """Algorithmically necessary FLOPs of one step from realised counts (recompute excluded):
     base linears forward on both streams + data gradient of the noisy stream, LoRA forward /
     dgrad / wgrad on noisy rows, attention over allowed pairs only (forward QK^T and PV for both
@@ -136,7 +149,8 @@ def algorithmic_flops(cfg: dict, wl: dict, mask, ce_rows: int, r: int) -> dict:
         "lora": 6 * n_lora * T,
         "attn_fwd": 4 * d * Hq * Lyr * (p_clean + p_noisy),
         "attn_bwd": (4 * d * Hq * p_noisy + 4 * d * Hq * p_intra) * Lyr,
-        "lm_head": 2 * H * V * ce_rows * 2,
+        # LM head: forward over the student rows and the teacher rows, data gradient of the student rows
+        "lm_head": 2 * H * V * (2 * head_rows[0] + head_rows[1]),
     }
     f["total"] = sum(f.values())
     return f
@@ -184,7 +198,7 @@ def cpu_baseline(threads: int) -> dict:
 
 
 TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "hbm_traffic_gemm_nt_w4m16_256_qwen3_8b_step.md")
+                               "hbm_traffic_qwen3_8b_step.md")
 
 
 def measured_traffic() -> int | None:
@@ -222,6 +236,9 @@ def main() -> int:
                     help="micro-batch rows (default: the workload's); larger batches may recompute layers")
     ap.add_argument("--recompute", default="auto", choices=["auto", "on", "off"],
                     help="noisy-stream activation recompute: auto = only the layers HBM cannot hold")
+    ap.add_argument("--objective", default="ce", choices=["ce", "kl", "tv"],
+                    help="ce: CE with data targets and 1/t weights (the headline); tv / kl: the distribution "
+                         "losses against the clean-stream teacher (tv is the released recipe's objective)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -241,6 +258,7 @@ def main() -> int:
     wl = dict(wl, warmup=args.warmup, steps_per_stage=max(1, args.steps // 4))
     if args.batch is not None:
         wl["batch"] = args.batch
+    wl["objective"] = args.objective
     if args.layers is None:
         args.layers = base_cfg["num_hidden_layers"]
     cfg = dict(base_cfg, num_hidden_layers=args.layers)
@@ -277,7 +295,11 @@ def main() -> int:
                                                                 step=10 ** 6)
         shifted = shift_labels_for_next_token(batch["labels"], pos)
         ce_rows = int((noised & (shifted != -100)).sum())
-        per_block[b] = algorithmic_flops(cfg, wl, mask, ce_rows, wl["lora_rank"])
+        supervised = int((batch["labels"] != -100).sum())
+        # (student rows, teacher rows) of the LM head: CE on the noised rows with a next token;
+        # TV / KL on every supervised row, student and teacher
+        head_rows = (ce_rows, 0) if wl.get("objective", "ce") == "ce" else (supervised, supervised)
+        per_block[b] = algorithmic_flops(cfg, wl, mask, head_rows, wl["lora_rank"])
     base._bd_step = draws
     flops = {k: sum(per_block[b][k] for b in blocks) / len(blocks) for k in per_block[blocks[0]]}
 
@@ -307,7 +329,7 @@ def main() -> int:
                    "layers": args.layers, "global_batch": wl["batch"], "seq_len": wl["seq_len"],
                    "block_size": blocks[0] if len(set(blocks)) == 1 else blocks,
                    "lora_rank": wl["lora_rank"], "lora_alpha": wl["lora_alpha"],
-                   "objective": "CE (data targets, 1/t weights)", "parallelism": "single GPU"},
+                   "objective": objective(wl.get("objective", "ce"))[1], "parallelism": "single GPU"},
         "mfu": round(mfu, 4), "algorithmic_tflop_per_step": round(flops["total"] / 1e12, 2),
         "flops_breakdown_tflop": {k: round(v / 1e12, 2) for k, v in flops.items() if k != "total"},
         "roofline": {"kernel": "gemm_nt_bf16_w4m16_kernel (256x256 tiles, 16x16x32 MFMA; fused LoRA linears, "
