@@ -9,10 +9,18 @@
 // alpha/r); transposed compute copies are produced by a batched tile-transpose.
 #include "common.h"
 
+// Partial sums of squares: 16-byte loads over the 4-aligned body (the flat buffers are
+// 256-byte aligned), scalar loads for the tail; fixed order per workgroup.
 __global__ __launch_bounds__(256) void sumsq_kernel(int64_t n, const float* __restrict__ x, float* __restrict__ part) {
   __shared__ float red[32];
   float s = 0.f;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) s += x[i] * x[i];
+  const int64_t n4 = ((uintptr_t)x & 15) == 0 ? n / 4 : 0;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+    const float4 v = ((const float4*)x)[i];
+    s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) s += x[i] * x[i];
   s = block_sum(s, red);
   if (threadIdx.x == 0) part[blockIdx.x] = s;
 }
@@ -46,17 +54,50 @@ struct AdamArgs {
   float lr, b1, b2, eps, wd, bc1, bc2_sqrt;
 };
 
+// One element's update (torch.optim.AdamW's arithmetic order); returns the new parameter.
+__device__ __forceinline__ float adamw_one(const AdamArgs& a, float coef, float step_size, float& g, float p, float& m,
+                                           float& v) {
+  g *= coef;
+  if (a.wd != 0.f) p *= 1.f - a.lr * a.wd;
+  m = m + (1.f - a.b1) * (g - m);
+  v = v * a.b2 + (1.f - a.b2) * g * g;
+  const float denom = sqrtf(v) / a.bc2_sqrt + a.eps;
+  return p - step_size * (m / denom);
+}
+
+// Four elements per thread with 16-byte loads and stores over the body (all flat buffers are
+// 256-byte aligned; the body is used only when every pointer is), one element per thread for
+// the tail. The bf16 compute copy is written 8 bytes at a time.
 __global__ __launch_bounds__(256) void adamw_kernel(const AdamArgs a) {
   const float coef = a.clip ? a.clip[1] : 1.f;
   const float step_size = a.lr / a.bc1;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256) {
-    const float g = a.g[i] * coef;
-    float p = a.p[i];
-    if (a.wd != 0.f) p *= 1.f - a.lr * a.wd;
-    const float m = a.m[i] + (1.f - a.b1) * (g - a.m[i]);
-    const float v = a.v[i] * a.b2 + (1.f - a.b2) * g * g;
-    const float denom = sqrtf(v) / a.bc2_sqrt + a.eps;
-    p -= step_size * (m / denom);
+  const bool vec = (((uintptr_t)a.p | (uintptr_t)a.g | (uintptr_t)a.m | (uintptr_t)a.v) & 15) == 0 &&
+                   ((uintptr_t)a.copy & (a.copy_f32 ? 15 : 7)) == 0 && (a.n_unscaled & 3) == 0;
+  const int64_t n4 = vec ? a.n / 4 : 0;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+    float4 g = ((const float4*)a.g)[i], p = ((const float4*)a.p)[i];
+    float4 m = ((const float4*)a.m)[i], v = ((const float4*)a.v)[i];
+    p.x = adamw_one(a, coef, step_size, g.x, p.x, m.x, v.x);
+    p.y = adamw_one(a, coef, step_size, g.y, p.y, m.y, v.y);
+    p.z = adamw_one(a, coef, step_size, g.z, p.z, m.z, v.z);
+    p.w = adamw_one(a, coef, step_size, g.w, p.w, m.w, v.w);
+    ((float4*)a.p)[i] = p;
+    ((float4*)a.m)[i] = m;
+    ((float4*)a.v)[i] = v;
+    ((float4*)a.g)[i] = g;
+    if (a.copy) {
+      const float sc = 4 * i < a.n_unscaled ? 1.f : a.copy_scale;
+      if (a.copy_f32) {
+        ((float4*)a.copy)[i] = make_float4(p.x * sc, p.y * sc, p.z * sc, p.w * sc);
+      } else {
+        ((uint2*)a.copy)[i] = make_uint2(pack2_bf16(p.x * sc, p.y * sc), pack2_bf16(p.z * sc, p.w * sc));
+      }
+    }
+  }
+  for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += stride) {
+    float g = a.g[i], m = a.m[i], v = a.v[i];
+    const float p = adamw_one(a, coef, step_size, g, a.p[i], m, v);
     a.p[i] = p;
     a.m[i] = m;
     a.v[i] = v;
