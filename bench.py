@@ -113,13 +113,20 @@ def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813, total_
     labels = ids.clone()
     batch = {"input_ids": ids, "labels": labels, "attention_mask": torch.ones_like(ids)}
     if wl.get("packed"):
+        # examples of log-normal lengths (10% prompt each) packed into the rows by the collator
+        from uno_amd.training.data import UnoPackingCollator
+
+        class _Pad:
+            pad_token_id = 0
+
         segs = packed_segments(L, seed + 3)
-        pos, start = [], 0
+        gen = torch.Generator().manual_seed(seed + 4)
+        feats = []
         for n in segs:
-            pos.append(torch.arange(n))
-            labels[:, start:start + n // 10] = -100
-            start += n
-        batch["position_ids"] = torch.cat(pos).unsqueeze(0).expand(B, -1).contiguous().to(device)
+            ex = torch.randint(0, cfg.vocab_size - 1, (n,), generator=gen).tolist()
+            feats.append({"input_ids": ex, "labels": [-100] * (n // 10) + ex[n // 10:]})
+        packed = UnoPackingCollator(_Pad(), sequence_length=L, rows=B)(feats)
+        batch = {k: v.to(device) for k, v in packed.items()}
         wl["segments"] = segs
     else:
         labels[:, :wl["prompt"]] = -100

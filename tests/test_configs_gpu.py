@@ -19,6 +19,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from oracle import layout as olay
 from oracle import step as ostep
 from oracle.model import Cfg, init_lora, init_params
 from uno_amd.model import UnoQwen3Config, UnoQwen3ForCausalLM
@@ -228,3 +229,37 @@ def test_packed_segments_tv_fp32_step(dev):
 def test_packed_segments_bf16_step_d128(dev):
     print(f"[configs] packed row {SEGMENTS}, block 32, d 128, bf16", flush=True)
     _bf16_one_step(dev, PACKED128, CE, 32, segments=SEGMENTS)
+
+
+def test_packing_collator_rows_fp32_step(dev):
+    """Rows built by the packing collator from variable-length examples (each 10% prompt): two
+    rows of several segments plus an all-padding tail segment, block 32, against the oracle on the
+    same collated batch (position_ids segments, training/modeling.py:84-98)."""
+    from uno_amd.training.data import UnoPackingCollator
+
+    class Tok:
+        pad_token_id = 0
+
+    spec = dict(PACKED, B=2)
+    g = torch.Generator().manual_seed(11)
+    feats = []
+    for n in (150, 97, 201, 64, 180, 230):
+        ids = torch.randint(1, spec["vocab_size"] - 1, (n,), generator=g).tolist()
+        feats.append({"input_ids": ids, "labels": [-100] * max(1, n // 10) + ids[max(1, n // 10):]})
+    batch = UnoPackingCollator(Tok(), sequence_length=spec["L"], rows=2)(feats)
+    print(f"[configs] collator rows, segments {[t.tolist() for t in olay.calculate_token_nums(batch['position_ids'])]}",
+          flush=True)
+    mine_obj, ref_obj = CE
+    ocfg, params, lora, lm, trainer = _setup(spec, torch.float32, dev, mine_obj, [32])
+    leaves = {k: v.clone().requires_grad_(True) for k, v in lora.items()}
+    ref_loss, _ = ostep.compute_loss(params, leaves, ocfg, batch, ref_obj, block_size=32,
+                                     mask_token_id=ocfg.vocab_size - 1, seed=SEED, step=0)
+    ref_loss.backward()
+    loss = trainer.compute_loss(lm, _to(batch, dev))
+    loss.backward()
+    torch.cuda.synchronize()
+    lrel = abs(loss.item() - ref_loss.item()) / abs(ref_loss.item())
+    mine = _my_grads(lm)
+    worst = max(((mine[k].cpu() - v.grad).norm() / v.grad.norm().clamp_min(1e-30)).item() for k, v in leaves.items())
+    print(f"   loss rel {lrel:.2e}; worst grad rel L2 {worst:.2e}", flush=True)
+    assert lrel < 1e-5 and worst < 2e-4

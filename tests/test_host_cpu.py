@@ -161,3 +161,30 @@ def test_portable_adapter_metadata(tmp_path):
     cfg = json.loads((tmp_path / "adapter_config.json").read_text())
     assert cfg["base_model_name_or_path"] == "s-sahoo/uno-qwen3-8B"
     assert "base_model: s-sahoo/uno-qwen3-8B" in (tmp_path / "README.md").read_text()
+
+
+def test_packing_collator_layout():
+    """First-fit packing: every example lands once, in order, in one row; positions restart at each
+    example; the unused tail is its own all-padding segment with IGNORE_INDEX labels."""
+    class Tok:
+        pad_token_id = 0
+    lengths = [5, 3, 7, 2]
+    feats = [{"input_ids": list(range(100 * (i + 1), 100 * (i + 1) + n)),
+              "labels": [-100] + list(range(100 * (i + 1) + 1, 100 * (i + 1) + n))} for i, n in enumerate(lengths)]
+    col = udata.UnoPackingCollator(Tok(), sequence_length=8)
+    assert col.plan(lengths) == [[0, 1], [2], [3]]
+    out = col(feats)
+    assert out["input_ids"][0].tolist() == feats[0]["input_ids"] + feats[1]["input_ids"]
+    assert out["position_ids"][0].tolist() == [0, 1, 2, 3, 4, 0, 1, 2]
+    assert out["position_ids"][1].tolist() == [0, 1, 2, 3, 4, 5, 6, 0]
+    assert out["position_ids"][2].tolist() == [0, 1, 0, 1, 2, 3, 4, 5]
+    assert out["labels"][2].tolist() == feats[3]["labels"] + [-100] * 6
+    assert out["attention_mask"][1].tolist() == [1] * 7 + [0]
+    segs = [t.tolist() for t in olay.calculate_token_nums(out["position_ids"])]
+    assert segs == [[5, 3], [7, 1], [2, 6]]
+    # fixed row count: padded with all-padding rows, an error when too small
+    assert udata.UnoPackingCollator(Tok(), sequence_length=8, rows=4)(feats)["input_ids"].shape == (4, 8)
+    with pytest.raises(ValueError):
+        udata.UnoPackingCollator(Tok(), sequence_length=8, rows=2)(feats)
+    with pytest.raises(ValueError):
+        col([{"input_ids": [1] * 9, "labels": [1] * 9}])
