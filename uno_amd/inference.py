@@ -1,0 +1,180 @@
+"""Draft forward of Uno's two-pass block decoding on the training step's kernels.
+
+The inference side of the conditional LoRA (nano_vllm_uno/engine/two_pass_decoding.py:243-283,
+draft_stage): each sequence feeds a block [seed, noise_1, ..., noise_(L-1)] through the decoder
+over its KV cache; the LoRA update is gated per row -- off on the seed, on for the noise rows
+(nano_vllm_uno/layers/linear.py:166-307, `lora_mask`) -- and attention is causal over the cache and
+the block (nano_vllm_uno/layers/attention.py:628-668, BLOCK_DECODE: the block's K/V are stored into
+the cache first, then flash attention with causal=True over the cached lengths). After the draft
+the noise K/V are discarded: only the committed rows (the seed) advance the cache.
+
+Kernels, all shared with the training step:
+* the gated LoRA is the GEMM's K-extension: h = m (.) (x A^T) by the skinny GEMM with its row gate,
+  then y = x W^T + h (s B)^T (+ residual) in the 256x256 / register-staged MFMA GEMMs;
+* the cache is head-major, [layers][B, Hkv, max_len, D] for K and V, so one (sequence, K/V head)
+  pair's keys are contiguous rows; the block's queries of that pair (L rows x the q-heads sharing
+  the K/V head, at most 128) are laid out as the 128 query rows of one attention workgroup over
+  that key range, with per-row key intervals [start, start + cached + j + 1) -- the block-diffusion
+  attention kernel then reads each cache row once per pair;
+* a prefill (empty caches) is the causal forward of the prompt with the LoRA gated off, through
+  the clean-stream attention path (keys = the prompt itself).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import kernels as K
+from .layers import Geometry
+
+
+class BlockKVCache:
+    """Per-layer K and V, head-major [B, Hkv, max_len, D], and the committed length per sequence."""
+
+    def __init__(self, geo: Geometry, layers: int, batch: int, max_len: int, device, dtype):
+        shape = (batch, geo.nk, max_len, geo.d)
+        self.k = [torch.zeros(shape, device=device, dtype=dtype) for _ in range(layers)]
+        self.v = [torch.zeros(shape, device=device, dtype=dtype) for _ in range(layers)]
+        self.lengths = torch.zeros(batch, device=device, dtype=torch.int64)
+        self.batch, self.max_len, self.geo = batch, max_len, geo
+
+
+class BlockDecoder:
+    """Runs prefill and draft blocks of a Uno model (UnoLoraModel or a base model with an
+    adapter attached) on the HIP kernels."""
+
+    def __init__(self, lm):
+        base = lm.get_base_model() if hasattr(lm, "get_base_model") else lm
+        self.base = base
+        self.decoder = base.model
+        self.lora = self.decoder._uno_lora
+        if self.lora is None:
+            raise RuntimeError("BlockDecoder needs a model with a LoRA adapter attached (create_lora_model).")
+        self.geo = self.decoder.geo
+
+    def new_cache(self, batch: int, max_len: int) -> BlockKVCache:
+        return BlockKVCache(self.geo, len(self.decoder.layers), batch, max_len, self.base.device, self.base.dtype)
+
+    # ---- public entry points ------------------------------------------------------------------
+    @torch.no_grad()
+    def prefill(self, cache: BlockKVCache, prompt_ids: torch.Tensor) -> torch.Tensor:
+        """Causal forward of [B, P] prompt tokens into empty caches (LoRA off); returns logits
+        [B, P, V] and commits all P rows."""
+        if int(cache.lengths.max()) != 0:
+            raise RuntimeError("prefill expects empty caches")
+        B, P = prompt_ids.shape
+        gate = torch.zeros((B, P), device=prompt_ids.device, dtype=torch.bool)
+        return self._forward(cache, prompt_ids, gate, commit=P, prefill=True)
+
+    @torch.no_grad()
+    def draft_block(self, cache: BlockKVCache, block_ids: torch.Tensor, lora_mask: torch.Tensor | None = None,
+                    commit: int = 1) -> torch.Tensor:
+        """One draft block [B, L] at positions cached + 0 .. L-1; returns logits [B, L, V]. The
+        LoRA gate defaults to the draft layout (off on the seed row, on for the noise rows);
+        ``commit`` rows (the seed) stay in the cache, the rest are discarded."""
+        B, L = block_ids.shape
+        if lora_mask is None:
+            lora_mask = torch.ones((B, L), device=block_ids.device, dtype=torch.bool)
+            lora_mask[:, 0] = False
+        if tuple(lora_mask.shape) != (B, L):
+            raise RuntimeError(f"LoRA row mask {tuple(lora_mask.shape)} does not match the block {(B, L)}")
+        if not 0 <= commit <= L:
+            raise ValueError(f"commit must lie in [0, {L}]")
+        return self._forward(cache, block_ids, lora_mask.to(torch.bool), commit=commit, prefill=False)
+
+    # ---- the decoder -----------------------------------------------------------------------------
+    def _forward(self, cache: BlockKVCache, ids: torch.Tensor, gate: torch.Tensor, commit: int, prefill: bool):
+        g, lora, dec = self.geo, self.lora, self.decoder
+        B, L = ids.shape
+        if B != cache.batch:
+            raise RuntimeError(f"block batch {B} does not match the cache batch {cache.batch}")
+        lengths = cache.lengths
+        if int((lengths + L).max()) > cache.max_len:
+            raise RuntimeError("the block does not fit in the KV cache")
+        rep = g.nq // g.nk
+        if not prefill and rep * L > 128:
+            raise NotImplementedError(f"draft blocks hold at most 128 / {rep} rows per sequence (got {L})")
+        dev = ids.device
+        M = B * L
+        j = torch.arange(L, device=dev)
+        pos = (lengths[:, None] + j[None, :]).reshape(-1).contiguous()            # [M] int64
+        gate_rows = gate.reshape(-1).contiguous()
+        maps = self._maps(cache, lengths, B, L, prefill)
+        h = K.embedding(ids.reshape(-1).contiguous().to(torch.int64), dec.embed_tokens.weight)
+        for li, layer in enumerate(dec.layers):
+            lw = layer.weights()
+            h = self._layer(h, lw, li, pos, gate_rows, cache, maps, B, L, prefill)
+        x, _ = K.rmsnorm_fwd(h, dec.norm.weight, g.eps)
+        logits = K.gemm_nt(x, self.base.lm_head.weight)
+        cache.lengths += commit
+        return logits.view(B, L, -1)
+
+    def _maps(self, cache, lengths, B, L, prefill):
+        """Row maps of the cache store and of the decode query layout, and the key intervals."""
+        g = self.geo
+        dev = lengths.device
+        i32 = dict(device=dev, dtype=torch.int32)
+        b = torch.arange(B, device=dev)[:, None, None]
+        t = torch.arange(L, device=dev)[None, :, None]
+        kv = torch.arange(g.nk, device=dev)[None, None, :]
+        # cache store: key row (b, t, head) of the block -> cache row (b, head, lengths_b + t)
+        store = ((b * g.nk + kv) * cache.max_len + lengths[:, None, None] + t).reshape(-1).to(**i32)
+        out = {"store": store}
+        if prefill:
+            starts = (torch.arange(B, device=dev) * L)[:, None]
+            iv = torch.zeros((B * L, 8), **i32)
+            iv[:, 0] = starts.expand(B, L).reshape(-1)
+            iv[:, 1] = (starts + torch.arange(1, L + 1, device=dev)[None, :]).reshape(-1)
+            out["iv"] = iv
+            return out
+        rep = g.nq // g.nk
+        # decode layout: query (b, t, head h = kv * rep + r) -> row (b * nk + kv) * 128 + r * L + t
+        r = torch.arange(rep, device=dev)
+        qrow = ((b * g.nk + kv)[..., None] * 128 + r[None, None, None, :] * L + t[..., None])   # [B, L, nk, rep]
+        out["qrow"] = qrow.reshape(-1).to(**i32)
+        rows = B * g.nk * 128
+        iv = torch.zeros((rows, 8), **i32)
+        slot = torch.arange(128, device=dev)
+        pair = torch.arange(B * g.nk, device=dev)
+        valid = slot < rep * L
+        tt = slot % L
+        start = pair[:, None] * cache.max_len                                           # [pairs, 1]
+        seen = lengths.repeat_interleave(g.nk)[:, None] + tt[None, :] + 1               # causal over cache + block
+        # rows past rep * L are padding: they see the pair's first key and their output is dropped
+        iv[:, 0] = start.expand(-1, 128).reshape(-1)
+        iv[:, 1] = torch.where(valid[None, :], start + seen, start + 1).reshape(-1)
+        out["iv"] = iv
+        return out
+
+    def _layer(self, h0, lw, li, pos, gate_rows, cache, maps, B, L, prefill):
+        g, lora = self.geo, self.lora
+        r = lora.rank
+        q_end, k_end = g.q, g.q + g.kv
+        M = h0.shape[0]
+        x1, _ = K.rmsnorm_fwd(h0, lw.ln_in, g.eps)
+        h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv"), gate=gate_rows)
+        qkv = K.gemm_nt(x1, lw.w_qkv, a2=h_qkv, b2=lora.sb_c(li, "qkv"),
+                        segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)])
+        q, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, pos, self.decoder.inv_freq, g.eps)
+        v = qkv[:, k_end:]
+        ck = cache.k[li].view(-1, g.d)
+        cv = cache.v[li].view(-1, g.d)
+        # the block's K/V into the cache rows (b, head, cached + t)
+        K.rows_copy(k.reshape(M * g.nk, g.d), ck, M * g.nk, dmap=maps["store"])
+        K.rows_copy(v.contiguous().view(M * g.nk, g.d), cv, M * g.nk, dmap=maps["store"])
+        if prefill:
+            o, _ = K.attn_fwd(q, k, v, maps["iv"], g.nq, g.nk, g.d)
+        else:
+            rows = maps["iv"].shape[0]
+            qd = torch.zeros((rows, g.d), device=q.device, dtype=q.dtype)
+            K.rows_copy(q.reshape(M * g.nq, g.d), qd, M * g.nq, dmap=maps["qrow"])
+            od, _ = K.attn_fwd(qd, ck, cv, maps["iv"], 1, 1, g.d)
+            o = torch.empty((M, g.q), device=q.device, dtype=q.dtype)
+            K.rows_copy(od, o.view(M * g.nq, g.d), M * g.nq, smap=maps["qrow"])
+        h_o = K.gemm_nt(o, lora.a_c(li, "o"), gate=gate_rows)
+        h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o"), residual=h0)
+        x2, _ = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
+        h_gu = K.gemm_nt(x2, lora.a_c(li, "gu"), gate=gate_rows)
+        gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu"), segments=[(g.F, 0), (2 * g.F, r)])
+        s = K.swiglu_fwd(gu, g.F)
+        h_d = K.gemm_nt(s, lora.a_c(li, "d"), gate=gate_rows)
+        return K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d"), residual=h1)
