@@ -201,7 +201,7 @@ def cpu_baseline(threads: int) -> dict:
             "sample": (f"fp32 CPU oracle, Qwen3-8B widths, 1 x {L} tokens: 1 decoder layer fwd+bwd "
                        f"({t_layer:.2f} s) and LM head + CE ({t_head:.2f} s); step extrapolated to 36 layers "
                        f"x {WORKLOAD['batch']} sequences = {t_step:.1f} s"),
-            "cpu_model": _cpu_model()}
+            **host_info()}
 
 
 TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -230,6 +230,34 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def host_info() -> dict:
+    """The CPU the baseline ran on: model, logical CPUs this process may use, physical cores
+    (distinct (package, core) pairs of /proc/cpuinfo among them) and RAM."""
+    usable = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    cores, cpu, pkg = set(), None, "0"
+    try:
+        for line in open("/proc/cpuinfo"):
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "processor":
+                cpu = int(val)
+            elif key == "physical id":
+                pkg = val
+            elif key == "core id" and cpu in usable:
+                cores.add((pkg, val))
+    except OSError:
+        pass
+    ram = None
+    try:
+        for line in open("/proc/meminfo"):
+            if line.startswith("MemTotal:"):
+                ram = round(int(line.split()[1]) / 1024 ** 2, 1)
+    except OSError:
+        pass
+    return {"cpu_model": _cpu_model(), "logical_cpus": len(usable), "physical_cores": len(cores) or None,
+            "ram_gib": ram}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -247,7 +275,8 @@ def main() -> int:
                     help="ce: CE with data targets and 1/t weights (the headline); tv / kl: the distribution "
                          "losses against the clean-stream teacher (tv is the released recipe's objective)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-threads", type=int, default=None,
+                    help="threads of the CPU baseline (default: every physical core this process may use)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run three plain 1 GiB device copies (the reference kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -356,7 +385,9 @@ def main() -> int:
         print("[bench] timing CPU baseline", file=sys.stderr, flush=True)
         del model, lm, trainer, batch
         torch.cuda.empty_cache()
-        out["cpu_baseline"] = cpu_baseline(args.cpu_threads)
+        hi = host_info()
+        threads = args.cpu_threads or hi["physical_cores"] or hi["logical_cpus"]
+        out["cpu_baseline"] = cpu_baseline(threads)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out))
