@@ -1193,6 +1193,56 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     return;
   }
   const bool interior = m0 + BM <= p.M && n0 + BN <= p.N && p.gate == nullptr;
+  if constexpr (EPI == 0 && std::is_same<OutT, bf16_t>::value) {
+    if (interior && (p.ldc & 7) == 0 && (!R || (p.ldr & 7) == 0)) {
+      // Interior tile with bf16 output: each wave stages its 128 x 128 fp32 quadrant (alpha
+      // applied) through a private 32 KB of the idle LDS stages, 64 rows at a time, and stores by
+      // rows: 16 lanes per row, 8 columns (16 bytes) each, the residual read the same way. 16-byte
+      // chunk c of staged row r sits at slot c ^ (r & 15).
+      asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed
+      float* q = (float*)smem + wid * 64 * 128;
+      const int rsub = lane >> 4, c16 = lane & 15;
+      const int64_t rowb = m0 + wm * 128 + rsub;
+      const int col = n0 + wn * 128 + 8 * c16;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int r = i * 16 + lr;
+            f32x4_t v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[4 * h + i][j][e] * p.alpha;
+            *(f32x4_t*)&q[r * 128 + (((4 * j + lk) ^ (r & 15)) << 2)] = v;
+          }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll 4
+        for (int it = 0; it < 16; ++it) {
+          const int r = it * 4 + rsub;
+          const f32x4_t v0 = *(const f32x4_t*)&q[r * 128 + (((2 * c16) ^ (r & 15)) << 2)];
+          const f32x4_t v1 = *(const f32x4_t*)&q[r * 128 + (((2 * c16 + 1) ^ (r & 15)) << 2)];
+          const int64_t row = rowb + 64 * h + it * 4;
+          float a[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          if (R) {
+            const uint4 rw = *(const uint4*)((const bf16_t*)R + row * p.ldr + col);
+            const uint32_t* rp = (const uint32_t*)&rw;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              a[2 * e] += __uint_as_float(rp[e] << 16);
+              a[2 * e + 1] += __uint_as_float(rp[e] & 0xffff0000u);
+            }
+          }
+          *(uint4*)((bf16_t*)C + row * p.ldc + col) =
+              make_uint4(pack2_bf16(a[0], a[1]), pack2_bf16(a[2], a[3]), pack2_bf16(a[4], a[5]), pack2_bf16(a[6], a[7]));
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);     // the half's reads are done before the next overwrites
+        __builtin_amdgcn_wave_barrier();
+      }
+      return;
+    }
+  }
   if (R) {
     if (interior) epilogue(std::true_type{}, std::false_type{}); else epilogue(std::true_type{}, std::true_type{});
   } else {
