@@ -1135,6 +1135,39 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     // both outputs by rows, 16 lanes per row: gate and up as 128-byte runs, C as one.
     // Interior tiles only (checked by the caller).
     const int f0 = (n0 + wn * 128) / 2;
+    if (p.C2 == nullptr && (p.ldc & 7) == 0) {
+      // Output only: each wave's 128 x 64 block goes through a private 16 KB of the idle LDS
+      // stages (16-byte chunk c of row r at slot c ^ ((r >> 1) & 7)) and is stored by rows, eight
+      // lanes per 128-byte row.
+      asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed
+      bf16_t* q = smem + wid * 128 * 64;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = i * 16 + lr;
+#pragma unroll
+        for (int j = 0; j < TN / 2; ++j) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float gv = bf16_to_f32(f32_to_bf16(acc[i][j][e] * p.alpha));
+            const float uv = bf16_to_f32(f32_to_bf16(acc[i][j + TN / 2][e] * p.alpha));
+            v[e] = bf16_to_f32(f32_to_bf16(gv * sigmoidf_(gv))) * uv;
+          }
+          *(uint2*)&q[r * 64 + (((2 * j + (lk >> 1)) ^ ((r >> 1) & 7)) << 3) + (lk & 1) * 4] =
+              make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_wave_barrier();
+      const int c8 = lane & 7, rs = lane >> 3;
+      OutT* dst = C + (int64_t)(m0 + wm * 128 + rs) * p.ldc + f0 + 8 * c8;
+#pragma unroll 4
+      for (int it = 0; it < 16; ++it) {
+        const int r = it * 8 + rs;
+        *(uint4*)(dst + (int64_t)(it * 8) * p.ldc) = *(const uint4*)&q[r * 64 + ((c8 ^ ((r >> 1) & 7)) << 3)];
+      }
+      return;
+    }
     if (p.C2 == nullptr) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
