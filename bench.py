@@ -8,9 +8,10 @@ t ~ U(0.05, 1) per block, uniform token ids, objective CE with data targets and 
 
 Prints ONE JSON line. ``value`` = training tokens/s (B*L input tokens per step, the reference's
 accounting). ``roofline`` = the dominant kernel (256x256 bf16 MFMA GEMM of the fused LoRA
-linears and the LM head): algorithmic FLOPs per launch / mean launch time, HIP events around every such launch
-in the timed region. ``cpu_baseline`` = the CPU oracle of the same step timed on this host on a
-bounded sample (see cpu_baseline()).
+linears and the LM head): algorithmic FLOPs per launch / mean launch time, from HIP events around
+every such launch in as many steps again right after the timed ones (an event delays the next
+dispatch by a few microseconds, so the timed steps carry none). ``cpu_baseline`` = the CPU oracle
+of the same step timed on this host on a bounded sample (see cpu_baseline()).
 """
 from __future__ import annotations
 
@@ -339,14 +340,20 @@ def main() -> int:
     base._bd_step = draws
     flops = {k: sum(per_block[b][k] for b in blocks) / len(blocks) for k in per_block[blocks[0]]}
 
-    rec = K.LaunchRecorder(lambda dt, M, N, Kd, K2, segs: dt == torch.bfloat16 and K.nt_uses_256_tiles(M, N, segs))
     torch.cuda.synchronize()
-    K.set_recorder(rec)
     t0 = time.perf_counter()
     for i in range(args.steps):
         trainer.train_step(batch)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    # Roofline window: as many further steps with HIP events around every 256x256 GEMM launch.
+    # A recorded event delays the next dispatch by a few microseconds, so these steps are not the
+    # ones that give the step time.
+    rec = K.LaunchRecorder(lambda dt, M, N, Kd, K2, segs: dt == torch.bfloat16 and K.nt_uses_256_tiles(M, N, segs))
+    K.set_recorder(rec)
+    for i in range(args.steps):
+        trainer.train_step(batch)
+    torch.cuda.synchronize()
     K.set_recorder(None)
     ms_step = (t1 - t0) * 1000.0 / args.steps
     ms, fl = rec.elapsed()
@@ -373,7 +380,8 @@ def main() -> int:
                      "bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic() if args.workload == "qwen3_8b" else None,
-                     "launches": len(ms), "mean_launch_ms": round(gemm_ms, 4)},
+                     "launches": len(ms), "mean_launch_ms": round(gemm_ms, 4),
+                     "window": f"{args.steps} steps after the timed ones, HIP events around each launch"},
     }
     if wl.get("segments"):
         out["config"]["segments"] = wl["segments"]
