@@ -134,9 +134,15 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return r;
 }
 
-// Logistic function of the SwiGLU gate (one definition, so the fused GEMM epilogue and the
-// stand-alone SwiGLU kernel round identically).
-__device__ __forceinline__ float sigmoidf_(float g) { return 1.f / (1.f + expf(-g)); }
+// e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32, within 1 ulp; results below the normal
+// range flush to zero). Used where x <= 0 or the result only enters a sum or a ratio: softmax
+// weights of the loss kernels and the logistic function below.
+__device__ __forceinline__ float fast_expf(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
+// Logistic function of the SwiGLU gate, 1 / (1 + e^-g) with the hardware reciprocal (within
+// 1 ulp); +-inf give 0 and 1. One definition, so the fused GEMM epilogues and the stand-alone
+// SwiGLU kernels round identically.
+__device__ __forceinline__ float sigmoidf_(float g) { return __builtin_amdgcn_rcpf(1.f + fast_expf(-g)); }
 
 // Gradients of out = bf16(silu(g)) * u for upstream d: the same expression in the SwiGLU backward
 // kernel and the fused GEMM epilogue, so both round identically.

@@ -1072,7 +1072,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (cb + j * 16 + lk * 4 + q < p.N) se += expf(acc[i][j][q] - mx);
+          if (cb + j * 16 + lk * 4 + q < p.N) se += fast_expf(acc[i][j][q] - mx);
       se += __shfl_xor(se, 16);
       se += __shfl_xor(se, 32);
       if (row < p.M && cb < p.N) {
@@ -1111,7 +1111,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
         if (col >= p.N) continue;
         float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = cf * (expf(acc[i][j][q] - lse) - ((int64_t)(col + q) == t ? 1.f : 0.f));
+        for (int q = 0; q < 4; ++q) v[q] = cf * (fast_expf(acc[i][j][q] - lse) - ((int64_t)(col + q) == t ? 1.f : 0.f));
         if (col + 4 <= p.N) {
           store4(crow + col, nullptr, v);
         } else {

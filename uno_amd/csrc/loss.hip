@@ -32,8 +32,8 @@ __global__ __launch_bounds__(256) void row_lse_update_kernel(const T* __restrict
   const T* zr = z + (int64_t)row * ldz;
   float m = -INFINITY, s = 0.f;
   auto add = [&](float v) {
-    if (v > m) { s = s * expf(m - v) + 1.f; m = v; }   // expf(-inf) = 0 on the first value
-    else s += expf(v - m);
+    if (v > m) { s = s * fast_expf(m - v) + 1.f; m = v; }   // fast_expf(-inf) = 0 on the first value
+    else s += fast_expf(v - m);
   };
   int j0 = 0;
   if constexpr (std::is_same<T, float>::value) {
@@ -42,21 +42,21 @@ __global__ __launch_bounds__(256) void row_lse_update_kernel(const T* __restrict
       for (int q = threadIdx.x; q < nv; q += 256) {
         const float4 v = *(const float4*)(zr + 4 * q);
         const float mv = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
-        if (mv > m) { s *= expf(m - mv); m = mv; }
-        s += expf(v.x - m) + expf(v.y - m) + expf(v.z - m) + expf(v.w - m);
+        if (mv > m) { s *= fast_expf(m - mv); m = mv; }
+        s += fast_expf(v.x - m) + fast_expf(v.y - m) + fast_expf(v.z - m) + fast_expf(v.w - m);
       }
       j0 = 4 * nv;
     }
   }
   for (int j = j0 + threadIdx.x; j < Vc; j += 256) add(ldf(zr + j));
   const float mb = block_max(m, red);
-  s = block_sum(m == -INFINITY ? 0.f : s * expf(m - mb), red);
+  s = block_sum(m == -INFINITY ? 0.f : s * fast_expf(m - mb), red);
   m = mb;
   if (threadIdx.x == 0) {
     float M0 = first ? -INFINITY : run_max[row];
     float S0 = first ? 0.f : run_sum[row];
     const float Mn = fmaxf(M0, m);
-    run_sum[row] = (S0 > 0.f ? S0 * expf(M0 - Mn) : 0.f) + s * expf(m - Mn);
+    run_sum[row] = (S0 > 0.f ? S0 * fast_expf(M0 - Mn) : 0.f) + s * fast_expf(m - Mn);
     run_max[row] = Mn;
     if (tgt) {
       const int64_t t = tgt[row];
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void ce_grad_chunk_kernel(const float* __restr
       const int nv = Vc / 4;
       for (int q = threadIdx.x; q < nv; q += 256) {
         const float4 v = *(const float4*)(zr + 4 * q);
-        float p[4] = {expf(v.x - l), expf(v.y - l), expf(v.z - l), expf(v.w - l)};
+        float p[4] = {fast_expf(v.x - l), fast_expf(v.y - l), fast_expf(v.z - l), fast_expf(v.w - l)};
         if (t >= 4 * q && t < 4 * q + 4) p[t - 4 * q] -= 1.f;
         *(uint2*)(dr + 4 * q) = make_uint2(pack2_bf16(c * p[0], c * p[1]), pack2_bf16(c * p[2], c * p[3]));
       }
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void ce_grad_chunk_kernel(const float* __restr
     }
   }
   for (int j = j0 + threadIdx.x; j < Vc; j += 256) {
-    float p = expf(zr[j] - l);
+    float p = fast_expf(zr[j] - l);
     if (j == t) p -= 1.f;
     Elem<TO>::store(dr + j, c * p);
   }
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(256) void ce_parts_reduce_kernel(int nparts, const 
   for (int b = threadIdx.x; b < nparts; b += 256) m = fmaxf(m, pm[b]);
   m = block_max(m, red);
   float s = 0.f;
-  for (int b = threadIdx.x; b < nparts; b += 256) s += ps[b] > 0.f ? ps[b] * expf(pm[b] - m) : 0.f;
+  for (int b = threadIdx.x; b < nparts; b += 256) s += ps[b] > 0.f ? ps[b] * fast_expf(pm[b] - m) : 0.f;
   s = block_sum(s, red);
   if (threadIdx.x == 0) { run_max[row] = m; run_sum[row] = s; }
 }
