@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256) void softmax_stats_kernel(const T* __restrict_
   for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, ldf(zr + j));
   m = block_max(m, red);
   float s = 0.f;
-  for (int j = threadIdx.x; j < V; j += 256) s += expf(ldf(zr + j) - m);
+  for (int j = threadIdx.x; j < V; j += 256) s += fast_expf(ldf(zr + j) - m);
   s = block_sum(s, red);
   if (threadIdx.x == 0) { mx[row] = m; se[row] = fmaxf(s, 1.17549435e-38f); }
 }
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void tv_fwd_kernel(const T* __restrict__ zs, i
   const T* t = zt + (int64_t)row * ldt;
   float l1 = 0.f, S = 0.f;
   for (int j = threadIdx.x; j < V; j += 256) {
-    const float ps = expf(ldf(s + j) - a) * ia, pt = expf(ldf(t + j) - b) * ib;
+    const float ps = fast_expf(ldf(s + j) - a) * ia, pt = fast_expf(ldf(t + j) - b) * ib;
     const float d = ps - pt;
     l1 += fabsf(d);
     S += (d > 0.f ? ps : (d < 0.f ? -ps : 0.f));
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(256) void tv_bwd_kernel(const T* zs, int64_t lds, c
   const T* t = zt + (int64_t)row * ldt;
   T* gr = grad + (int64_t)row * ldg;
   for (int j = threadIdx.x; j < V; j += 256) {
-    const float ps = expf(ldf(s + j) - a) * ia, pt = expf(ldf(t + j) - b) * ib;
+    const float ps = fast_expf(ldf(s + j) - a) * ia, pt = fast_expf(ldf(t + j) - b) * ib;
     const float d = ps - pt;
     const float sg = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
     Elem<T>::store(gr + j, ps * (sg - S) * c);
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void kl_fwd_kernel(const T* __restrict__ zs, i
   float kl = 0.f;
   for (int j = threadIdx.x; j < V; j += 256) {
     const float ls = ldf(s + j) - la, lt = ldf(t + j) - lb;
-    kl += expf(ls) * (ls - lt);
+    kl += fast_expf(ls) * (ls - lt);
   }
   kl = block_sum(kl, red);
   if (threadIdx.x == 0) row_kl[row] = kl;
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void kl_bwd_kernel(const T* zs, int64_t lds, c
   T* gr = grad + (int64_t)row * ldg;
   for (int j = threadIdx.x; j < V; j += 256) {
     const float ls = ldf(s + j) - la, lt = ldf(t + j) - lb;
-    Elem<T>::store(gr + j, expf(ls) * ((ls - lt) - k) * c);
+    Elem<T>::store(gr + j, fast_expf(ls) * ((ls - lt) - k) * c);
   }
 }
 
