@@ -50,7 +50,7 @@ int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
  * gate features 64 b + [0, 64); rows 128 b + [64, 128): the same up features); rounded exactly as
  * unok_gemm_nt followed by unok_swiglu_fwd. With gu non-null, also stores the product itself as
  * gu[M, N] = [gate | up] (the layout of the plain product, for the backward). M and N multiples of
- * 256, K and K2 of 64; A2 may be null (K2 ignored). The remote Qwen3 decoder's MLP input to
+ * 256, K of 64 and K2 of 32; A2 may be null (K2 ignored). The remote Qwen3 decoder's MLP input to
  * down_proj, act_fn(gate_proj(x)) * up_proj(x) (modeling_qwen3.py:81-82), with the LoRA terms of
  * gate_proj and up_proj (peft 0.15.2 lora.Linear; training/lora.py:136-179). */
 int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
@@ -59,7 +59,7 @@ int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t lda, const v
 
 /* dgu[M, 2F] = SwiGLU backward of dS = A[M,K] B[F,K]^T + A2[M,K2] B2[F,K2]^T against
  * gu[M, 2F] = [gate | up] (dS is never stored); bf16, rounded exactly as unok_gemm_nt followed by
- * unok_swiglu_bwd. M and F multiples of 256, K and K2 of 64. Backward of the remote decoder's MLP
+ * unok_swiglu_bwd. M and F multiples of 256, K of 64, K2 of 32. Backward of the remote decoder's MLP
  * act_fn(gate_proj(x)) * up_proj(x) through down_proj (modeling_qwen3.py:81-82) with the LoRA
  * data-gradient extension of down_proj (peft 0.15.2 lora.Linear). */
 int unok_gemm_nt_swiglu_bwd(int M, int F, int K, const void* A, int64_t lda, const void* B, int64_t ldb,

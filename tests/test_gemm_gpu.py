@@ -242,3 +242,60 @@ def test_gemm_nt_swiglu_bwd_matches_unfused(dev, M, F, Kd, K2):
     fused = K.gemm_nt_swiglu_bwd(dy, wt, a2, b2, gu)
     torch.cuda.synchronize()
     assert torch.equal(fused, ref)
+
+
+@pytest.mark.parametrize("r", [32, 96])
+def test_gemm_nt_lora_rank_not_multiple_of_64(dev, r):
+    """LoRA extension of K2 = 32 (mod 64) on the 256x256 kernel (rank 32 of the 1B configuration):
+    the last extension tile is half full. Against fp32 torch, and bit for bit against the same
+    product with the extension zero-padded to the next multiple of 64."""
+    torch.manual_seed(r)
+    M, N, Kd = 4096, 6144, 512
+    ends = [4096, 5120, 6144]
+    assert K.nt_uses_256_tiles(M, N, ends)
+    a = torch.randn(M, Kd, device=dev).bfloat16()
+    w = (torch.randn(N, Kd, device=dev) * 0.1).bfloat16()
+    h = torch.randn(M, 3 * r, device=dev).bfloat16()
+    bl = (torch.randn(N, r, device=dev) * 0.1).bfloat16()
+    res = torch.randn(M, N, device=dev).bfloat16()
+    segs = [(4096, 0), (5120, r), (6144, 2 * r)]
+    out = K.gemm_nt(a, w, a2=h, b2=bl, segments=segs, residual=res)
+    ref = a.float() @ w.float().T
+    start = 0
+    for j, e in enumerate(ends):
+        ref[:, start:e] += h[:, j * r:(j + 1) * r].float() @ bl[start:e].float().T
+        start = e
+    ref += res.float()
+    rp = (r + 63) // 64 * 64
+    hp = torch.zeros(M, 3 * rp, device=dev, dtype=torch.bfloat16)
+    for j in range(3):
+        hp[:, j * rp:j * rp + r] = h[:, j * r:(j + 1) * r]
+    bp = torch.zeros(N, rp, device=dev, dtype=torch.bfloat16)
+    bp[:, :r] = bl
+    padded = K.gemm_nt(a, w, a2=hp, b2=bp, segments=[(4096, 0), (5120, rp), (6144, 2 * rp)], residual=res)
+    torch.cuda.synchronize()
+    assert _rel(out, ref) < 8e-3
+    assert torch.equal(out, padded)
+
+
+def test_gemm_nt_swiglu_bwd_rank_32(dev):
+    """The SwiGLU-backward product with a rank-32 LoRA extension equals the product with the
+    extension zero-padded to 64, bit for bit, and the unfused path within bf16 rounding."""
+    torch.manual_seed(5)
+    M, F, Kd, r = 1024, 1536, 512, 32
+    dy = (torch.randn(M, Kd, device=dev) * 0.5).bfloat16()
+    wt = (torch.randn(F, Kd, device=dev) * 0.1).bfloat16()
+    gu = (torch.randn(M, 2 * F, device=dev) * 2.0).bfloat16()
+    a2 = (torch.randn(M, r, device=dev) * 0.5).bfloat16()
+    b2 = (torch.randn(F, r, device=dev) * 0.1).bfloat16()
+    a2p = torch.zeros(M, 64, device=dev, dtype=torch.bfloat16)
+    a2p[:, :r] = a2
+    b2p = torch.zeros(F, 64, device=dev, dtype=torch.bfloat16)
+    b2p[:, :r] = b2
+    fused = K.gemm_nt_swiglu_bwd(dy, wt, a2, b2, gu)
+    padded = K.gemm_nt_swiglu_bwd(dy, wt, a2p, b2p, gu)
+    ds = (dy.float() @ wt.float().T + a2.float() @ b2.float().T).bfloat16()
+    ref = K.swiglu_bwd(ds, gu, F)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, padded)
+    assert _rel(fused, ref) < 1e-2

@@ -841,7 +841,10 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
   const int n0 = (ing / gsz) * BN;
   const bool ext = p.A2 != nullptr && p.K2 > 0;
   const int nk1 = p.K / BK;
-  const int nk = nk1 + (ext ? p.K2 / BK : 0);
+  // The LoRA extension runs in whole 64-deep tiles; K2 = 32 (mod 64) leaves the last one half full,
+  // and its second 32-wide k-step then runs on zeroed fragments.
+  const int nk = nk1 + (ext ? (p.K2 + BK - 1) / BK : 0);
+  const bool half_last = ext && (p.K2 % BK) != 0;
 
   const int lrowi = lane / CPR, slot = lane % CPR;
   __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(((int64_t)(p.M - 1) * p.lda + p.K) * 2));
@@ -955,6 +958,12 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t kb = dma_tile(min(kt + 2, nk - 1));
+    if (half_last && kt == nk - 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa1[i] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb1[j] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+    }
     step(fa1, fb1, fa0, fb0, nxt, 0, DF{}, kb, cur);
   }
   __builtin_amdgcn_s_waitcnt(0x0070);       // clamped loads still write LDS
@@ -1348,8 +1357,8 @@ UNOK_EXPORT int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t 
                M, N, K);
   if (M == 0 || N == 0) return 0;
   const bool ext = A2 != nullptr && K2 > 0;
-  UNOK_REQUIRE(M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && K > 0 && (!ext || K2 % 64 == 0), UNOK_EINVAL,
-               "gemm_nt_swiglu: M=%d and N=%d must be multiples of 256, K=%d and K2=%d of 64", M, N, K, K2);
+  UNOK_REQUIRE(M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && K > 0 && (!ext || K2 % 32 == 0), UNOK_EINVAL,
+               "gemm_nt_swiglu: M=%d and N=%d must be multiples of 256, K=%d of 64 and K2=%d of 32", M, N, K, K2);
   UNOK_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldc % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(C) &&
                    (!ext || (lda2 % 8 == 0 && ldb2 % 8 == 0 && aligned16(A2) && aligned16(B2))) &&
                    (gu == nullptr || (ldgu % 8 == 0 && aligned16(gu))),
@@ -1367,15 +1376,15 @@ UNOK_EXPORT int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t 
 
 // dgu[M, 2F] = SwiGLU backward of dS = A[M,K] B[F,K]^T + A2[M,K2] B2[F,K2]^T (bf16, never stored)
 // against gu[M, 2F] = [gate | up]; rounded exactly as unok_gemm_nt followed by unok_swiglu_bwd.
-// M and F multiples of 256, K and K2 of 64.
+// M and F multiples of 256, K of 64, K2 of 32.
 UNOK_EXPORT int unok_gemm_nt_swiglu_bwd(int M, int F, int K, const void* A, int64_t lda, const void* B,
                                         int64_t ldb, const void* A2, int64_t lda2, const void* B2, int64_t ldb2,
                                         int K2, const void* gu, int64_t ldgu, void* dgu, int64_t lddgu,
                                         void* stream) {
   UNOK_REQUIRE(M >= 0 && F >= 0 && K >= 0 && K2 >= 0, UNOK_EINVAL, "gemm_nt_swiglu_bwd: negative size");
   if (M == 0 || F == 0) return 0;
-  UNOK_REQUIRE(M % 256 == 0 && F % 256 == 0 && K % 64 == 0 && K > 0 && K2 % 64 == 0, UNOK_EINVAL,
-               "gemm_nt_swiglu_bwd: M=%d and F=%d must be multiples of 256, K=%d and K2=%d of 64", M, F, K, K2);
+  UNOK_REQUIRE(M % 256 == 0 && F % 256 == 0 && K % 64 == 0 && K > 0 && K2 % 32 == 0, UNOK_EINVAL,
+               "gemm_nt_swiglu_bwd: M=%d and F=%d must be multiples of 256, K=%d of 64 and K2=%d of 32", M, F, K, K2);
   UNOK_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ldgu % 8 == 0 && lddgu % 8 == 0 && aligned16(A) && aligned16(B) &&
                    aligned16(gu) && aligned16(dgu) && (K2 == 0 || (lda2 % 8 == 0 && ldb2 % 8 == 0 && aligned16(A2) &&
                                                                    aligned16(B2))),
@@ -1504,7 +1513,7 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
   } else if (N <= 128 || !segs_ok(256) || big_tiles < 256) {
     if ((long long)((M + 127) / 128) * ((N + 127) / 128) < 256) launch_nt_bf16<64, 128>(p, out_dtype, st);
     else launch_nt_bf16<128, 128>(p, out_dtype, st);
-  } else if (K % 64 == 0 && (!p.A2 || p.K2 % 64 == 0)) {
+  } else if (K % 64 == 0 && (!p.A2 || p.K2 % 32 == 0)) {
     if (out_dtype == UNOK_F32) launch_nt_large<float>(p, st); else launch_nt_large<bf16_t>(p, st);
   } else {
     launch_nt_bf16<256, 256>(p, out_dtype, st);

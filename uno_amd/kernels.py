@@ -228,7 +228,7 @@ def gemm_nt_swiglu(a: torch.Tensor, b_interleaved: torch.Tensor, *, a2: torch.Te
                    out: torch.Tensor | None = None) -> torch.Tensor:
     """silu(gate) * up of a @ b.T (+ a2 @ b2.T) for gate/up weight rows interleaved in blocks of 64
     (``interleave_gate_up``; b2 likewise); bf16, M and the row count of b multiples of 256, K and
-    K2 = b2.shape[1] of 64. With ``gu`` ([M, rows]), also stores the product as [gate | up]."""
+    K2 = b2.shape[1] of 32. With ``gu`` ([M, rows]), also stores the product as [gate | up]."""
     _rowmajor(a, "a")
     _rowmajor(b_interleaved, "b")
     M, K = a.shape

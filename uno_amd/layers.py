@@ -108,7 +108,7 @@ def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: St
     x2, rstd2 = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
     h_gu = K.gemm_nt(x2, lora.a_c(li, "gu"))
     sb_gu_i = lora.sb_gu_i(li) if lw.w_gu_i is not None and x2.dtype == torch.bfloat16 else None
-    if sb_gu_i is not None and (2 * r) % 64 == 0 and K.swiglu_fused_ok(x2.shape[0], g.F, x2.shape[1]):
+    if sb_gu_i is not None and (2 * r) % 32 == 0 and K.swiglu_fused_ok(x2.shape[0], g.F, x2.shape[1]):
         # gate/up product with its LoRA terms, SwiGLU in the epilogue; [gate | up] kept for backward
         gu = torch.empty((x2.shape[0], 2 * g.F), device=x2.device, dtype=x2.dtype)
         s = K.gemm_nt_swiglu(x2, lw.w_gu_i, a2=h_gu, b2_interleaved=sb_gu_i, gu=gu)
@@ -158,7 +158,7 @@ class NoisyLayer(torch.autograd.Function):
         # ---- down projection ----------------------------------------------------------
         g_d = K.gemm_nt(dh2, lora.sb_t(li, "d"))                              # [M, r]
         K.gemm_tn(dh2, h_d, out=gb(li, "d"), alpha=sc_l, beta=1.0)            # dB_d
-        if dh2.dtype == torch.bfloat16 and M % 256 == 0 and g.F % 256 == 0 and g.H % 64 == 0 and r % 64 == 0:
+        if dh2.dtype == torch.bfloat16 and M % 256 == 0 and g.F % 256 == 0 and g.H % 64 == 0 and r % 32 == 0:
             # dS = dh2 W_d + g_d A_d never leaves the GEMM: its epilogue applies the SwiGLU backward
             dgu = K.gemm_nt_swiglu_bwd(dh2, lw.w_d_t, g_d, lora.a_t(li, "d"), gu)
         else:
