@@ -349,7 +349,7 @@ def main() -> int:
     # Roofline window: as many further steps with HIP events around every 256x256 GEMM launch.
     # A recorded event delays the next dispatch by a few microseconds, so these steps are not the
     # ones that give the step time.
-    rec = K.LaunchRecorder(lambda dt, M, N, Kd, K2, segs: dt == torch.bfloat16 and K.nt_uses_256_tiles(M, N, segs))
+    rec = K.LaunchRecorder(lambda dt, M, N, Kd, K2, segs: dt == torch.bfloat16 and K.nt_uses_256_tiles(M, N, segs, Kd))
     K.set_recorder(rec)
     for i in range(args.steps):
         trainer.train_step(batch)

@@ -1510,7 +1510,8 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
   } else if (N <= 64 || !segs_ok(128)) {
     UNOK_REQUIRE(segs_ok(64), UNOK_EINVAL, "gemm_nt(bf16): segment ends must be multiples of 64");
     launch_nt_bf16<128, 64>(p, out_dtype, st);
-  } else if (N <= 128 || !segs_ok(256) || big_tiles < 256) {
+  } else if (N <= 128 || !segs_ok(256) || big_tiles < (K >= 8192 ? 192 : 256)) {
+    // (a long-K product keeps the 256x256 kernel down to three quarters of a tile per CU)
     if ((long long)((M + 127) / 128) * ((N + 127) / 128) < 256) launch_nt_bf16<64, 128>(p, out_dtype, st);
     else launch_nt_bf16<128, 128>(p, out_dtype, st);
   } else if (K % 64 == 0 && (!p.A2 || p.K2 % 32 == 0)) {

@@ -36,13 +36,13 @@ def set_recorder(rec: LaunchRecorder | None) -> None:
     _recorder = rec
 
 
-def nt_uses_256_tiles(M: int, N: int, seg_end) -> bool:
+def nt_uses_256_tiles(M: int, N: int, seg_end, K: int = 0) -> bool:
     """Mirror of the tile choice in unok_gemm_nt for bf16 (the 256x256 MFMA kernel)."""
     if N <= 128:
         return False
     if any(e % 256 for e in list(seg_end)[:-1]):
         return False
-    return ((M + 255) // 256) * ((N + 255) // 256) >= 256
+    return ((M + 255) // 256) * ((N + 255) // 256) >= (192 if K >= 8192 else 256)
 
 
 def _rowmajor(t: torch.Tensor, name: str) -> None:
