@@ -10,8 +10,11 @@ Prints ONE JSON line. ``value`` = training tokens/s (B*L input tokens per step, 
 accounting). ``roofline`` = the dominant kernel (256x256 bf16 MFMA GEMM of the fused LoRA
 linears and the LM head): algorithmic FLOPs per launch / mean launch time, from HIP events around
 every such launch in as many steps again right after the timed ones (an event delays the next
-dispatch by a few microseconds, so the timed steps carry none). ``cpu_baseline`` = the CPU oracle
-of the same step timed on this host on a bounded sample (see cpu_baseline()).
+dispatch by a few microseconds, so the timed steps carry none). ``step_ms`` = median and
+10th / 90th percentile of the timed steps from one HIP event between consecutive steps.
+``cpu_baseline`` = the CPU oracle of the same step timed on this host on a bounded sample (see
+cpu_baseline()). ``--workload draft_8b`` measures the inference-side draft forward instead (see
+run_draft()).
 """
 from __future__ import annotations
 
@@ -65,11 +68,18 @@ def objective(name: str):
     return table[name]
 
 
+# The inference side (--workload draft_8b): the draft forward of two-pass block decoding on the
+# Qwen3-8B shape with the same rank-64 adapter, 8 sequences whose caches hold a 4096-token prompt,
+# blocks of 16 rows (seed + 15 noise rows, LoRA on the noise rows), one committed row per block.
+DRAFT = dict(batch=8, prompt=4096, block_size=16, lora_rank=64, lora_alpha=128)
+
 WORKLOAD_NAMES = {
     "qwen3_8b": "Qwen3-8B-shape cond-LoRA block-diffusion step (36 layers, 4 x 4096 tokens, block 16, LoRA r64)",
     "dense_1b": "1B-class (16 layers, hidden 2048, 16q/8kv) cond-LoRA step, rank 32",
     "mha_7b": "7B MHA (no q/k-norm, vocab 32000) cond-LoRA step, block curriculum 4/8/16/32",
     "packed_16k": "Qwen3-8B-shape step on one 16384-token row of packed segments, block 32",
+    "draft_8b": "Qwen3-8B-shape draft forward of two-pass block decoding: 8 sequences x 16-row blocks "
+                "over 4096-token KV caches, gated rank-64 LoRA, one HIP graph per block",
 }
 
 
@@ -162,6 +172,115 @@ def algorithmic_flops(cfg: dict, wl: dict, mask, head_rows: tuple[int, int], r: 
     }
     f["total"] = sum(f.values())
     return f
+
+
+def spread(ms: list[float]) -> dict:
+    """Median, 10th and 90th percentile (nearest rank) of per-step HIP-event times in ms."""
+    srt = sorted(ms)
+    pick = lambda f: round(srt[min(len(srt) - 1, max(0, int(round(f * (len(srt) - 1)))))], 3)
+    return {"median": pick(0.5), "p10": pick(0.1), "p90": pick(0.9), "n": len(srt)}
+
+
+def draft_bytes(cfg: dict, B: int, L: int, cached: float, r: int) -> dict:
+    """Algorithmic HBM bytes of one draft block of B sequences x L rows over caches holding
+    ``cached`` rows per sequence (mean): every frozen linear weight and the LM head read once, the
+    bf16 LoRA A and (alpha/r) B compute copies read once, each (sequence, K/V head)'s cache rows
+    read once (cached + L rows of K and of V: the block's own rows are stored before attention
+    reads them), the block's K/V rows written, the embedding rows gathered and the logits written,
+    all bf16. The activations passed between kernels (about 36 MB per layer at B*L = 128 rows,
+    L2- and MALL-resident) are not counted."""
+    H, F, d = cfg["hidden_size"], cfg["intermediate_size"], cfg["head_dim"]
+    q, kv, Lyr, V = cfg["num_attention_heads"] * d, cfg["num_key_value_heads"] * d, cfg["num_hidden_layers"], cfg["vocab_size"]
+    nk = cfg["num_key_value_heads"]
+    n_lin = Lyr * (H * (q + 2 * kv) + q * H + 3 * H * F)
+    n_lora = Lyr * r * ((H + q) + 2 * (H + kv) + (q + H) + 2 * (H + F) + (F + H))
+    b = {"linear_weights": 2 * n_lin, "lora": 2 * n_lora, "lm_head": 2 * V * H,
+         "kv_read": int(Lyr * B * nk * (cached + L) * d * 2 * 2), "kv_write": Lyr * B * L * nk * d * 2 * 2,
+         "embedding": B * L * H * 2, "logits": B * L * V * 2}
+    b["total"] = sum(b.values())
+    return b
+
+
+def run_draft(args) -> int:
+    """Draft-forward benchmark: prefill B x 4096 prompt tokens into the caches, capture one draft
+    block as a HIP graph, replay it for the warm-up and the timed blocks (HIP events on the
+    replaying stream around each block). ``value`` = drafted rows/s (B*L per block); the roofline
+    is the block's algorithmic HBM bytes over its time against 8 TB/s."""
+    from uno_amd.inference import BlockDecoder
+    from uno_amd.model import UnoQwen3Config, UnoQwen3ForCausalLM
+    from uno_amd.training.config import LoraSettings
+    from uno_amd.training.lora import create_lora_model
+
+    seed = 20260813
+    layers = args.layers or QWEN3_8B["num_hidden_layers"]
+    cfg_kw = dict(QWEN3_8B, num_hidden_layers=layers)
+    wl = dict(DRAFT)
+    if args.batch is not None:
+        wl["batch"] = args.batch
+    B, P, L, r = wl["batch"], wl["prompt"], wl["block_size"], wl["lora_rank"]
+    dev = "cuda:0"
+    model = UnoQwen3ForCausalLM(UnoQwen3Config(**cfg_kw, block_size=L, noise_seed=seed), device=dev,
+                                dtype=torch.bfloat16)
+    model.random_init(seed, std=0.02)
+    lm, _ = create_lora_model(model, LoraSettings("all", r, wl["lora_alpha"], 0.0), seed=seed + 1)
+    dec = BlockDecoder(lm)
+    n_blocks = args.warmup + args.steps
+    cache = dec.new_cache(B, P + n_blocks + L)
+    g = torch.Generator(device=dev).manual_seed(seed + 2)
+    V = cfg_kw["vocab_size"]
+    prompt = torch.randint(0, V - 1, (B, P), device=dev, generator=g)
+    blocks = torch.randint(0, V - 1, (n_blocks, B, L), device=dev, generator=g)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    logits = dec.prefill(cache, prompt)
+    e1.record()
+    torch.cuda.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+    del logits
+    torch.cuda.empty_cache()
+    print(f"[bench] prefill {B} x {P} tokens: {prefill_ms:.1f} ms", file=sys.stderr, flush=True)
+    dg = dec.capture_draft(cache, L)
+    for i in range(args.warmup):
+        dg.replay(blocks[i])
+    torch.cuda.synchronize()
+    print(f"[bench] draft graph captured; warmup {args.warmup} blocks done", file=sys.stderr, flush=True)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    cached0 = float(cache.lengths.float().mean())
+    t0 = time.perf_counter()
+    evs[0].record()
+    for i in range(args.steps):
+        dg.replay(blocks[args.warmup + i])
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]
+    ms_block = (t1 - t0) * 1000.0 / args.steps
+    ev_ms = sum(per) / len(per)
+    cached = cached0 + (args.steps - 1) / 2.0          # one committed row per block
+    by = draft_bytes(cfg_kw, B, L, cached, r)
+    gbs = by["total"] / (ev_ms / 1000.0) / 1e9
+    out = {
+        "metric": "draft rows/s/GPU, Qwen3-8B-shape two-pass draft block forward (8 x 16 rows, 4096-token caches)",
+        "value": round(B * L / (ms_block / 1000.0), 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_block, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (uniform token ids, random N(0,0.02) weights)",
+        "config": {"workload": WORKLOAD_NAMES["draft_8b"], "layers": layers, "sequences": B, "block_size": L,
+                   "cached_rows_mean": cached, "lora_rank": r, "lora_alpha": wl["lora_alpha"],
+                   "parallelism": "single GPU"},
+        "step_ms": spread(per),
+        "prefill_ms": round(prefill_ms, 1), "prefill_tokens_per_s": round(B * P / (prefill_ms / 1000.0), 1),
+        "bytes_per_block_gb": {k: round(v / 1e9, 4) for k, v in by.items()},
+        "roofline": {"kernel": "the draft block's HIP graph (every kernel of the 36-layer forward and the LM head)",
+                     "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "launches": args.steps,
+                     "mean_launch_ms": round(ev_ms, 4),
+                     "window": "the timed blocks, HIP events around each graph replay"},
+        "cpu_baseline": None,
+        "peak_hbm_gb": round(torch.cuda.max_memory_allocated() / 1e9, 1),
+    }
+    print(json.dumps(out))
+    return 0
 
 
 def cpu_baseline(threads: int) -> dict:
@@ -264,7 +383,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS),
+    ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS) + ["draft_8b"],
                     help="qwen3_8b is the headline; the others measure further model/batch shapes")
     ap.add_argument("--layers", type=int, default=None,
                     help="decoder layers (default: the workload's full depth)")
@@ -289,6 +408,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.workload == "draft_8b":
+        return run_draft(args)
     from uno_amd import kernels as K
 
     base_cfg, wl = WORKLOADS[args.workload]
@@ -341,11 +462,15 @@ def main() -> int:
     flops = {k: sum(per_block[b][k] for b in blocks) / len(blocks) for k in per_block[blocks[0]]}
 
     torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
+    evs[0].record()
     for i in range(args.steps):
         trainer.train_step(batch)
+        evs[i + 1].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    per_step = [evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]
     # Roofline window: as many further steps with HIP events around every 256x256 GEMM launch.
     # A recorded event delays the next dispatch by a few microseconds, so these steps are not the
     # ones that give the step time.
@@ -373,6 +498,7 @@ def main() -> int:
                    "block_size": blocks[0] if len(set(blocks)) == 1 else blocks,
                    "lora_rank": wl["lora_rank"], "lora_alpha": wl["lora_alpha"],
                    "objective": objective(wl.get("objective", "ce"))[1], "parallelism": "single GPU"},
+        "step_ms": spread(per_step),
         "mfu": round(mfu, 4), "algorithmic_tflop_per_step": round(flops["total"] / 1e12, 2),
         "flops_breakdown_tflop": {k: round(v / 1e12, 2) for k, v in flops.items() if k != "total"},
         "roofline": {"kernel": "gemm_nt_bf16_w4m16_kernel (256x256 tiles, 16x16x32 MFMA; fused LoRA linears, "

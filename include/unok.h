@@ -66,6 +66,31 @@ int unok_gemm_nt_swiglu_bwd(int M, int F, int K, const void* A, int64_t lda, con
                             const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,
                             const void* gu, int64_t ldgu, void* dgu, int64_t lddgu, void* stream);
 
+/* Gated LoRA linear for decode and draft blocks (bf16), where M = sequences x block rows (128 for 8
+ * sequences of 16) and the product streams the weight once:
+ *   y = A B^T + H[:, seg_col(n) : +r] LB[n, :r]^T + Res,  H = bf16(gate (.) (A LA^T))  [M, R],
+ * A [M,K] activations, B [N,K] weight, LA [R,K] the LoRA A rows of all segments, LB [N,r] the
+ * (alpha/r)-scaled LoRA B; segment i covers output columns [seg_end[i-1], seg_end[i]) and reads
+ * H columns [seg_col[i], seg_col[i] + r). LA null: no LoRA (R, LB, r and the segments ignored).
+ * epilogue 0: C[M,N] = y;  epilogue 1: C[M,N/2] = silu(G) (.) U of y = [G | U] (no Res), rounded as
+ * y in bf16 followed by unok_swiglu_fwd. The product runs on 128 x 128 output tiles (the LA rows are
+ * extra columns), each split into `splits` ranges of the K tiles (splits <= 0: chosen from the
+ * shape) so the grid fills the chip; the ranges' fp32 partial sums go through `workspace` (at
+ * least unok_gemm_nt_rows_workspace() bytes, 16-byte aligned) and a second kernel adds them in
+ * range order (the result does not depend on timing), forms H and applies the rank-r update and
+ * the epilogue. One range without LoRA and epilogue 0 writes C directly and needs no workspace.
+ * K a multiple of 128, N of 4 (of 8 for epilogue 1), R of 4 (at most 512), r of 8 (at most 128).
+ * Replaces: the LoRA linear of the draft forward, nano_vllm_uno/layers/linear.py:241-307 (base
+ * projection plus lora_B(lora_A(x) * lora_mask) * scaling, the mask off on the seed row), called
+ * from engine/two_pass_decoding.py:273-283, and the MLP activation that follows gate_up_proj
+ * (SiluAndMul, nano_vllm_uno/layers/activation.py:6, applied at nano_vllm_uno/models/qwen3.py:128-132). */
+int64_t unok_gemm_nt_rows_workspace(int M, int N, int K, int R, int epilogue, int splits);
+int unok_gemm_nt_rows(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
+                      const void* LA, int64_t ldla, int R, const void* LB, int64_t ldlb, int r,
+                      int nseg, const int* seg_end, const int* seg_col,
+                      void* C, int64_t ldc, const void* Res, int64_t ldres, const uint8_t* gate,
+                      int epilogue, int splits, void* workspace, int64_t ws_bytes, void* stream);
+
 /* C[P,Q] (fp32) = beta * C + alpha * A[Mrows,P]^T B[Mrows,Q] (split-K over rows through a
  * caller workspace of unok_gemm_tn_workspace() bytes). LoRA weight gradients
  * dB = s dY^T h, dA = g^T x. Replaces: autograd of lora_A / lora_B (peft 0.15.2) under

@@ -29,6 +29,9 @@ SIGNATURES: dict[str, tuple] = {
     "unok_gemm_nt_swiglu": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i, _p, _i64, _p, _i64, _p]),
     "unok_gemm_nt_swiglu_bwd": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i, _p, _i64, _p, _i64,
                                      _p]),
+    "unok_gemm_nt_rows_workspace": (_i64, [_i, _i, _i, _i, _i, _i]),
+    "unok_gemm_nt_rows": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _i, _p, _i64, _i, _i, _ip, _ip, _p, _i64,
+                               _p, _i64, _p, _i, _i, _p, _i64, _p]),
     "unok_gemm_tn_workspace": (_i64, [_i, _i, _i]),
     "unok_gemm_tn": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _f, _f, _p, _i64, _p]),
     "unok_gemm_tn_noalloc": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _f, _f, _p]),

@@ -81,14 +81,20 @@ class BlockDecoder:
             raise ValueError(f"commit must lie in [0, {L}]")
         return self._forward(cache, block_ids, lora_mask.to(torch.bool), commit=commit, prefill=False)
 
+    def capture_draft(self, cache: BlockKVCache, block_size: int, commit: int = 1) -> "DraftGraph":
+        """A draft block of [cache.batch, block_size] rows over ``cache`` captured as one HIP graph
+        (see DraftGraph)."""
+        return DraftGraph(self, cache, block_size, commit)
+
     # ---- the decoder -----------------------------------------------------------------------------
-    def _forward(self, cache: BlockKVCache, ids: torch.Tensor, gate: torch.Tensor, commit: int, prefill: bool):
+    def _forward(self, cache: BlockKVCache, ids: torch.Tensor, gate: torch.Tensor, commit: int, prefill: bool,
+                 check: bool = True):
         g, lora, dec = self.geo, self.lora, self.decoder
         B, L = ids.shape
         if B != cache.batch:
             raise RuntimeError(f"block batch {B} does not match the cache batch {cache.batch}")
         lengths = cache.lengths
-        if int((lengths + L).max()) > cache.max_len:
+        if check and int((lengths + L).max()) > cache.max_len:
             raise RuntimeError("the block does not fit in the KV cache")
         rep = g.nq // g.nk
         if not prefill and rep * L > 128:
@@ -104,7 +110,9 @@ class BlockDecoder:
             lw = layer.weights()
             h = self._layer(h, lw, li, pos, gate_rows, cache, maps, B, L, prefill)
         x, _ = K.rmsnorm_fwd(h, dec.norm.weight, g.eps)
-        logits = K.gemm_nt(x, self.base.lm_head.weight)
+        V = self.base.lm_head.weight.shape[0]
+        head = K.gemm_nt_rows if self._rows_path(M, x.dtype, prefill) and V % 4 == 0 else K.gemm_nt
+        logits = head(x, self.base.lm_head.weight)
         cache.lengths += commit
         return logits.view(B, L, -1)
 
@@ -138,22 +146,39 @@ class BlockDecoder:
         valid = slot < rep * L
         tt = slot % L
         start = pair[:, None] * cache.max_len                                           # [pairs, 1]
-        seen = lengths.repeat_interleave(g.nk)[:, None] + tt[None, :] + 1               # causal over cache + block
+        seen = lengths[:, None].expand(B, g.nk).reshape(-1, 1) + tt[None, :] + 1        # causal over cache + block
         # rows past rep * L are padding: they see the pair's first key and their output is dropped
         iv[:, 0] = start.expand(-1, 128).reshape(-1)
         iv[:, 1] = torch.where(valid[None, :], start + seen, start + 1).reshape(-1)
         out["iv"] = iv
         return out
 
+    def _rows_path(self, M: int, dtype, prefill: bool) -> bool:
+        """Draft blocks in bf16 take the few-row products (K ranges over the whole chip) when every
+        linear's shape fits them; prefills and fp32 models take gemm_nt."""
+        g, r = self.geo, self.lora.rank
+        return (not prefill and dtype == torch.bfloat16 and M <= 512 and r % 8 == 0 and 3 * r <= 512
+                and all(k % 128 == 0 for k in (g.H, g.q, g.F)))
+
     def _layer(self, h0, lw, li, pos, gate_rows, cache, maps, B, L, prefill):
         g, lora = self.geo, self.lora
         r = lora.rank
         q_end, k_end = g.q, g.q + g.kv
         M = h0.shape[0]
+        few = self._rows_path(M, h0.dtype, prefill)
+        qkv_segments = [(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)]
+
+        def linear(x, w, part, segments=None, residual=None, swiglu=False):
+            """Gated LoRA linear: x w^T + (m (.) x A^T)[:, seg] (s B)^T (+ residual)."""
+            if few:
+                return K.gemm_nt_rows(x, w, lora_a=lora.a_c(li, part), lora_b=lora.sb_c(li, part),
+                                      segments=segments, residual=residual, gate=gate_rows, swiglu=swiglu)
+            h = K.gemm_nt(x, lora.a_c(li, part), gate=gate_rows)
+            y = K.gemm_nt(x, w, a2=h, b2=lora.sb_c(li, part), segments=segments, residual=residual)
+            return K.swiglu_fwd(y, y.shape[1] // 2) if swiglu else y
+
         x1, _ = K.rmsnorm_fwd(h0, lw.ln_in, g.eps)
-        h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv"), gate=gate_rows)
-        qkv = K.gemm_nt(x1, lw.w_qkv, a2=h_qkv, b2=lora.sb_c(li, "qkv"),
-                        segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)])
+        qkv = linear(x1, lw.w_qkv, "qkv", qkv_segments)
         q, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, pos, self.decoder.inv_freq, g.eps)
         v = qkv[:, k_end:]
         ck = cache.k[li].view(-1, g.d)
@@ -170,11 +195,64 @@ class BlockDecoder:
             od, _ = K.attn_fwd(qd, ck, cv, maps["iv"], 1, 1, g.d)
             o = torch.empty((M, g.q), device=q.device, dtype=q.dtype)
             K.rows_copy(od, o.view(M * g.nq, g.d), M * g.nq, smap=maps["qrow"])
-        h_o = K.gemm_nt(o, lora.a_c(li, "o"), gate=gate_rows)
-        h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o"), residual=h0)
+        h1 = linear(o, lw.w_o, "o", residual=h0)
         x2, _ = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
-        h_gu = K.gemm_nt(x2, lora.a_c(li, "gu"), gate=gate_rows)
-        gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu"), segments=[(g.F, 0), (2 * g.F, r)])
-        s = K.swiglu_fwd(gu, g.F)
-        h_d = K.gemm_nt(s, lora.a_c(li, "d"), gate=gate_rows)
-        return K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d"), residual=h1)
+        # few-row path: the reduction of the gate/up product applies the SwiGLU ([gate | up] is never stored)
+        s = linear(x2, lw.w_gu, "gu", [(g.F, 0), (2 * g.F, r)], swiglu=True)
+        return linear(s, lw.w_d, "d", residual=h1)
+
+
+class DraftGraph:
+    """A draft block of fixed shape [B, L] over one cache, captured as a single HIP graph.
+
+    The decoder issues about twenty kernels per layer; launched one by one from Python, a block of a
+    36-layer model costs more host time than device time. Replaying the captured graph is one host
+    call per block. Everything that depends on the committed lengths (the positions, the cache
+    store rows, the decode query layout and the key intervals) is computed on the device from
+    ``cache.lengths`` inside the graph, so each replay drafts at the current lengths and then
+    advances them by ``commit``, exactly as ``BlockDecoder.draft_block``.
+
+    ``replay`` returns the graph's own logits buffer [B, L, V], overwritten by the next replay.
+    The cache capacity is checked on the host against the longest committed length read at
+    capture plus the commits since; after changing ``cache.lengths`` by other means, capture
+    again."""
+
+    def __init__(self, decoder: BlockDecoder, cache: BlockKVCache, block_size: int, commit: int = 1):
+        B, L = cache.batch, block_size
+        rep = decoder.geo.nq // decoder.geo.nk
+        if rep * L > 128:
+            raise NotImplementedError(f"draft blocks hold at most 128 / {rep} rows per sequence (got {L})")
+        if not 0 <= commit <= L:
+            raise ValueError(f"commit must lie in [0, {L}]")
+        dev = cache.lengths.device
+        self.cache, self.block_size, self.commit = cache, L, commit
+        self.ids = torch.zeros((B, L), device=dev, dtype=torch.int64)
+        self.gate = torch.ones((B, L), device=dev, dtype=torch.bool)
+        self.gate[:, 0] = False
+        self._len_max = int(cache.lengths.max())
+        if self._len_max + L > cache.max_len:
+            raise RuntimeError("the block does not fit in the KV cache")
+        # One eager pass without commit before the capture: it sets each kernel's launch attributes
+        # outside the graph. Its K/V rows lie past the committed lengths, where the first replay
+        # writes them again.
+        decoder._forward(cache, self.ids, self.gate, commit=0, prefill=False)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = decoder._forward(cache, self.ids, self.gate, commit=commit, prefill=False, check=False)
+
+    def replay(self, block_ids: torch.Tensor, lora_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """Draft one block [B, L] of token ids (device int64); ``lora_mask`` [B, L] replaces the
+        default gate (off on the seed row, on for the noise rows) for this and later replays."""
+        if tuple(block_ids.shape) != tuple(self.ids.shape):
+            raise RuntimeError(f"block {tuple(block_ids.shape)} does not match the captured {tuple(self.ids.shape)}")
+        if self._len_max + self.block_size > self.cache.max_len:
+            raise RuntimeError("the block does not fit in the KV cache")
+        self.ids.copy_(block_ids)
+        if lora_mask is not None:
+            if tuple(lora_mask.shape) != tuple(self.gate.shape):
+                raise RuntimeError(f"LoRA row mask {tuple(lora_mask.shape)} does not match the block")
+            self.gate.copy_(lora_mask)
+        self.graph.replay()
+        self._len_max += self.commit
+        return self.logits

@@ -19,13 +19,16 @@ class LaunchRecorder:
 
     def __init__(self, predicate):
         self.predicate = predicate
-        self.records = []   # (start_event, end_event, flops)
+        self.records = []   # (start_event, end_event, flops, (M, N, K, K2))
 
     def elapsed(self):
         torch.cuda.synchronize()
-        ms = [a.elapsed_time(b) for a, b, _ in self.records]
-        fl = [f for _, _, f in self.records]
+        ms = [r[0].elapsed_time(r[1]) for r in self.records]
+        fl = [r[2] for r in self.records]
         return ms, fl
+
+    def shapes(self):
+        return [r[3] for r in self.records]
 
 
 _recorder: LaunchRecorder | None = None
@@ -120,7 +123,60 @@ def gemm_nt(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
            N.ptr(gate), float(alpha), N.stream())
     if rec is not None:
         ev1.record()
-        rec.records.append((ev0, ev1, 2.0 * M * Nn * (K + K2)))
+        rec.records.append((ev0, ev1, 2.0 * M * Nn * (K + K2), (M, Nn, K, K2)))
+    return out
+
+
+def gemm_nt_rows(a: torch.Tensor, b: torch.Tensor, *, lora_a: torch.Tensor | None = None,
+                 lora_b: torch.Tensor | None = None, segments: Sequence[tuple[int, int]] | None = None,
+                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
+                 swiglu: bool = False, splits: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Few-row gated LoRA linear (decode and draft blocks), bf16:
+    y = a b^T + h[:, seg] lora_b^T + residual with h = bf16(gate (.) a lora_a^T).
+
+    a [M,K], b [N,K]; lora_a [R,K] (all segments' A rows), lora_b [N,r] ((alpha/r) B);
+    ``segments`` is a list of (n_end, h_col) pairs: output columns < n_end (and >= the previous
+    end) use h[:, h_col:h_col+r]. With ``swiglu`` the result is silu(G) * U of y = [G | U],
+    [M, N/2]. ``splits`` = 0 lets the library choose the K ranges."""
+    _rowmajor(a, "a")
+    _rowmajor(b, "b")
+    M, K = a.shape
+    Nn = b.shape[0]
+    if b.shape[1] != K or a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise RuntimeError(f"gemm_nt_rows: bf16 a [M,K] and b [N,K] required, got {tuple(a.shape)} {tuple(b.shape)}")
+    R = r = 0
+    seg_end, seg_col = [], []
+    if lora_a is not None:
+        _rowmajor(lora_a, "lora_a")
+        _rowmajor(lora_b, "lora_b")
+        if lora_a.dtype != a.dtype or lora_b.dtype != a.dtype or lora_a.shape[1] != K or lora_b.shape[0] != Nn:
+            raise RuntimeError("gemm_nt_rows: LoRA operands must be bf16 lora_a [R,K] and lora_b [N,r]")
+        R, r = lora_a.shape[0], lora_b.shape[1]
+        segs = list(segments) if segments else [(Nn, 0)]
+        seg_end = [s[0] for s in segs]
+        seg_col = [s[1] for s in segs]
+    ncol = Nn // 2 if swiglu else Nn
+    if out is None:
+        out = torch.empty((M, ncol), device=a.device, dtype=a.dtype)
+    _rowmajor(out, "out")
+    if tuple(out.shape) != (M, ncol) or out.dtype != a.dtype:
+        raise RuntimeError("gemm_nt_rows: out has the wrong shape or dtype")
+    if residual is not None:
+        _rowmajor(residual, "residual")
+        if swiglu or tuple(residual.shape) != (M, Nn) or residual.dtype != a.dtype:
+            raise RuntimeError("gemm_nt_rows: residual must match out (and is not taken with swiglu)")
+    if gate is not None:
+        if gate.dtype not in (torch.bool, torch.uint8) or gate.numel() != M or not gate.is_contiguous():
+            raise RuntimeError("gemm_nt_rows: gate must be a contiguous bool/uint8 vector of length M")
+    epi = 1 if swiglu else 0
+    nbytes = N.lib().unok_gemm_nt_rows_workspace(M, Nn, K, R, epi, int(splits))
+    ws = torch.empty((nbytes + 3) // 4, device=a.device, dtype=torch.float32) if nbytes > 0 else None
+    N.call("unok_gemm_nt_rows", M, Nn, K, N.ptr(a), _ld(a), N.ptr(b), _ld(b),
+           N.ptr(lora_a), _ld(lora_a) if lora_a is not None else 0, R,
+           N.ptr(lora_b), _ld(lora_b) if lora_b is not None else 0, r,
+           len(seg_end), N.int_array(seg_end), N.int_array(seg_col),
+           N.ptr(out), _ld(out), N.ptr(residual), _ld(residual) if residual is not None else 0,
+           N.ptr(gate), epi, int(splits), N.ptr(ws), nbytes, N.stream())
     return out
 
 
@@ -260,7 +316,7 @@ def gemm_nt_swiglu(a: torch.Tensor, b_interleaved: torch.Tensor, *, a2: torch.Te
            N.ptr(out), _ld(out), N.ptr(gu), _ld(gu) if gu is not None else 0, N.stream())
     if rec is not None:
         ev1.record()
-        rec.records.append((ev0, ev1, 2.0 * M * rows * (K + K2)))
+        rec.records.append((ev0, ev1, 2.0 * M * rows * (K + K2), (M, rows, K, K2)))
     return out
 
 
@@ -294,7 +350,7 @@ def gemm_nt_swiglu_bwd(a: torch.Tensor, b: torch.Tensor, a2: torch.Tensor | None
            N.ptr(dgu), _ld(dgu), N.stream())
     if rec is not None:
         ev1.record()
-        rec.records.append((ev0, ev1, 2.0 * M * F * (K + K2)))
+        rec.records.append((ev0, ev1, 2.0 * M * F * (K + K2), (M, F, K, K2)))
     return dgu
 
 
