@@ -79,7 +79,8 @@ int unok_gemm_nt_swiglu_bwd(int M, int F, int K, const void* A, int64_t lda, con
  * least unok_gemm_nt_rows_workspace() bytes, 16-byte aligned) and a second kernel adds them in
  * range order (the result does not depend on timing), forms H and applies the rank-r update and
  * the epilogue. One range without LoRA and epilogue 0 writes C directly and needs no workspace.
- * K a multiple of 128, N of 4 (of 8 for epilogue 1), R of 4 (at most 512), r of 8 (at most 128).
+ * K a multiple of 128, N of 4 (of 32 for epilogue 1), R and r of 8 (R at most 512, r at most 128),
+ * segment ends (but the last) of 16 and segment columns of 8.
  * Replaces: the LoRA linear of the draft forward, nano_vllm_uno/layers/linear.py:241-307 (base
  * projection plus lora_B(lora_A(x) * lora_mask) * scaling, the mask off on the seed row), called
  * from engine/two_pass_decoding.py:273-283, and the MLP activation that follows gate_up_proj
@@ -166,6 +167,33 @@ int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D, const void
                   const float* LSE, const void* dO, int64_t lddo, float* Dsum,
                   void* dQ, int64_t lddq, void* dK, int64_t lddk, void* dV, int64_t lddv,
                   float scale, void* stream);
+
+/* ---- Draft-block attention over the KV cache -------------------------------------------------- */
+
+/* q/k RMSNorm + RoPE of a draft block's fused qkv rows [B*L, (nq + 2 nk) * D] (the arithmetic of
+ * unok_qknorm_rope_fwd; wq / wk null: no q/k norm), at positions lengths[b] + t; the block's K and V
+ * rows into this layer's caches kc / vc [B, nk, max_len, D] at rows lengths[b] + t (rows at or past
+ * max_len are not written); the queries into qd [B * nk * 128, D]: the rep = nq / nk q heads of
+ * K/V head kv and sequence b fill rows 128 (b nk + kv) + L (h % rep) + t, the other rows of each
+ * 128 are zeroed. bf16, D in {64, 128}, rep * L <= 128. Replaces: the q/k norm and rotary embedding
+ * of Qwen3Attention.forward (nano_vllm_uno/models/qwen3.py:81-99) and the KV-cache store of
+ * nano_vllm_uno/layers/attention.py:628-668 (BLOCK_DECODE). */
+int unok_decode_prep(int B, int L, int nq, int nk, int D, const void* qkv, int64_t ld, const void* wq,
+                     const void* wk, const int64_t* lengths, const float* inv_freq, float eps, void* kc,
+                     void* vc, int max_len, void* qd, void* stream);
+/* Split-key attention of draft blocks: S * QR rows, row i attending with query Q[i % QR] (one
+ * head) to K / V rows over its interval iv[i] (int32[8], keys [iv[0], iv[1])), O and LSE per row
+ * as unok_attn_fwd. The S rows of one query cover disjoint ranges of its cache keys, so the grid
+ * holds S workgroups per (sequence, K/V head) pair. Replaces: the causal flash attention over the
+ * cache of nano_vllm_uno/layers/attention.py:658-666 (flash_attn_with_kvcache, causal=True). */
+int unok_attn_fwd_split(int QR, int S, int D, const void* Q, int64_t ldq, const void* K, int64_t ldk,
+                        const void* V, int64_t ldv, const int32_t* iv, void* O, int64_t ldo, float* LSE,
+                        float scale, void* stream);
+/* out[dst[i]] (rows of D) = merge of the S partial rows s * QR + i of unok_attn_fwd_split by their
+ * log-sum-exp weights (rows with dst[i] < 0 are skipped). The split-key combine inside the flash
+ * attention that nano_vllm_uno/layers/attention.py:658-666 calls. */
+int unok_attn_split_combine(int QR, int S, int D, const void* opart, int64_t ldp, const float* lse,
+                            const int32_t* dst, void* out, int64_t ldo, void* stream);
 
 /* ---- Block-diffusion batch preparation ----------------------------------------------------- */
 

@@ -129,3 +129,89 @@ def test_rows_rejects_bad_shapes(dev):
     lb = torch.randn(64, 16, device=dev).bfloat16()
     with pytest.raises(ValueError, match="LoRA hidden columns"):
         K.gemm_nt_rows(a, w, lora_a=la, lora_b=lb, segments=[(32, 0), (64, 8)])
+
+
+def _bf16_close(a, b):
+    """Elementwise within one bf16 rounding step of the reference value."""
+    a, b = a.float(), b.float()
+    return bool(((a - b).abs() <= b.abs() * 2.0 ** -7 + 1e-6).all())
+
+
+@pytest.mark.parametrize("D,nq,nk,L,norm", [(128, 8, 2, 16, True), (64, 4, 2, 8, True), (128, 4, 1, 32, False)])
+def test_decode_prep_matches_training_kernels(dev, D, nq, nk, L, norm):
+    """unok_decode_prep against unok_qknorm_rope_fwd at the same positions (lengths_b + t) plus the
+    cache-store and query-layout row copies: K / V rows land at the committed lengths, the queries
+    at row 128 (b nk + kv) + L (h % rep) + t, the other rows of each 128 are zeroed and no other
+    cache row is written."""
+    print(f"[decode prep] D={D} nq={nq} nk={nk} L={L} norm={norm}", flush=True)
+    torch.manual_seed(D + L)
+    B, max_len, rep = 3, 96, nq // nk
+    lengths = torch.tensor([5, 17, 96 - L], device=dev, dtype=torch.int64)
+    M = B * L
+    qkv = torch.randn(M, (nq + 2 * nk) * D, device=dev).bfloat16()
+    wq = (torch.rand(D, device=dev) + 0.5).bfloat16() if norm else None
+    wk = (torch.rand(D, device=dev) + 0.5).bfloat16() if norm else None
+    inv_freq = 1.0 / (1e6 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    kc = torch.zeros(B, nk, max_len, D, device=dev, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    qd = torch.full((B * nk * 128, D), 7.0, device=dev, dtype=torch.bfloat16)
+    K.decode_prep(qkv, wq, wk, lengths, inv_freq, 1e-6, kc, vc, qd, B, L, nq, nk, D)
+    pos = (lengths[:, None] + torch.arange(L, device=dev)[None]).reshape(-1).contiguous()
+    q, k, _ = K.qknorm_rope_fwd(qkv, nq, nk, D, wq, wk, pos, inv_freq, 1e-6)
+    v = qkv[:, (nq + nk) * D:]
+    torch.cuda.synchronize()
+    q = q.view(B, L, nq, D)
+    k = k.view(B, L, nk, D)
+    v = v.reshape(B, L, nk, D)
+    written = torch.zeros(B, nk, max_len, dtype=torch.bool)
+    for b in range(B):
+        n = int(lengths[b])
+        assert _bf16_close(kc[b, :, n:n + L].transpose(0, 1), k[b]), b
+        assert torch.equal(vc[b, :, n:n + L].transpose(0, 1), v[b]), b
+        written[b, :, n:n + L] = True
+        for kv in range(nk):
+            blk = qd[(b * nk + kv) * 128:(b * nk + kv + 1) * 128]
+            for rr in range(rep):
+                assert _bf16_close(blk[rr * L:(rr + 1) * L], q[b, :, kv * rep + rr]), (b, kv, rr)
+            assert not blk[rep * L:].any()
+    assert not kc.cpu()[~written].any() and not vc.cpu()[~written].any()
+
+
+def test_attn_split_matches_unsplit(dev):
+    """Split-key attention plus the log-sum-exp merge against the single-range kernel over the same
+    causal cache prefix, including a sequence shorter than the number of ranges (ranges without
+    keys) and padding rows, which the merge skips."""
+    torch.manual_seed(11)
+    D, L, rep, S, max_len = 128, 16, 2, 4, 160
+    lengths = [3, 40, 137]
+    pairs = len(lengths)
+    QR = pairs * 128
+    kc = torch.randn(pairs * max_len, D, device=dev).bfloat16()
+    vc = torch.randn(pairs * max_len, D, device=dev).bfloat16()
+    qd = torch.randn(QR, D, device=dev).bfloat16()
+    iv = torch.zeros(QR, 8, dtype=torch.int32)
+    ivs = torch.zeros(S * QR, 8, dtype=torch.int32)
+    dst = torch.full((QR,), -1, dtype=torch.int32)
+    for p, n in enumerate(lengths):
+        start = p * max_len
+        c = n // S
+        for slot in range(128):
+            row = p * 128 + slot
+            if slot >= rep * L:
+                continue
+            t = slot % L
+            seen = n + t + 1
+            iv[row, 0], iv[row, 1] = start, start + seen
+            dst[row] = row
+            for s in range(S):
+                lo = s * c
+                hi = seen if s == S - 1 else min((s + 1) * c, seen)
+                ivs[s * QR + row, 0], ivs[s * QR + row, 1] = start + lo, start + max(hi, lo)
+    ref, _ = K.attn_fwd(qd, kc, vc, iv.to(dev), 1, 1, D)
+    od, lse = K.attn_fwd_split(qd, kc, vc, ivs.to(dev), QR, S, D)
+    out = torch.zeros(QR, D, device=dev, dtype=torch.bfloat16)
+    K.attn_split_combine(od, lse, dst.to(dev), QR, S, D, out)
+    torch.cuda.synchronize()
+    valid = (dst >= 0).to(dev)
+    assert _rel(out[valid], ref[valid]) < 1e-2
+    assert not out[~valid].any()

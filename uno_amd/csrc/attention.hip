@@ -37,6 +37,7 @@ struct AttnArgs {
   void* dK; int64_t lddk;              // [Mk2, Hkv*D]
   void* dV; int64_t lddv;
   int Mq, Mk2, Hq, Hkv;
+  int q_mod;                           // > 0: query row i reads Q row i % q_mod (split-key decode)
   float scale;                         // d^-0.5
   float scale_log2;                    // d^-0.5 * log2(e)
 };
@@ -146,9 +147,10 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
     qrow[qg] = qt * BQ + w * (32 * QG) + qg * 32 + lq;
     qvalid[qg] = qrow[qg] < p.Mq;
     ivq[qg] = qvalid[qg] ? *(const int4*)(p.iv + (int64_t)qrow[qg] * 8) : make_int4(0, 0, 0, 0);
+    const int qsrc = p.q_mod > 0 ? qrow[qg] % p.q_mod : qrow[qg];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
-      qreg[qg][ks] = qvalid[qg] ? ld_bf16x8(Q + (int64_t)qrow[qg] * p.ldq + h * D + ks * 16 + g * 8)
+      qreg[qg][ks] = qvalid[qg] ? ld_bf16x8(Q + (int64_t)qsrc * p.ldq + h * D + ks * 16 + g * 8)
                                 : __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
   }
 
@@ -918,6 +920,31 @@ UNOK_EXPORT int unok_attn_fwd(int dtype, int Mq, int Hq, int Hkv, int D, const v
     else launch_fwd<64>(Mq, Hq, st, a);
   }
   return unok::check_launch("attn_fwd");
+}
+
+// Split-key forward of decode and draft blocks: S * QR query rows, row i reading query Q[i % QR]
+// against one K/V head over its own key interval (the split's share of the cache), with O and
+// LSE per row; unok_attn_split_combine merges the S partial rows of each query.
+UNOK_EXPORT int unok_attn_fwd_split(int QR, int S, int D, const void* Q, int64_t ldq, const void* K, int64_t ldk,
+                                    const void* V, int64_t ldv, const int32_t* iv, void* O, int64_t ldo, float* LSE,
+                                    float scale, void* stream) {
+  UNOK_REQUIRE(QR >= 0 && S >= 1, UNOK_EINVAL, "attn_fwd_split: QR=%d S=%d", QR, S);
+  if (QR == 0) return 0;
+  UNOK_REQUIRE((int64_t)QR * S < (1ll << 31), UNOK_EINVAL, "attn_fwd_split: too many rows");
+  int rc = check_geom(UNOK_BF16, D, 1, 1);
+  if (rc) return rc;
+  UNOK_REQUIRE(al16(Q) && al16(K) && al16(V) && al16(O) && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 &&
+                   ldo % 8 == 0,
+               UNOK_EALIGN, "attn_fwd_split: operands must be 16-byte aligned with strides multiple of 8");
+  AttnArgs a{};
+  a.Q = Q; a.ldq = ldq; a.K1 = K; a.ldk1 = ldk; a.V1 = V; a.ldv1 = ldv;
+  a.iv = iv; a.O = O; a.ldo = ldo; a.LSE = LSE;
+  a.Mq = QR * S; a.Hq = 1; a.Hkv = 1; a.q_mod = QR;
+  a.scale = scale; a.scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 128) launch_fwd<128>(a.Mq, 1, st, a);
+  else launch_fwd<64>(a.Mq, 1, st, a);
+  return unok::check_launch("attn_fwd_split");
 }
 
 // Backward. Computes Dsum into the caller's [Mq,Hq] fp32 buffer, dQ for every query, and,

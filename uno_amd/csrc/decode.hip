@@ -180,17 +180,20 @@ __global__ __launch_bounds__(RB_W * 64) void gemm_nt_rows_kernel(const RowsGemm 
 
 // ---------------------------------------------------------------------------------------
 // Reduction with the rank-r LoRA update and the epilogue. Workgroup tile: 16 rows x 128 product
-// columns (EPI 0) or 16 rows x 64 SwiGLU features, i.e. the 64 gate and the 64 matching up columns
-// (EPI 1). It first forms h = bf16(m (.) sum of the LoRA-column partials) for its rows (all R
-// columns) and stages its columns' (s B) rows in LDS, then every thread adds the partials of 4
-// columns (and 4 up columns) of its rows in range order, adds h[:, seg] . (s B)[col] in fp32, the
-// residual, and rounds:
-// EPI 0: C[M, N]   = bf16(sum + h . sB + Res);
+// columns ("slots"; EPI 0) or 16 rows x 64 SwiGLU features, i.e. the 64 gate and the 64 matching up
+// columns (EPI 1).
+//   1. h = bf16(m (.) sum of the LoRA-column partials) for the tile's rows (all R columns) into
+//      LDS, and the slots' (s B) rows into LDS;
+//   2. the rank-r update u[row, slot] = h[row, seg(slot) + :r] . (s B)[slot, :r] with 16x16x32
+//      MFMAs (each wave two 16-slot tiles), fp32 into LDS;
+//   3. every thread adds the partials of 4 columns (and 4 up columns) of its rows in range order,
+//      then u, the residual, and rounds:
+// EPI 0: C[M, N]   = bf16(sum + u + Res);
 // EPI 1: C[M, N/2] = bf16(bf16(silu(g)) * u), g = bf16(gate column value), u = bf16(up column value)
 //        (the [gate | up] product rounded to bf16 and then the SwiGLU of unok_swiglu_fwd).
-// The partial sums of one value are loaded eight ranges at a time and added in range order.
+// Segment boundaries are multiples of 16, so each 16-slot tile reads one segment of h.
 // ---------------------------------------------------------------------------------------
-constexpr int RR_ROWS = 16, RR_SLOTS = 128;
+constexpr int RR_ROWS = 16, RR_SLOTS = 128, RR_ULD = RR_SLOTS + 4;
 
 struct RowsReduce {
   const float* ws; int64_t ldw; int splits;
@@ -210,20 +213,7 @@ __device__ __forceinline__ int red_seg_col(const RowsReduce& p, int n) {
   return c;
 }
 
-// sum over k < splits of src[k * plane], added in k order, eight loads in flight
-template <typename T>
-__device__ __forceinline__ T ordered_sum(const T* src, int64_t plane, int splits) {
-  T s{};
-  for (int k0 = 0; k0 < splits; k0 += 8) {
-    T v[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) v[q] = k0 + q < splits ? src[(k0 + q) * plane] : T{};
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (k0 + q < splits) s += v[q];
-  }
-  return s;
-}
+__device__ __forceinline__ int round32(int x) { return (x + 31) & ~31; }
 
 template <int EPI>
 __global__ __launch_bounds__(256) void rows_reduce_kernel(const RowsReduce p) {
@@ -231,17 +221,20 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(const RowsReduce p) {
   constexpr int NG = RR_SLOTS / (4 * NH);          // column groups of 4 per workgroup row: 32 / 16
   constexpr int RPT = RR_ROWS * NG / 256;          // rows per thread: 2 (EPI 0) or 1 (EPI 1)
   extern __shared__ __attribute__((aligned(16))) float rsm[];
-  const int rld = p.r + 8;                         // bf16 row stride of the staged (s B) rows
-  float* Hs = rsm;                                 // [RR_ROWS][R] fp32 (bf16-rounded values)
-  bf16_t* Ls = (bf16_t*)(rsm + RR_ROWS * p.R);     // [RR_SLOTS][rld]
+  const bool lora = p.LB != nullptr;
+  const int rp = round32(p.r);
+  const int hld = p.R + 32;                        // bf16 row stride of h (zero tail read by the last steps)
+  const int rld = rp + 8;                          // bf16 row stride of the staged (s B) rows
+  float* Us = rsm;                                                   // [RR_ROWS][RR_ULD] fp32
+  bf16_t* Hs = (bf16_t*)(rsm + RR_ROWS * RR_ULD);                    // [RR_ROWS][hld]
+  bf16_t* Ls = Hs + RR_ROWS * hld;                                   // [RR_SLOTS][rld]
 
   const int nout = EPI == 1 ? p.N / 2 : p.N;
   const int ctiles = (nout + NG * 4 - 1) / (NG * 4);
   const int r0 = (blockIdx.x / ctiles) * RR_ROWS;
   const int c0 = (blockIdx.x % ctiles) * NG * 4;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t plane = (int64_t)p.M * p.ldw;
-  const bool lora = p.LB != nullptr;
 
   // product column of slot q of this tile: EPI 0: c0 + q; EPI 1: gate c0 + q for q < 64, up
   // N/2 + c0 + q - 64 above
@@ -250,13 +243,40 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(const RowsReduce p) {
     else return c0 + q;
   };
   if (lora) {
-    for (int i = tid; i < RR_ROWS * p.R; i += 256) {
-      const int rr = i / p.R, j = i % p.R;
-      const int row = min(r0 + rr, p.M - 1);
-      const float s = ordered_sum(p.ws + (int64_t)row * p.ldw + p.N + j, plane, p.splits);
-      const bool on = p.gate == nullptr || p.gate[row] != 0;
-      Hs[i] = on ? Elem<bf16_t>::round(s) : 0.f;
+    // h: four (row, column) items per thread at a time, each with up to eight ranges' loads in flight
+    const int items = RR_ROWS * p.R;
+    for (int i0 = tid; i0 < items; i0 += 4 * 256) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      const float* src[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = min(i0 + u * 256, items - 1);
+        const int row = min(r0 + i / p.R, p.M - 1);
+        src[u] = p.ws + (int64_t)row * p.ldw + p.N + i % p.R;
+      }
+      for (int k0 = 0; k0 < p.splits; k0 += 8) {
+        float v[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int q = 0; q < 8; ++q) v[u][q] = k0 + q < p.splits ? src[u][(k0 + q) * plane] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (k0 + q < p.splits) acc[u] += v[u][q];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * 256;
+        if (i >= items) break;
+        const int rr = i / p.R, j = i % p.R;
+        const int row = min(r0 + rr, p.M - 1);
+        const bool on = p.gate == nullptr || p.gate[row] != 0;
+        Hs[rr * hld + j] = on ? f32_to_bf16(acc[u]) : (bf16_t)0;
+      }
     }
+    for (int i = tid; i < RR_ROWS * 32; i += 256) Hs[(i / 32) * hld + p.R + i % 32] = 0;
     const int vec = p.r / 8;
     for (int i = tid; i < RR_SLOTS * vec; i += 256) {
       const int q = i / vec, v = i % vec;
@@ -264,51 +284,65 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(const RowsReduce p) {
       *(uint4*)(Ls + q * rld + v * 8) = *(const uint4*)(p.LB + (int64_t)colq * p.ldlb + v * 8);
     }
     __syncthreads();
+    // rank-r update on MFMA: wave w takes slot tiles 2 w and 2 w + 1; lane l supplies (s B) of slot
+    // l % 16 and h of row l % 16 at k = 32 kk + 8 (l / 16) + [0, 8); the result of slot
+    // 4 (l / 16) + e, row l % 16 is D element e of lane l
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int s0 = (wid * 2 + tt) * 16;
+      const int hc = red_seg_col(p, slot_col(s0));
+      f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+      for (int kk = 0; kk < rp; kk += 32) {
+        const int k = kk + 8 * (lane >> 4);
+        bf16x8_t lb = *(const bf16x8_t*)(Ls + (s0 + (lane & 15)) * rld + k);
+        if (k >= p.r) lb = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
+        const bf16x8_t hv = *(const bf16x8_t*)(Hs + (lane & 15) * hld + hc + k);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lb, hv, d, 0, 0, 0);
+      }
+      *(f32x4_t*)(Us + (lane & 15) * RR_ULD + s0 + 4 * (lane >> 4)) = d;
+    }
+    __syncthreads();
   }
 
   const int cg = tid % NG, rg = tid / NG;
   const int cbase = c0 + cg * 4;
   if (cbase >= nout) return;
+  // partial sums: all rows and column groups of this thread, up to eight ranges in flight each,
+  // added in range order
   float4 acc[RPT][NH];
+  const float4* src[RPT][NH];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int row = min(r0 + rg * RPT + i, p.M - 1);
 #pragma unroll
-    for (int h = 0; h < NH; ++h)
-      acc[i][h] = ordered_sum((const float4*)(p.ws + (int64_t)row * p.ldw + cbase + h * nout), plane / 4, p.splits);
+    for (int h = 0; h < NH; ++h) {
+      acc[i][h] = make_float4(0.f, 0.f, 0.f, 0.f);
+      src[i][h] = (const float4*)(p.ws + (int64_t)row * p.ldw + cbase + h * nout);
+    }
   }
-  // rank-r update: h[row, seg(col) + j] * (s B)[col, j]
+  const int64_t plane4 = plane / 4;
+  for (int k0 = 0; k0 < p.splits; k0 += 8) {
+    float4 v[RPT][NH][8];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          v[i][h][q] = k0 + q < p.splits ? src[i][h][(k0 + q) * plane4] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (k0 + q < p.splits) acc[i][h] += v[i][h][q];
+  }
   if (lora) {
 #pragma unroll
-    for (int h = 0; h < NH; ++h) {
-      const int q0 = h * NG * 4 + cg * 4;            // slot of this thread's first column in group h
-      const int hc = red_seg_col(p, slot_col(q0));   // four columns share one segment
-      for (int j = 0; j < p.r; j += 8) {
-        float lb[4][8];
+    for (int i = 0; i < RPT; ++i)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint4 u = *(const uint4*)(Ls + (q0 + c) * rld + j);
-          const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            lb[c][2 * e] = __uint_as_float(w[e] << 16);
-            lb[c][2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < RPT; ++i) {
-          const float* hrow = Hs + (rg * RPT + i) * p.R + hc + j;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float hv = hrow[e];
-            acc[i][h].x += hv * lb[0][e];
-            acc[i][h].y += hv * lb[1][e];
-            acc[i][h].z += hv * lb[2][e];
-            acc[i][h].w += hv * lb[3][e];
-          }
-        }
-      }
-    }
+      for (int h = 0; h < NH; ++h) acc[i][h] += *(const float4*)(Us + (rg * RPT + i) * RR_ULD + h * NG * 4 + cg * 4);
   }
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
@@ -360,7 +394,141 @@ int rows_auto_splits(int M, int N, int R, int nk, bool need_ws) {
 bool rows_needs_ws(int epilogue, int R, int splits) { return splits > 1 || epilogue != 0 || R > 0; }
 
 size_t rows_reduce_lds(int R, int r) {
-  return R > 0 ? (size_t)RR_ROWS * R * sizeof(float) + (size_t)RR_SLOTS * (r + 8) * sizeof(bf16_t) : 0;
+  if (R == 0) return 0;
+  const int rp = (r + 31) & ~31;
+  return (size_t)RR_ROWS * RR_ULD * sizeof(float) + (size_t)RR_ROWS * (R + 32) * sizeof(bf16_t) +
+         (size_t)RR_SLOTS * (rp + 8) * sizeof(bf16_t);
+}
+
+// ---------------------------------------------------------------------------------------
+// Attention of a draft block over the KV cache, in three kernels per layer:
+//   prep     q/k RMSNorm + RoPE of the fused qkv rows (the arithmetic of unok_qknorm_rope_fwd),
+//            the block's K and V rows into the caches at (b, kv head, length_b + t), and the
+//            queries into the decode layout: the queries of one (sequence, K/V head) pair, rep q
+//            heads x L rows, are the first rep * L of 128 rows (row 128 pair + L (h % rep) + t),
+//            the rest zero;
+//   attn     unok_attn_fwd_split over S key ranges of each pair's cache rows;
+//   combine  the S partial rows of each query merged by their log-sum-exp weights and written to
+//            the attention output [B * L, nq * D] at (b * L + t, head h).
+// ---------------------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void decode_prep_kernel(const bf16_t* __restrict__ qkv, int64_t ld,
+                                                          const bf16_t* __restrict__ wq, const bf16_t* __restrict__ wk,
+                                                          const int64_t* __restrict__ lengths,
+                                                          const float* __restrict__ inv_freq, float eps,
+                                                          bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
+                                                          int max_len, bf16_t* __restrict__ qd, int B, int L, int nq,
+                                                          int nk) {
+  constexpr int LPH = D / 8, HALF = D / 2;          // lanes per head row, 8 elements per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPH;
+  const int sub = lane % LPH, c0 = sub * 8;
+  const int M = B * L, nh = nq + 2 * nk, rep = nq / nk;
+  const int64_t heads = (int64_t)M * nh;
+  const int pad = 128 - rep * L;
+  if (item >= heads) {
+    // zero padding rows of the decode query layout
+    const int64_t z = item - heads;
+    if (z >= (int64_t)B * nk * pad) return;
+    const int64_t row = (z / pad) * 128 + rep * L + z % pad;
+    *(uint4*)(qd + row * D + c0) = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  const int m = (int)(item / nh), hd = (int)(item % nh);
+  const int b = m / L, t = m % L;
+  const int64_t len = lengths[b];
+  float x[8];
+  {
+    const uint4 u = *(const uint4*)(qkv + (int64_t)m * ld + (int64_t)hd * D + c0);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { x[2 * i] = __uint_as_float(w[i] << 16); x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u); }
+  }
+  bf16_t* dst;
+  if (hd < nq + nk) {
+    const bool isq = hd < nq;
+    const bf16_t* wn = isq ? wq : wk;
+    if (wn != nullptr) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+      for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      const float r = rsqrtf(ss / (float)D + eps);
+      const uint4 u = *(const uint4*)(wn + c0);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float w0 = __uint_as_float(w[i] << 16), w1 = __uint_as_float(w[i] & 0xffff0000u);
+        x[2 * i] = Elem<bf16_t>::round(Elem<bf16_t>::round(x[2 * i] * r) * w0);
+        x[2 * i + 1] = Elem<bf16_t>::round(Elem<bf16_t>::round(x[2 * i + 1] * r) * w1);
+      }
+    }
+    const float p = (float)(len + t);
+    const int j0 = c0 % HALF;
+    const float sgn = c0 < HALF ? -1.f : 1.f;
+    float out[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float sv, cv;
+      sincosf(p * inv_freq[j0 + e], &sv, &cv);
+      const float y = __shfl_xor(x[e], LPH / 2, 64);   // partner element i +- d/2
+      out[e] = x[e] * cv + sgn * y * sv;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = out[e];
+    if (isq) {
+      const int kv = hd / rep, rr = hd % rep;
+      dst = qd + ((int64_t)(b * nk + kv) * 128 + rr * L + t) * D;
+    } else {
+      if (len + t >= max_len) return;
+      dst = kc + ((int64_t)(b * nk + hd - nq) * max_len + len + t) * D;
+    }
+  } else {
+    if (len + t >= max_len) return;
+    dst = vc + ((int64_t)(b * nk + hd - nq - nk) * max_len + len + t) * D;
+  }
+  *(uint4*)(dst + c0) = make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]),
+                                   pack2_bf16(x[6], x[7]));
+}
+
+// O[dst[i]] = sum_s 2^(lse_s - m) O_s[i] / sum_s 2^(lse_s - m) over the S partial rows s * QR + i
+// (lse in log2 units, m their maximum; a range without keys has lse = -inf and weight 0); rows
+// with dst[i] < 0 are skipped.
+template <int D>
+__global__ __launch_bounds__(256) void attn_split_combine_kernel(const bf16_t* __restrict__ op, int64_t ldp,
+                                                                 const float* __restrict__ lse,
+                                                                 const int32_t* __restrict__ dst, int QR, int S,
+                                                                 bf16_t* __restrict__ out, int64_t ldo) {
+  constexpr int LPR = D / 8;
+  const int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
+  if (item >= QR) return;
+  const int i = (int)item, c0 = (threadIdx.x % LPR) * 8;
+  const int d = dst[i];
+  if (d < 0) return;
+  float m = -INFINITY;
+  for (int s = 0; s < S; ++s) m = fmaxf(m, lse[(int64_t)s * QR + i]);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.f;
+  if (m != -INFINITY) {
+    for (int s = 0; s < S; ++s) {
+      const float l = lse[(int64_t)s * QR + i];
+      if (l == -INFINITY) continue;
+      const float w = exp2f(l - m);
+      wsum += w;
+      const uint4 u = *(const uint4*)(op + ((int64_t)s * QR + i) * ldp + c0);
+      const uint32_t v[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc[2 * k] += w * __uint_as_float(v[k] << 16);
+        acc[2 * k + 1] += w * __uint_as_float(v[k] & 0xffff0000u);
+      }
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  *(uint4*)(out + (int64_t)d * ldo + c0) =
+      make_uint4(pack2_bf16(acc[0] * inv, acc[1] * inv), pack2_bf16(acc[2] * inv, acc[3] * inv),
+                 pack2_bf16(acc[4] * inv, acc[5] * inv), pack2_bf16(acc[6] * inv, acc[7] * inv));
 }
 
 }  // namespace
@@ -389,7 +557,8 @@ UNOK_EXPORT int unok_gemm_nt_rows(int M, int N, int K, const void* A, int64_t ld
                (long long)ldb);
   UNOK_REQUIRE(N % 4 == 0 && ldc % 4 == 0 && ((uintptr_t)C & 7) == 0, UNOK_EALIGN,
                "gemm_nt_rows: N=%d and ldc=%lld must be multiples of 4 and C 8-byte aligned", N, (long long)ldc);
-  UNOK_REQUIRE(epilogue == 0 || N % 8 == 0, UNOK_EINVAL, "gemm_nt_rows: the SwiGLU epilogue needs N=%d a multiple of 8", N);
+  UNOK_REQUIRE(epilogue == 0 || N % 32 == 0, UNOK_EINVAL, "gemm_nt_rows: the SwiGLU epilogue needs N=%d a multiple of 32",
+               N);
   UNOK_REQUIRE(epilogue == 0 || Res == nullptr, UNOK_EINVAL, "gemm_nt_rows: the SwiGLU epilogue takes no residual");
   UNOK_REQUIRE(Res == nullptr || (ldres % 4 == 0 && ((uintptr_t)Res & 7) == 0), UNOK_EALIGN,
                "gemm_nt_rows: ldres=%lld must be a multiple of 4 and Res 8-byte aligned", (long long)ldres);
@@ -398,8 +567,8 @@ UNOK_EXPORT int unok_gemm_nt_rows(int M, int N, int K, const void* A, int64_t ld
   q.nseg = 1;
   for (int i = 0; i < 4; ++i) { q.seg_end[i] = N; q.seg_col[i] = 0; }
   if (lora) {
-    UNOK_REQUIRE(R > 0 && R <= 512 && R % 4 == 0 && LB != nullptr && r > 0 && r <= 128 && r % 8 == 0, UNOK_EINVAL,
-                 "gemm_nt_rows: LoRA needs 0 < R <= 512 A rows (a multiple of 4) and a rank 0 < r <= 128 "
+    UNOK_REQUIRE(R > 0 && R <= 512 && R % 8 == 0 && LB != nullptr && r > 0 && r <= 128 && r % 8 == 0, UNOK_EINVAL,
+                 "gemm_nt_rows: LoRA needs 0 < R <= 512 A rows (a multiple of 8) and a rank 0 < r <= 128 "
                  "(a multiple of 8), got R=%d r=%d", R, r);
     UNOK_REQUIRE(ldla % 8 == 0 && ((uintptr_t)LA & 15) == 0 && ldlb % 8 == 0 && ((uintptr_t)LB & 15) == 0,
                  UNOK_EALIGN, "gemm_nt_rows: ldla=%lld ldlb=%lld must be multiples of 8 and LA/LB 16-byte aligned",
@@ -410,11 +579,11 @@ UNOK_EXPORT int unok_gemm_nt_rows(int M, int N, int K, const void* A, int64_t ld
       for (int i = 0; i < nseg; ++i) {
         q.seg_end[i] = seg_end[i];
         q.seg_col[i] = seg_col[i];
-        UNOK_REQUIRE(seg_col[i] >= 0 && seg_col[i] + r <= R, UNOK_EINVAL,
-                     "gemm_nt_rows: segment %d reads LoRA hidden columns %d..%d of %d", i, seg_col[i],
+        UNOK_REQUIRE(seg_col[i] >= 0 && seg_col[i] % 8 == 0 && seg_col[i] + r <= R, UNOK_EINVAL,
+                     "gemm_nt_rows: segment %d reads LoRA hidden columns %d..%d of %d (start a multiple of 8)", i, seg_col[i],
                      seg_col[i] + r, R);
-        UNOK_REQUIRE(i + 1 == nseg || seg_end[i] % 4 == 0, UNOK_EINVAL,
-                     "gemm_nt_rows: segment end %d not a multiple of 4", seg_end[i]);
+        UNOK_REQUIRE(i + 1 == nseg || seg_end[i] % 16 == 0, UNOK_EINVAL,
+                     "gemm_nt_rows: segment end %d not a multiple of 16", seg_end[i]);
       }
       UNOK_REQUIRE(seg_end[nseg - 1] == N, UNOK_EINVAL, "gemm_nt_rows: last segment must end at N");
     } else {
@@ -472,4 +641,54 @@ UNOK_EXPORT int unok_gemm_nt_rows(int M, int N, int K, const void* A, int64_t ld
     hipLaunchKernelGGL((rows_reduce_kernel<1>), dim3((unsigned)blocks), dim3(256), rlds, st, q);
   }
   return unok::check_launch("gemm_nt_rows_reduce");
+}
+
+// q/k norm + RoPE of a draft block's fused qkv rows, its K/V rows into the caches and its queries
+// into the decode layout (see decode_prep_kernel). bf16; D in {64, 128}; wq / wk null: no q/k norm.
+UNOK_EXPORT int unok_decode_prep(int B, int L, int nq, int nk, int D, const void* qkv, int64_t ld, const void* wq,
+                                 const void* wk, const int64_t* lengths, const float* inv_freq, float eps, void* kc,
+                                 void* vc, int max_len, void* qd, void* stream) {
+  UNOK_REQUIRE(B >= 0 && L >= 0 && nq > 0 && nk > 0 && nq % nk == 0, UNOK_EINVAL,
+               "decode_prep: B=%d L=%d nq=%d nk=%d", B, L, nq, nk);
+  if (B == 0 || L == 0) return 0;
+  UNOK_REQUIRE(D == 64 || D == 128, UNOK_EINVAL, "decode_prep: head dim %d not in {64,128}", D);
+  UNOK_REQUIRE((nq / nk) * L <= 128, UNOK_EINVAL, "decode_prep: %d q heads x %d rows exceed 128 rows per K/V head",
+               nq / nk, L);
+  UNOK_REQUIRE(ld % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)kc & 15) == 0 && ((uintptr_t)vc & 15) == 0 &&
+                   ((uintptr_t)qd & 15) == 0 && (wq == nullptr || ((uintptr_t)wq & 15) == 0) &&
+                   (wk == nullptr || ((uintptr_t)wk & 15) == 0),
+               UNOK_EALIGN, "decode_prep: rows must be 16-byte aligned");
+  const int64_t heads = (int64_t)B * L * (nq + 2 * nk);
+  const int64_t pads = (int64_t)B * nk * (128 - (nq / nk) * L);
+  const int lph = D / 8;
+  const int64_t blocks = ((heads + pads) * lph + 255) / 256;
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 128)
+    hipLaunchKernelGGL((decode_prep_kernel<128>), dim3((unsigned)blocks), dim3(256), 0, st, (const bf16_t*)qkv, ld,
+                       (const bf16_t*)wq, (const bf16_t*)wk, lengths, inv_freq, eps, (bf16_t*)kc, (bf16_t*)vc, max_len,
+                       (bf16_t*)qd, B, L, nq, nk);
+  else
+    hipLaunchKernelGGL((decode_prep_kernel<64>), dim3((unsigned)blocks), dim3(256), 0, st, (const bf16_t*)qkv, ld,
+                       (const bf16_t*)wq, (const bf16_t*)wk, lengths, inv_freq, eps, (bf16_t*)kc, (bf16_t*)vc, max_len,
+                       (bf16_t*)qd, B, L, nq, nk);
+  return unok::check_launch("decode_prep");
+}
+
+// Merge of the S partial rows of split-key attention (see attn_split_combine_kernel). bf16.
+UNOK_EXPORT int unok_attn_split_combine(int QR, int S, int D, const void* opart, int64_t ldp, const float* lse,
+                                        const int32_t* dst, void* out, int64_t ldo, void* stream) {
+  UNOK_REQUIRE(QR >= 0 && S >= 1, UNOK_EINVAL, "attn_split_combine: QR=%d S=%d", QR, S);
+  if (QR == 0) return 0;
+  UNOK_REQUIRE(D == 64 || D == 128, UNOK_EINVAL, "attn_split_combine: head dim %d not in {64,128}", D);
+  UNOK_REQUIRE(ldp % 8 == 0 && ldo % 8 == 0 && ((uintptr_t)opart & 15) == 0 && ((uintptr_t)out & 15) == 0, UNOK_EALIGN,
+               "attn_split_combine: rows must be 16-byte aligned");
+  const int64_t blocks = ((int64_t)QR * (D / 8) + 255) / 256;
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 128)
+    hipLaunchKernelGGL((attn_split_combine_kernel<128>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const bf16_t*)opart, ldp, lse, dst, QR, S, (bf16_t*)out, ldo);
+  else
+    hipLaunchKernelGGL((attn_split_combine_kernel<64>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const bf16_t*)opart, ldp, lse, dst, QR, S, (bf16_t*)out, ldo);
+  return unok::check_launch("attn_split_combine");
 }

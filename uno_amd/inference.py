@@ -121,12 +121,42 @@ class BlockDecoder:
         g = self.geo
         dev = lengths.device
         i32 = dict(device=dev, dtype=torch.int32)
+        rep = g.nq // g.nk
+        out = {}
+        slot = torch.arange(128, device=dev)
+        pair = torch.arange(B * g.nk, device=dev)
+        valid = slot < rep * L
+        tt = slot % L
+        start = pair[:, None] * cache.max_len                                           # [pairs, 1]
+        lens = lengths[:, None].expand(B, g.nk).reshape(-1, 1)                          # [pairs, 1]
+        seen = lens + tt[None, :] + 1                                                   # causal over cache + block
+        if not prefill and self._split_path(dev, cache):
+            # split-key layout: S key ranges per (sequence, K/V head) pair; range s of a query row
+            # holds keys [s c, (s + 1) c) of its causal prefix (c = committed length // S), the last
+            # range the rest; padding rows get empty ranges
+            pairs = B * g.nk
+            S = max(1, min(8, 256 // pairs))
+            QR = pairs * 128
+            c = lens // S
+            s_idx = torch.arange(S, device=dev)[:, None, None]                          # [S, 1, 1]
+            lo = s_idx * c[None]                                                         # [S, pairs, 1]
+            hi = torch.where(s_idx == S - 1, seen[None], torch.minimum((s_idx + 1) * c[None], seen[None]))
+            hi = torch.maximum(hi, lo)
+            lo = torch.where(valid[None, None, :], lo, 0)
+            hi = torch.where(valid[None, None, :], hi, 0)
+            ivs = torch.zeros((S * QR, 8), **i32)
+            ivs[:, 0] = (start[None] + lo).reshape(-1)
+            ivs[:, 1] = (start[None] + hi).reshape(-1)
+            # decode row (pair b nk + kv, slot r L + t) -> output row (b L + t) nq + kv rep + r
+            dst = ((pair // g.nk)[:, None] * L + tt[None, :]) * g.nq + (pair % g.nk)[:, None] * rep + (slot // L)[None, :]
+            out["dst"] = torch.where(valid[None, :], dst, -1).reshape(-1).to(**i32)
+            out["ivs"], out["S"], out["QR"] = ivs, S, QR
+            return out
         b = torch.arange(B, device=dev)[:, None, None]
         t = torch.arange(L, device=dev)[None, :, None]
         kv = torch.arange(g.nk, device=dev)[None, None, :]
         # cache store: key row (b, t, head) of the block -> cache row (b, head, lengths_b + t)
-        store = ((b * g.nk + kv) * cache.max_len + lengths[:, None, None] + t).reshape(-1).to(**i32)
-        out = {"store": store}
+        out["store"] = ((b * g.nk + kv) * cache.max_len + lengths[:, None, None] + t).reshape(-1).to(**i32)
         if prefill:
             starts = (torch.arange(B, device=dev) * L)[:, None]
             iv = torch.zeros((B * L, 8), **i32)
@@ -134,24 +164,20 @@ class BlockDecoder:
             iv[:, 1] = (starts + torch.arange(1, L + 1, device=dev)[None, :]).reshape(-1)
             out["iv"] = iv
             return out
-        rep = g.nq // g.nk
         # decode layout: query (b, t, head h = kv * rep + r) -> row (b * nk + kv) * 128 + r * L + t
         r = torch.arange(rep, device=dev)
         qrow = ((b * g.nk + kv)[..., None] * 128 + r[None, None, None, :] * L + t[..., None])   # [B, L, nk, rep]
         out["qrow"] = qrow.reshape(-1).to(**i32)
-        rows = B * g.nk * 128
-        iv = torch.zeros((rows, 8), **i32)
-        slot = torch.arange(128, device=dev)
-        pair = torch.arange(B * g.nk, device=dev)
-        valid = slot < rep * L
-        tt = slot % L
-        start = pair[:, None] * cache.max_len                                           # [pairs, 1]
-        seen = lengths[:, None].expand(B, g.nk).reshape(-1, 1) + tt[None, :] + 1        # causal over cache + block
+        iv = torch.zeros((B * g.nk * 128, 8), **i32)
         # rows past rep * L are padding: they see the pair's first key and their output is dropped
         iv[:, 0] = start.expand(-1, 128).reshape(-1)
         iv[:, 1] = torch.where(valid[None, :], start + seen, start + 1).reshape(-1)
         out["iv"] = iv
         return out
+
+    def _split_path(self, dev, cache) -> bool:
+        """bf16 draft blocks run the attention as prep + split-key attention + combine."""
+        return cache.k[0].dtype == torch.bfloat16 and self.geo.d in (64, 128)
 
     def _rows_path(self, M: int, dtype, prefill: bool) -> bool:
         """Draft blocks in bf16 take the few-row products (K ranges over the whole chip) when every
@@ -179,10 +205,20 @@ class BlockDecoder:
 
         x1, _ = K.rmsnorm_fwd(h0, lw.ln_in, g.eps)
         qkv = linear(x1, lw.w_qkv, "qkv", qkv_segments)
-        q, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, pos, self.decoder.inv_freq, g.eps)
-        v = qkv[:, k_end:]
         ck = cache.k[li].view(-1, g.d)
         cv = cache.v[li].view(-1, g.d)
+        if not prefill and "ivs" in maps:
+            # q/k norm + RoPE, cache store and query layout in one kernel; split-key attention; merge
+            S, QR = maps["S"], maps["QR"]
+            qd = torch.empty((QR, g.d), device=qkv.device, dtype=qkv.dtype)
+            K.decode_prep(qkv, lw.q_norm, lw.k_norm, cache.lengths, self.decoder.inv_freq, g.eps, cache.k[li],
+                          cache.v[li], qd, B, L, g.nq, g.nk, g.d)
+            od, lse = K.attn_fwd_split(qd, ck, cv, maps["ivs"], QR, S, g.d)
+            o = torch.empty((M, g.q), device=qkv.device, dtype=qkv.dtype)
+            K.attn_split_combine(od, lse, maps["dst"], QR, S, g.d, o.view(M * g.nq, g.d))
+            return self._mlp(o, h0, lw, li, linear)
+        q, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, pos, self.decoder.inv_freq, g.eps)
+        v = qkv[:, k_end:]
         # the block's K/V into the cache rows (b, head, cached + t)
         K.rows_copy(k.reshape(M * g.nk, g.d), ck, M * g.nk, dmap=maps["store"])
         K.rows_copy(v.contiguous().view(M * g.nk, g.d), cv, M * g.nk, dmap=maps["store"])
@@ -195,6 +231,11 @@ class BlockDecoder:
             od, _ = K.attn_fwd(qd, ck, cv, maps["iv"], 1, 1, g.d)
             o = torch.empty((M, g.q), device=q.device, dtype=q.dtype)
             K.rows_copy(od, o.view(M * g.nq, g.d), M * g.nq, smap=maps["qrow"])
+        return self._mlp(o, h0, lw, li, linear)
+
+    def _mlp(self, o, h0, lw, li, linear):
+        """o projection (+ residual), post-attention norm and the SwiGLU MLP (+ residual)."""
+        g, r = self.geo, self.lora.rank
         h1 = linear(o, lw.w_o, "o", residual=h0)
         x2, _ = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
         # few-row path: the reduction of the gate/up product applies the SwiGLU ([gate | up] is never stored)

@@ -427,6 +427,44 @@ def attn_fwd(q, k1, v1, iv, Hq, Hkv, D, *, k2=None, v2=None, scale=None):
     return o, lse
 
 
+def attn_fwd_split(q, k, v, iv, QR: int, S: int, D: int, *, scale=None):
+    """Split-key attention of decode blocks: S * QR rows, row i reading query q[i % QR] (one head)
+    against k / v rows over its interval iv[i]; returns (O [S*QR, D], LSE2 [S*QR] fp32)."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        _rowmajor(t, nm)
+    scale = D ** -0.5 if scale is None else scale
+    rows = QR * S
+    if iv.dtype != torch.int32 or tuple(iv.shape) != (rows, 8) or q.shape[0] < QR:
+        raise RuntimeError("attn_fwd_split: int32 iv [S*QR, 8] and q [>= QR, D] required")
+    o = torch.empty((rows, D), device=q.device, dtype=q.dtype)
+    lse = torch.empty(rows, device=q.device, dtype=torch.float32)
+    N.call("unok_attn_fwd_split", QR, S, D, N.ptr(q), _ld(q), N.ptr(k), _ld(k), N.ptr(v), _ld(v), N.ptr(iv),
+           N.ptr(o), _ld(o), N.ptr(lse), float(scale), N.stream())
+    return o, lse
+
+
+def attn_split_combine(o, lse, dst, QR: int, S: int, D: int, out):
+    """out[dst[i]] = merge of the S partial rows s * QR + i (rows with dst[i] < 0 skipped)."""
+    _rowmajor(o, "o")
+    _rowmajor(out, "out")
+    if dst.dtype != torch.int32 or dst.numel() < QR or lse.numel() < QR * S:
+        raise RuntimeError("attn_split_combine: int32 dst [QR] and lse [S*QR] required")
+    N.call("unok_attn_split_combine", QR, S, D, N.ptr(o), _ld(o), N.ptr(lse), N.ptr(dst), N.ptr(out), _ld(out),
+           N.stream())
+    return out
+
+
+def decode_prep(qkv, wq, wk, lengths, inv_freq, eps: float, kc, vc, qd, B: int, L: int, nq: int, nk: int, D: int):
+    """q/k norm + RoPE of a draft block's qkv rows [B*L, (nq+2nk)*D], its K/V rows into the caches
+    kc / vc [B, nk, max_len, D] at the committed lengths, its queries into qd [B*nk*128, D]."""
+    _rowmajor(qkv, "qkv")
+    if qkv.dtype != torch.bfloat16 or lengths.dtype != torch.int64 or not kc.is_contiguous() or not vc.is_contiguous():
+        raise RuntimeError("decode_prep: bf16 qkv, int64 lengths and contiguous caches required")
+    N.call("unok_decode_prep", B, L, nq, nk, D, N.ptr(qkv), _ld(qkv), N.ptr(wq), N.ptr(wk), N.ptr(lengths),
+           N.ptr(inv_freq), float(eps), N.ptr(kc), N.ptr(vc), kc.shape[2], N.ptr(qd), N.stream())
+    return qd
+
+
 def attn_bwd(q, k1, v1, iv, o, lse, do, Hq, Hkv, D, *, k2=None, v2=None, ivk=None, dk=None, dv=None,
              scale=None):
     """Returns dQ; writes dK/dV of source-2 keys into ``dk``/``dv`` when given."""
