@@ -47,7 +47,7 @@ int check_launch(const char* what);
 #define UNOK_SET_LDS_ONCE(kernel, bytes)                                                                \
   do {                                                                                                  \
     static const bool lds_set_ = [] {                                                                   \
-      hipFuncSetAttribute((const void*)(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)(bytes)); \
+      (void)hipFuncSetAttribute((const void*)(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)(bytes)); \
       return true;                                                                                      \
     }();                                                                                                \
     (void)lds_set_;                                                                                     \

@@ -813,20 +813,22 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 // ---------------------------------------------------------------------------------------
 // 256x256 bf16 NT kernel with 16x16x32 MFMAs: 4 waves of 128x128 (8 x 8 accumulators of 4 floats,
-// 256 AGPRs), BK 64 in 2 LDS stages filled by direct-to-LDS loads with the same swizzled layout as
-// the 32x32x16 kernel. A tile is two 32-wide k-steps: step 0 reads step 1's fragments, then the
-// barrier that frees the stage, then step 1 reads the next tile's step-0 fragments and issues the
-// loads of the tile two ahead into the freed stage (one per four MFMAs). Per 32 k and wave: 8 A +
-// 8 B fragment reads (16 bytes per lane) and 64 MFMAs. With the B fragment as the first operand,
-// lane l holds C[row 16i + l % 16][cols 16j + 4 (l / 16) + 0..3] of accumulator (i, j).
+// 256 AGPRs), BK 64, A tiles in 3 LDS stages and B tiles in 2 (160 KB), filled by direct-to-LDS
+// loads with the same swizzled layout as the 32x32x16 kernel. A tile is two 32-wide k-steps: step 0
+// reads step 1's fragments and issues the A loads of the tile two ahead, then the barrier, then
+// step 1 reads the next tile's step-0 fragments and issues that tile's B loads (one load per eight
+// MFMAs in both steps: with all 16 in one step the 64 B/clk vector-memory path saturated and
+// stalled the MFMA stream). Per 32 k and wave: 8 A + 8 B fragment reads (16 bytes per lane) and 64
+// MFMAs. With the B fragment as the first operand, lane l holds C[row 16i + l % 16][cols 16j +
+// 4 (l / 16) + 0..3] of accumulator (i, j).
 // ---------------------------------------------------------------------------------------
 template <typename OutT, int EPI = 0>
 __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p) {
   constexpr int BM = 256, BN = 256, BK = 64, NW = 4, TM = 8, TN = 8;
   constexpr int CPR = BK / 8, RPI = 64 / CPR, INS = BM / (RPI * NW);   // 8 loads per operand and wave
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
-  bf16_t* As = smem;                            // [2][BM*BK]
-  bf16_t* Bs = smem + 2 * BM * BK;              // [2][BN*BK]
+  bf16_t* As = smem;                            // [3][BM*BK]
+  bf16_t* Bs = smem + 3 * BM * BK;              // [2][BN*BK]
 
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -895,21 +897,20 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
 
-  // One k-step: 64 MFMAs on (fa, fb); after every fourth a fragment read of (rstage, rs) in the
-  // order the next step consumes them (fa[0], fb[0..7], fa[1..7]); with ND loads, one
-  // direct-to-LDS load after every 64/ND-th MFMA.
+  // One k-step: 64 MFMAs on (fa, fb); after every fourth a fragment read of A stage ra_st / B
+  // stage rb_st, k-step rs, in the order the next step consumes them (fa[0], fb[0..7], fa[1..7]);
+  // after every eighth one of the 8 direct-to-LDS loads of operand LB (0: A, 1: B) into stage dst.
   auto step = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[TN], bf16x8_t (&na)[TM], bf16x8_t (&nb)[TN],
-                  int rstage, int rs, auto dma_n, uint32_t kb, int dstage) {
-    constexpr int ND = decltype(dma_n)::value;
-    constexpr int EVERY = ND ? TM * TN / ND : 1;
-    const bf16_t* as = As + rstage * BM * BK + a_row0;
-    const bf16_t* bs = Bs + rstage * BN * BK + b_row0;
+                  int ra_st, int rb_st, int rs, auto lb, uint32_t kb, int dst) {
+    constexpr int LB = decltype(lb)::value;
+    const bf16_t* as = As + ra_st * BM * BK + a_row0;
+    const bf16_t* bs = Bs + rb_st * BN * BK + b_row0;
     const int co = ((4 * rs + lk) ^ sw) << 3;
 #pragma unroll
     for (int idx = 0; idx < TM * TN; ++idx) {
       const int i = idx / TN, j = idx % TN;
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-      if (ND && idx % EVERY == 0) dma_one(idx / EVERY, kb, dstage);
+      if (idx % 8 == 0) dma_one(LB * INS + idx / 8, kb, dst);
       if (idx % 4 == 0) {
         const int r = idx / 4;   // 0: fa[0]; 1..8: fb[0..7]; 9..15: fa[1..7]
         if (r == 0) na[0] = *(const bf16x8_t*)&as[co];
@@ -920,13 +921,13 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
 #pragma unroll
     for (int idx = 0; idx < TM * TN; ++idx) {
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      if (ND && idx % EVERY == 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
+      if (idx % 8 == 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
       if (idx % 4 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  using D0 = std::integral_constant<int, 0>;
-  using DF = std::integral_constant<int, 2 * INS>;
+  using LA = std::integral_constant<int, 0>;
+  using LBt = std::integral_constant<int, 1>;
 
   // Prologue: tiles 0 and 1 (clamped) in full; wait for tile 0; its step-0 fragments.
   {
@@ -949,22 +950,31 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
 #pragma unroll
     for (int j = 0; j < TN; ++j) fb0[j] = *(const bf16x8_t*)&bs[j * 16 * BK + co];
   }
+  // A tiles rotate through 3 stages, B tiles through 2. Tile kt+2's A loads fly during tile kt's
+  // first step (into the A stage tile kt-1 used, free since tile kt-1's middle barrier), its B
+  // loads during the second (into tile kt's B stage, free after this tile's middle barrier), so
+  // every step carries 8 loads per wave and the A loads have two to three steps to land.
+  int sa = 0;                 // A stage of tile kt
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1, nxt = cur ^ 1;
-    __builtin_amdgcn_sched_barrier(0);
-    step(fa0, fb0, fa1, fb1, cur, 1, D0{}, 0u, 0);
-    // Tile kt+1 is complete once every wave is here with its loads landed; stage cur is free.
-    __builtin_amdgcn_s_waitcnt(0x0070);
-    asm volatile("s_barrier" ::: "memory");
+    const int sa1 = sa == 2 ? 0 : sa + 1, sa2 = sa1 == 2 ? 0 : sa1 + 1;
+    const int sb = kt & 1;
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t kb = dma_tile(min(kt + 2, nk - 1));
+    step(fa0, fb0, fa1, fb1, sa, sb, 1, LA{}, kb, sa2);
+    // Tile kt+1 is complete once every wave is here with its loads landed (only tile kt+2's A
+    // loads may still fly); tile kt's B stage is free.
+    wait_vm<INS>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
     if (half_last && kt == nk - 1) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa1[i] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
 #pragma unroll
       for (int j = 0; j < TN; ++j) fb1[j] = __builtin_bit_cast(bf16x8_t, make_uint4(0, 0, 0, 0));
     }
-    step(fa1, fb1, fa0, fb0, nxt, 0, DF{}, kb, cur);
+    step(fa1, fb1, fa0, fb0, sa1, sb ^ 1, 0, LBt{}, kb, sb);
+    sa = sa1;
   }
   __builtin_amdgcn_s_waitcnt(0x0070);       // clamped loads still write LDS
 
@@ -997,24 +1007,27 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     // 128 x 128 quadrant of dS into a private 32 KB of the (now idle) LDS stages, 16-byte chunks
     // XOR-swizzled by row so that both the fragment-ordered writes and the row-ordered reads are
     // conflict-free, then walks it four rows per step: every gu load and dgu store is a 256-byte
-    // run per row (16 bytes per lane), with the gu loads of the next eight rows in flight.
-    constexpr int PB = 2, NBATCH = 128 / (4 * PB);
+    // run per row (16 bytes per lane), with the gu loads of the next DEPTH batches of eight rows
+    // in flight (the K loop's fragment registers hold them), the first ones issued before the
+    // staging so that their latency passes behind it.
+    constexpr int PB = 2, NBATCH = 128 / (4 * PB), DEPTH = 6;
     const int F = p.N;
     const int rsub = lane >> 4, c16 = lane & 15;
     const int64_t row0 = m0 + wm * 128 + rsub;
     const int col = n0 + wn * 128 + c16 * 8;
     const bf16_t* gsrc = (const bf16_t*)p.R + row0 * p.ldr + col;
     bf16_t* dst = (bf16_t*)p.C + row0 * p.ldc + col;
-    uint4 gw[2][PB], uw[2][PB];
-    auto load_batch = [&](int b, int buf) {
+    uint4 gw[NBATCH][PB], uw[NBATCH][PB];   // fully unrolled: only DEPTH + 1 batches are live
+    auto load_batch = [&](int b) {
 #pragma unroll
       for (int t = 0; t < PB; ++t) {
         const bf16_t* g = gsrc + (int64_t)((b * PB + t) * 4) * p.ldr;
-        gw[buf][t] = *(const uint4*)g;
-        uw[buf][t] = *(const uint4*)(g + F);
+        gw[b][t] = *(const uint4*)g;
+        uw[b][t] = *(const uint4*)(g + F);
       }
     };
-    load_batch(0, 0);
+#pragma unroll
+    for (int b = 0; b < DEPTH; ++b) load_batch(b);
     asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed (waited above)
     bf16_t* q = smem + wid * 128 * 128;
 #pragma unroll
@@ -1031,14 +1044,14 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int b = 0; b < NBATCH; ++b) {
-      if (b + 1 < NBATCH) load_batch(b + 1, (b + 1) & 1);
+      if (b + DEPTH < NBATCH) load_batch(b + DEPTH);
 #pragma unroll
       for (int t = 0; t < PB; ++t) {
         const int r = (b * PB + t) * 4 + rsub;
         const uint4 dw = *(const uint4*)&q[r * 128 + ((c16 ^ (r & 15)) << 3)];
         const bf16_t* dv = (const bf16_t*)&dw;
-        const bf16_t* gv = (const bf16_t*)&gw[b & 1][t];
-        const bf16_t* uv = (const bf16_t*)&uw[b & 1][t];
+        const bf16_t* gv = (const bf16_t*)&gw[b][t];
+        const bf16_t* uv = (const bf16_t*)&uw[b][t];
         float dg[8], du[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -1240,12 +1253,22 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
       // Interior tile with bf16 output: each wave stages its 128 x 128 fp32 quadrant (alpha
       // applied) through a private 32 KB of the idle LDS stages, 64 rows at a time, and stores by
       // rows: 16 lanes per row, 8 columns (16 bytes) each, the residual read the same way. 16-byte
-      // chunk c of staged row r sits at slot c ^ (r & 15).
-      asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed
-      float* q = (float*)smem + wid * 64 * 128;
+      // chunk c of staged row r sits at slot c ^ (r & 15). The residual rows of both halves are
+      // loaded first, into the registers the K loop's fragments held, so their latency passes
+      // once, behind the staging, instead of once per group of rows.
       const int rsub = lane >> 4, c16 = lane & 15;
       const int64_t rowb = m0 + wm * 128 + rsub;
       const int col = n0 + wn * 128 + 8 * c16;
+      uint4 rw[2][16];
+      if (R) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int it = 0; it < 16; ++it)
+            rw[h][it] = *(const uint4*)((const bf16_t*)R + (rowb + 64 * h + it * 4) * p.ldr + col);
+      }
+      asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed
+      float* q = (float*)smem + wid * 64 * 128;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -1260,7 +1283,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
           }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
-#pragma unroll 4
+#pragma unroll
         for (int it = 0; it < 16; ++it) {
           const int r = it * 4 + rsub;
           const f32x4_t v0 = *(const f32x4_t*)&q[r * 128 + (((2 * c16) ^ (r & 15)) << 2)];
@@ -1268,8 +1291,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
           const int64_t row = rowb + 64 * h + it * 4;
           float a[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
           if (R) {
-            const uint4 rw = *(const uint4*)((const bf16_t*)R + row * p.ldr + col);
-            const uint32_t* rp = (const uint32_t*)&rw;
+            const uint32_t* rp = (const uint32_t*)&rw[h][it];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               a[2 * e] += __uint_as_float(rp[e] << 16);
@@ -1302,7 +1324,7 @@ template <typename OutT, int EPI = 0>
 static void launch_nt_w4m16(const GemmNT& p0, hipStream_t st) {
   GemmNT p = p0;
   p.group = w4m16_group(p.K + p.K2);
-  constexpr size_t lds = 2 * (256 + 256) * 64 * sizeof(bf16_t);
+  constexpr size_t lds = (3 * 256 + 2 * 256) * 64 * sizeof(bf16_t);   // 160 KB
   UNOK_SET_LDS_ONCE((gemm_nt_bf16_w4m16_kernel<OutT, EPI>), lds);
   const int nb = ((p.M + 255) / 256) * ((p.N + 255) / 256);
   hipLaunchKernelGGL((gemm_nt_bf16_w4m16_kernel<OutT, EPI>), dim3(nb), dim3(256), lds, st, p);
