@@ -219,6 +219,17 @@ template <int N> __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Waits until at most `later` (0 .. MAXL, wave-uniform) K tiles of LPT loads each are in flight.
+template <int LPT, int MAXL>
+__device__ __forceinline__ void wait_tiles(int later) {
+  if constexpr (MAXL == 0) {
+    wait_vm<0>();
+  } else {
+    if (later >= MAXL) wait_vm<MAXL * LPT>();
+    else wait_tiles<LPT, MAXL - 1>(later);
+  }
+}
+
 template <int BM, int BN, int NW, int BK, int STAGES, typename OutT, bool ROT = false>
 __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT p) {
   constexpr int CPR = BK / 8;                     // 16-byte chunks per tile row
@@ -334,11 +345,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_nt_bf16_dma_kernel(const GemmNT 
     if (s < nk) issue(s, s);
   for (int kt = 0; kt < nk; ++kt) {
     // Tile kt has landed once at most (tiles issued after it) * LPT loads are outstanding.
-    const int later = min(nk - 1 - kt, STAGES - 2);
-    if (later >= STAGES - 2) wait_vm<(STAGES - 2) * LPT>();
-    else if (STAGES > 3 && later == 2) wait_vm<(STAGES > 3 ? 2 * LPT : 0)>();
-    else if (STAGES > 2 && later == 1) wait_vm<(STAGES > 2 ? LPT : 0)>();
-    else wait_vm<0>();
+    wait_tiles<LPT, STAGES - 2>(min(nk - 1 - kt, STAGES - 2));
     // Plain s_barrier: a __syncthreads() fence would also wait for the tiles still in flight.
     // Each wave has waited for its own loads of tile kt above, so after the barrier the whole
     // tile is in LDS; the "memory" clobber keeps the compiler from moving LDS reads across it.
@@ -899,7 +906,8 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
 
   // One k-step: 64 MFMAs on (fa, fb); after every fourth a fragment read of A stage ra_st / B
   // stage rb_st, k-step rs, in the order the next step consumes them (fa[0], fb[0..7], fa[1..7]);
-  // after every eighth one of the 8 direct-to-LDS loads of operand LB (0: A, 1: B) into stage dst.
+  // between two of those reads, after every eighth MFMA (the third of each eight), one of the 8
+  // direct-to-LDS loads of operand LB (0: A, 1: B) into stage dst.
   auto step = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[TN], bf16x8_t (&na)[TM], bf16x8_t (&nb)[TN],
                   int ra_st, int rb_st, int rs, auto lb, uint32_t kb, int dst) {
     constexpr int LB = decltype(lb)::value;
@@ -910,7 +918,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     for (int idx = 0; idx < TM * TN; ++idx) {
       const int i = idx / TN, j = idx % TN;
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-      if (idx % 8 == 0) dma_one(LB * INS + idx / 8, kb, dst);
+      if (idx % 8 == 2) dma_one(LB * INS + idx / 8, kb, dst);
       if (idx % 4 == 0) {
         const int r = idx / 4;   // 0: fa[0]; 1..8: fb[0..7]; 9..15: fa[1..7]
         if (r == 0) na[0] = *(const bf16x8_t*)&as[co];
@@ -921,7 +929,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
 #pragma unroll
     for (int idx = 0; idx < TM * TN; ++idx) {
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-      if (idx % 8 == 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
+      if (idx % 8 == 2) __builtin_amdgcn_sched_group_barrier(SG_VMEM, 1, 0);
       if (idx % 4 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
