@@ -19,6 +19,7 @@
 #include "lds_tile.h"
 
 #include <stdlib.h>
+#include <type_traits>
 
 struct AttnArgs {
   const void* Q; int64_t ldq;          // [Mq, Hq*D]
@@ -210,22 +211,28 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
   int koff[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) koff[ks] = lq * D + (((ks * 2 + g) ^ kswz<D>(lq)) << 3);
-  int2 voff[NDT];
+  // LDS byte addresses of the V transpose loads in stage 0; the stage and the 16-key step are
+  // immediate offsets (the tile loop below is unrolled over the two stages).
+  uint2 vaddr[NDT];
+  const uint32_t vbase0 = lds_addr(Vs);
 #pragma unroll
-  for (int tt = 0; tt < NDT; ++tt) voff[tt] = tr_frag_off<D>(tt, lane);
+  for (int tt = 0; tt < NDT; ++tt) {
+    const int2 o = tr_frag_off<D>(tt, lane);
+    vaddr[tt] = make_uint2(vbase0 + 2 * o.x, vbase0 + 2 * o.y);
+  }
   if (nt > 0) fetch(0, 0);
-#pragma unroll 1
-  for (int t = 0; t < nt; ++t) {
+  // One K/V tile in LDS stage ST (t & 1), so every stage offset is a compile-time constant.
+  auto tile = [&](const int t, auto stc) {
+    constexpr int ST = decltype(stc)::value;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();                       // K(t), V(t) in LDS; every wave is done with tile t-1
-    if (t + 1 < nt) fetch(t + 1, (t + 1) & 1);
-    const bf16_t* Kc = Ks + (t & 1) * BK * D;
-    const uint32_t vbase = lds_addr(Vs + (t & 1) * BK * D);
+    if (t + 1 < nt) fetch(t + 1, ST ^ 1);
+    const bf16_t* Kc = Ks + ST * BK * D;
     const bool s2 = t >= n1;
     const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
     const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
     const int w_maxlo = s2 ? wb2.maxlo : wb1.maxlo, w_minhi = s2 ? wb2.minhi : wb1.minhi;
-    if (kt >= w_hi || kt + BK <= w_lo) continue;
+    if (kt >= w_hi || kt + BK <= w_lo) return;
     const bool full = kt >= w_maxlo && kt + BK <= w_minhi;
     // Scores of both 32-key halves (kk). All K fragments of the tile are read before the first
     // product, so the two MFMA chains run back to back instead of each MFMA waiting for its read.
@@ -274,8 +281,7 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int tt = 0; tt < NDT; ++tt)
-          tr_issue_p<D>(make_uint2(vbase + 2 * voff[tt].x, vbase + 2 * voff[tt].y), kk * 2 + hh, vlo[kk][hh][tt],
-                        vhi[kk][hh][tt]);
+          tr_issue_p<D, ST * BK * D * 2>(vaddr[tt], kk * 2 + hh, vlo[kk][hh][tt], vhi[kk][hh][tt]);
     };
     issue_v(0);   // in flight during the softmax
     // One running-max update per tile. Raw scores; the scale (> 0) is applied inside the
@@ -350,6 +356,13 @@ __global__ __launch_bounds__(256, QG == 1 ? 2 : 1) void attn_fwd_bf16_kernel(con
     }
     tr_wait_all<NDT>(vlo[1], vhi[1]);
     pv_half(1);
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+#pragma unroll 1
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, S0{});
+    if (t + 1 < nt) tile(t + 1, S1{});
   }
 #pragma unroll
   for (int qg = 0; qg < QG; ++qg) {
@@ -482,23 +495,29 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
   int koff[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) koff[ks] = lq * D + (((ks * 2 + g) ^ kswz<D>(lq)) << 3);
-  int2 toff[NDT];
+  // LDS byte addresses of the K^T transpose loads in stage 0; the stage and the 16-key step are
+  // immediate offsets (the tile loop below is unrolled over the two stages).
+  uint2 kaddr[NDT];
+  const uint32_t kbase0 = lds_addr(Ks);
 #pragma unroll
-  for (int tt = 0; tt < NDT; ++tt) toff[tt] = tr_frag_off<D>(tt, lane);
+  for (int tt = 0; tt < NDT; ++tt) {
+    const int2 o = tr_frag_off<D>(tt, lane);
+    kaddr[tt] = make_uint2(kbase0 + 2 * o.x, kbase0 + 2 * o.y);
+  }
   if (nt > 0) fetch(0, 0);
-#pragma unroll 1
-  for (int t = 0; t < nt; ++t) {
+  // One K/V tile in LDS stage ST (t & 1), so every stage offset is a compile-time constant.
+  auto tile = [&](const int t, auto stc) {
+    constexpr int ST = decltype(stc)::value;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();                       // K(t), V(t) in LDS; previous tile's reads are done
-    const bf16_t* Kc = Ks + (t & 1) * BK * D;
-    const bf16_t* Vc = Vs + (t & 1) * BK * D;
-    const uint32_t kbase_lds = lds_addr(Kc);
-    if (t + 1 < nt) fetch(t + 1, (t + 1) & 1);
+    const bf16_t* Kc = Ks + ST * BK * D;
+    const bf16_t* Vc = Vs + ST * BK * D;
+    if (t + 1 < nt) fetch(t + 1, ST ^ 1);
     const bool s2 = t >= n1;
     const int kt = s2 ? (kb2 / BK) * BK + (t - n1) * BK : (kb1 / BK) * BK + t * BK;
     const int w_lo = s2 ? wb2.lo : wb1.lo, w_hi = s2 ? wb2.hi : wb1.hi;
     const int w_maxlo = s2 ? wb2.maxlo : wb1.maxlo, w_minhi = s2 ? wb2.minhi : wb1.minhi;
-    if (kt >= w_hi || kt + BK <= w_lo) continue;
+    if (kt >= w_hi || kt + BK <= w_lo) return;
     const bool full = kt >= w_maxlo && kt + BK <= w_minhi;
     // key in [lo, hi)  <=>  (unsigned)(key - lo) < (unsigned)(hi - lo)
     const int lo = s2 ? ivq.z : ivq.x;
@@ -529,8 +548,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
       auto issue_k = [&](int hh) {
 #pragma unroll
         for (int tt = 0; tt < NDT; ++tt)
-          tr_issue_p<D>(make_uint2(kbase_lds + 2 * toff[tt].x, kbase_lds + 2 * toff[tt].y), kk * 2 + hh, klo[hh][tt],
-                        khi[hh][tt]);
+          tr_issue_p<D, ST * BK * D * 2>(kaddr[tt], kk * 2 + hh, klo[hh][tt], khi[hh][tt]);
       };
       issue_k(0);
       float pr[16];
@@ -560,6 +578,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
           dq[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_join(klo[hh][tt], khi[hh][tt]), b[hh], dq[tt], 0, 0, 0);
       }
     }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+#pragma unroll 1
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, S0{});
+    if (t + 1 < nt) tile(t + 1, S1{});
   }
   if (qvalid) {
     bf16_t* out = (bf16_t*)p.dQ + (int64_t)qrow * p.lddq + h * D;

@@ -43,13 +43,15 @@ __device__ __forceinline__ void tr_issue_at(uint2 a, u32x2_t& lo, u32x2_t& hi) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(lo) : "v"(a.x), "i"(OFF));
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(a.y), "i"(OFF));
 }
-template <int D>
+// BASE: a further constant byte displacement (e.g. the LDS stage), folded into the immediate.
+template <int D, int BASE = 0>
 __device__ __forceinline__ void tr_issue_p(uint2 a, int p, u32x2_t& lo, u32x2_t& hi) {
   constexpr int STEP = 16 * D * 2;   // bytes per 16 key rows
-  if (p == 0) tr_issue_at<0>(a, lo, hi);
-  else if (p == 1) tr_issue_at<STEP>(a, lo, hi);
-  else if (p == 2) tr_issue_at<2 * STEP>(a, lo, hi);
-  else tr_issue_at<3 * STEP>(a, lo, hi);
+  static_assert(BASE + 3 * STEP < 65536, "LDS immediate offset range");
+  if (p == 0) tr_issue_at<BASE>(a, lo, hi);
+  else if (p == 1) tr_issue_at<BASE + STEP>(a, lo, hi);
+  else if (p == 2) tr_issue_at<BASE + 2 * STEP>(a, lo, hi);
+  else tr_issue_at<BASE + 3 * STEP>(a, lo, hi);
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
