@@ -144,13 +144,17 @@ def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813, total_
     return model, lm, trainer, batch
 
 
-def algorithmic_flops(cfg: dict, wl: dict, mask, head_rows: tuple[int, int], r: int) -> dict:
+def algorithmic_flops(cfg: dict, wl: dict, mask, head_rows: tuple[int, int], r: int,
+                      clean_final: bool = True) -> dict:
     """Algorithmically necessary FLOPs of one step from realised counts (recompute excluded):
     base linears forward on both streams + data gradient of the noisy stream, LoRA forward /
     dgrad / wgrad on noisy rows, attention over allowed pairs only (forward QK^T and PV for both
     streams: 4d per pair; backward dP = dO V^T and dQ = dS K for noisy queries: 4d per pair, dK and dV
     for intra-block pairs: 4d per pair; the kernels' recomputation of S in the backward is not
-    counted), LM head forward + dgrad of CE rows."""
+    counted), LM head forward + dgrad of CE rows. Without ``clean_final`` (no loss reads the clean
+    stream's output) the clean stream's last layer is needed only up to its K and V: its q, o, MLP
+    products and its attention are not counted (the q product, which the step still computes, is
+    left out too)."""
     H, F, d = cfg["hidden_size"], cfg["intermediate_size"], cfg["head_dim"]
     q, kv, Lyr, V = cfg["num_attention_heads"] * d, cfg["num_key_value_heads"] * d, cfg["num_hidden_layers"], cfg["vocab_size"]
     Hq = cfg["num_attention_heads"]
@@ -161,11 +165,12 @@ def algorithmic_flops(cfg: dict, wl: dict, mask, head_rows: tuple[int, int], r: 
     p_clean = int((ivc[:, 1] - ivc[:, 0]).sum())
     p_intra = int((ivn[:, 3] - ivn[:, 2]).sum())
     p_noisy = int((ivn[:, 1] - ivn[:, 0]).sum()) + p_intra
+    tail = 0 if clean_final else 2 * T * (H * q + q * H + 3 * H * F)
     f = {
-        "linear_fwd": 2 * n_lin * 2 * T,
+        "linear_fwd": 2 * n_lin * 2 * T - tail,
         "linear_dgrad": 2 * n_lin * T,
         "lora": 6 * n_lora * T,
-        "attn_fwd": 4 * d * Hq * Lyr * (p_clean + p_noisy),
+        "attn_fwd": 4 * d * Hq * (Lyr * (p_clean + p_noisy) - (0 if clean_final else p_clean)),
         "attn_bwd": (4 * d * Hq * p_noisy + 4 * d * Hq * p_intra) * Lyr,
         # LM head: forward over the student rows and the teacher rows, data gradient of the student rows
         "lm_head": 2 * H * V * (2 * head_rows[0] + head_rows[1]),
@@ -457,7 +462,8 @@ def main() -> int:
         # (student rows, teacher rows) of the LM head: CE on the noised rows with a next token;
         # TV / KL on every supervised row, student and teacher
         head_rows = (ce_rows, 0) if wl.get("objective", "ce") == "ce" else (supervised, supervised)
-        per_block[b] = algorithmic_flops(cfg, wl, mask, head_rows, wl["lora_rank"])
+        per_block[b] = algorithmic_flops(cfg, wl, mask, head_rows, wl["lora_rank"],
+                                         clean_final=trainer._needs_teacher())
     base._bd_step = draws
     flops = {k: sum(per_block[b][k] for b in blocks) / len(blocks) for k in per_block[blocks[0]]}
 

@@ -163,3 +163,48 @@ def test_step_bf16_tolerances(dev, spec_name, obj):
     assert rms(mine) <= max(1e-2, 1.1 * rms(theirs))
     for k, (c, r) in mine.items():
         assert r <= max(1e-2, 1.3 * theirs[k][1]), (k, r, theirs[k][1])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_clean_tail_skipped_only_when_no_teacher(dev, dtype):
+    """A CE step on data targets skips the clean stream's last-layer output (only that layer's K/V
+    feed the noisy stream): loss and LoRA gradients are bit-identical to the step that computes it,
+    the decoder's setting is restored afterwards, and a TV step keeps computing it."""
+    obj, _ = OBJECTIVES["ce_data"]
+    _, _, _, model, lm, trainer, batch = _setup(MID, dtype, dev, obj)
+    decoder = model.model
+    assert trainer._needs_teacher() is False
+
+    seen = []
+    full = decoder.forward
+
+    def spy(*a, **k):
+        seen.append(decoder.clean_final_needed)
+        return full(*a, **k)
+
+    decoder.forward = spy
+    results = {}
+    draws = model._bd_step          # both steps draw the same noise
+    for forced in (None, True):
+        if forced:
+            trainer._needs_teacher = lambda: True
+        model._bd_step = draws
+        lm.zero_grad(set_to_none=True)
+        loss = trainer.compute_loss(lm, _to(batch, dev))
+        loss.backward()
+        torch.cuda.synchronize()
+        results[forced] = (loss.detach().clone(), {k: v.detach().clone() for k, v in _my_grads(lm).items()})
+        assert decoder.clean_final_needed is True
+    assert seen == [False, True]
+    (l0, g0), (l1, g1) = results[None], results[True]
+    assert torch.equal(l0, l1)
+    for k in g0:
+        assert torch.equal(g0[k], g1[k]), k
+
+    del trainer._needs_teacher
+    trainer.objective = OBJECTIVES["tv"][0]
+    assert trainer._needs_teacher() is True
+    seen.clear()
+    trainer.compute_loss(lm, _to(batch, dev))
+    assert seen == [True]
+    decoder.forward = full

@@ -90,6 +90,15 @@ def clean_layer(h: torch.Tensor, lw: LayerWeights, g: Geometry, sc: StreamContex
     return h2, k, v
 
 
+def clean_layer_kv(h: torch.Tensor, lw: LayerWeights, g: Geometry, sc: StreamContext):
+    """The K and V a clean-stream layer hands the noisy stream, without the layer's output (its
+    attention, o projection and MLP): the same kernels and values as clean_layer's k and v."""
+    x1, _ = K.rmsnorm_fwd(h, lw.ln_in, g.eps)
+    qkv = K.gemm_nt(x1, lw.w_qkv)
+    _, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
+    return k, qkv[:, g.q + g.kv:]
+
+
 def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: StreamContext, need_output: bool = True):
     """Forward of one noisy-stream layer; returns (h2 or None, the activations its backward reads).
     Deterministic: a second call on the same inputs reproduces every buffer bit for bit, which the

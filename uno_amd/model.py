@@ -340,6 +340,11 @@ class UnoQwen3Model(nn.Module):
         self.recompute_reserve_bytes = 24 << 30
         self.last_recompute_plan: list[bool] = []
         self._auto_plan = None      # (shape/budget key, plan) of the last "auto" decision
+        # Whether the clean stream's final hidden states are computed. With False, the last layer
+        # of the clean stream produces only the K/V the noisy stream reads (its attention, o
+        # projection and MLP, and the final norm, feed nothing else), and the clean rows of the
+        # output are zeros: for callers whose loss reads no teacher (CE on data targets).
+        self.clean_final_needed = True
 
     def recompute_plan(self, rows: int, rank: int, elem: int) -> list[bool]:
         """Which noisy-stream layers keep only their input for the backward (recompute) this step.
@@ -407,11 +412,18 @@ class UnoQwen3Model(nn.Module):
         emb = self.embed_tokens.weight
         with torch.no_grad():
             hc = K.embedding(mask.clean_ids, emb)
-            for lw in lws:
-                hc, k, v = Lyr.clean_layer(hc, lw, g, sc)
+            for li, lw in enumerate(lws):
+                if li == len(lws) - 1 and not self.clean_final_needed:
+                    k, v = Lyr.clean_layer_kv(hc, lw, g, sc)
+                    hc = None
+                else:
+                    hc, k, v = Lyr.clean_layer(hc, lw, g, sc)
                 sc.clean_k.append(k)
                 sc.clean_v.append(v)
-            clean_final, _ = K.rmsnorm_fwd(hc, self.norm.weight, g.eps)
+            if hc is not None:
+                clean_final, _ = K.rmsnorm_fwd(hc, self.norm.weight, g.eps)
+            else:
+                clean_final = torch.zeros((mask.B * mask.L, g.H), device=emb.device, dtype=emb.dtype)
             del hc
         hn = K.embedding(mask.noisy_ids, emb)
         if lora is None:

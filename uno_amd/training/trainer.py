@@ -207,8 +207,18 @@ class UnoTrainer(Trainer):
         concatenated_ids, concatenated_positions, bd_mask, noised_positions, _, p_mask = \
             base_model.prepare_for_bd_training(inputs["input_ids"], model_positions, labels == IGNORE_INDEX)
         self._lora_router.set_token_mask(noisy_region_mask)
-        hidden_states = run_prepared_uno_forward(model, base_model, inputs, concatenated_ids,
-                                                 concatenated_positions, bd_mask)
+        # The clean stream's final hidden states feed only the teacher side of the losses; the
+        # decoder skips them for this forward when no loss reads them.
+        decoder = base_model.model
+        keep = getattr(decoder, "clean_final_needed", None)
+        if keep is not None:
+            decoder.clean_final_needed = self._needs_teacher()
+        try:
+            hidden_states = run_prepared_uno_forward(model, base_model, inputs, concatenated_ids,
+                                                     concatenated_positions, bd_mask)
+        finally:
+            if keep is not None:
+                decoder.clean_final_needed = keep
         noisy_hidden, clean_hidden = extract_uno_regions(hidden_states, noisy_region_mask, sequence_length)
 
         supervised_mask = labels != IGNORE_INDEX
@@ -263,6 +273,11 @@ class UnoTrainer(Trainer):
             return combined_loss, {"loss": combined_loss, "ce_loss": ce_loss, "reverse_kl_loss": kl_loss,
                                    "tv_loss": tv_loss}
         return combined_loss
+
+    def _needs_teacher(self) -> bool:
+        """Whether the losses read the clean stream's hidden states (TV, KL, clean-argmax CE targets)."""
+        o = self.objective
+        return o.kl_weight > 0 or o.tv_weight > 0 or (o.ce_weight > 0 and o.internal_ce_target != "data")
 
     def logged(self) -> list[dict]:
         """The per-step objective metrics of compute_loss, as floats."""
