@@ -1128,6 +1128,39 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     // Cross-entropy gradient of the recomputed logits: dz = bf16(w g inv_n (exp(z - lse) - onehot)),
     // the same arithmetic as the separate gradient kernel over stored logits.
     const float gs = p.ce_g[0] * p.ce_inv_n[0];
+    if (m0 + BM <= p.M && n0 + BN <= p.N && (p.ldc & 7) == 0) {
+      // Interior tile: each wave rounds its 128 x 128 quadrant of dz into a private 32 KB of the
+      // idle LDS stages (16-byte chunk c of row r at slot c ^ (r & 15)) and stores it by rows, 16
+      // lanes per 256-byte row, instead of 8 bytes per lane scattered over 16 rows.
+      asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed
+      bf16_t* qs = smem + wid * 128 * 128;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = i * 16 + lr;
+        const int row = m0 + wm * 128 + r;
+        const float lse = p.ce_lse[row], cf = p.ce_w[row] * gs;
+        const int64_t t = p.ce_tgt[row] - p.ce_vocab0;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int col = n0 + wn * 128 + j * 16 + lk * 4;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = cf * (fast_expf(acc[i][j][e] - lse) - ((int64_t)(col + e) == t ? 1.f : 0.f));
+          *(uint2*)&qs[r * 128 + (((2 * j + (lk >> 1)) ^ lr) << 3) + (lk & 1) * 4] =
+              make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_wave_barrier();
+      const int rsub = lane >> 4, c16 = lane & 15;
+      bf16_t* dst = (bf16_t*)p.C + (int64_t)(m0 + wm * 128 + rsub) * p.ldc + n0 + wn * 128 + c16 * 8;
+#pragma unroll
+      for (int it = 0; it < 32; ++it) {
+        const int r = it * 4 + rsub;
+        *(uint4*)(dst + (int64_t)(it * 4) * p.ldc) = *(const uint4*)&qs[r * 128 + ((c16 ^ (r & 15)) << 3)];
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int row = m0 + wm * 128 + i * 16 + lr;
