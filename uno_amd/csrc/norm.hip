@@ -129,25 +129,28 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ 
 // angles fl32(pos * inv_freq[j]) are evaluated once per row (one sincosf per lane) into LDS.
 // Reads the fused qkv projection output, writes contiguous q and k.
 // ---------------------------------------------------------------------------------------
+// Head passes whose loads the qk-norm / RoPE kernels issue together.
+constexpr int QKR_GROUP = 5;
+
 template <typename T> struct Vec16;
 template <> struct Vec16<bf16_t> {
   static constexpr int N = 8;
-  __device__ __forceinline__ static void load(const bf16_t* p, float (&v)[8]) {
-    const uint4 u = *(const uint4*)p;
+  __device__ __forceinline__ static void unpack(const uint4 u, float (&v)[8]) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) { v[2 * i] = __uint_as_float(w[i] << 16); v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u); }
   }
+  __device__ __forceinline__ static void load(const bf16_t* p, float (&v)[8]) { unpack(*(const uint4*)p, v); }
   __device__ __forceinline__ static void store(bf16_t* p, const float (&v)[8]) {
     *(uint4*)p = make_uint4(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]), pack2_bf16(v[4], v[5]), pack2_bf16(v[6], v[7]));
   }
 };
 template <> struct Vec16<float> {
   static constexpr int N = 4;
-  __device__ __forceinline__ static void load(const float* p, float (&v)[4]) {
-    const float4 u = *(const float4*)p;
-    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+  __device__ __forceinline__ static void unpack(const uint4 u, float (&v)[4]) {
+    v[0] = __uint_as_float(u.x); v[1] = __uint_as_float(u.y); v[2] = __uint_as_float(u.z); v[3] = __uint_as_float(u.w);
   }
+  __device__ __forceinline__ static void load(const float* p, float (&v)[4]) { unpack(*(const uint4*)p, v); }
   __device__ __forceinline__ static void store(float* p, const float (&v)[4]) { *(float4*)p = make_float4(v[0], v[1], v[2], v[3]); }
 };
 
@@ -184,38 +187,49 @@ __global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const T* __restric
   for (int e = 0; e < EPL; ++e) { cv[e] = s_cs[w][j0 + e]; sv[e] = s_sn[w][j0 + e]; }
   const int nh = nq + nk;
   const bool norm = wq != nullptr;
-  for (int hb = 0; hb < nh; hb += HPW) {
-    const int head = hb + hh;
-    const bool valid = head < nh;
-    const bool isq = head < nq;
-    float x[EPL];
-    if (valid) Vec16<T>::load(qkv + (int64_t)row * ld + (int64_t)head * D + c0, x);
-    else {
+  float wqv[EPL], wkv[EPL];
+  if (norm) {
+    Vec16<T>::load(wq + c0, wqv);
+    Vec16<T>::load(wk + c0, wkv);
+  }
+  // Heads in groups of QKR_GROUP passes: the group's loads are all issued before its arithmetic,
+  // so each wavefront keeps several KB of the row in flight instead of one pass's 1 KB.
+  for (int hb0 = 0; hb0 < nh; hb0 += HPW * QKR_GROUP) {
+    uint4 raw[QKR_GROUP];
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) x[e] = 0.f;
+    for (int gi = 0; gi < QKR_GROUP; ++gi) {
+      const int head = hb0 + gi * HPW + hh;
+      raw[gi] = head < nh ? *(const uint4*)(qkv + (int64_t)row * ld + (int64_t)head * D + c0) : make_uint4(0, 0, 0, 0);
     }
-    if (norm) {
-      float ss = 0.f;
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) ss += x[e] * x[e];
+    for (int gi = 0; gi < QKR_GROUP; ++gi) {
+      const int head = hb0 + gi * HPW + hh;
+      const bool valid = head < nh;
+      const bool isq = head < nq;
+      float x[EPL];
+      Vec16<T>::unpack(raw[gi], x);
+      if (norm) {
+        float ss = 0.f;
 #pragma unroll
-      for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      const float r = rsqrtf(ss / (float)D + eps);
-      if (valid && lane % LPH == 0) rstd[(int64_t)row * nh + head] = r;
-      float wv[EPL];
-      if (valid) Vec16<T>::load((isq ? wq : wk) + c0, wv);
+        for (int e = 0; e < EPL; ++e) ss += x[e] * x[e];
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) x[e] = valid ? Elem<T>::round(Elem<T>::round(x[e] * r) * wv[e]) : 0.f;
-    }
-    float out[EPL];
+        for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float r = rsqrtf(ss / (float)D + eps);
+        if (valid && lane % LPH == 0) rstd[(int64_t)row * nh + head] = r;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const float y = __shfl_xor(x[e], LPH / 2, 64);   // partner element i +- d/2
-      out[e] = x[e] * cv[e] + sgn * y * sv[e];
-    }
-    if (valid) {
-      T* dst = isq ? qo + ((int64_t)row * nq + head) * D : ko + ((int64_t)row * nk + (head - nq)) * D;
-      Vec16<T>::store(dst + c0, out);
+        for (int e = 0; e < EPL; ++e)
+          x[e] = valid ? Elem<T>::round(Elem<T>::round(x[e] * r) * (isq ? wqv[e] : wkv[e])) : 0.f;
+      }
+      float out[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const float y = __shfl_xor(x[e], LPH / 2, 64);   // partner element i +- d/2
+        out[e] = x[e] * cv[e] + sgn * y * sv[e];
+      }
+      if (valid) {
+        T* dst = isq ? qo + ((int64_t)row * nq + head) * D : ko + ((int64_t)row * nk + (head - nq)) * D;
+        Vec16<T>::store(dst + c0, out);
+      }
     }
   }
 }
@@ -244,46 +258,59 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const T* __restric
   for (int e = 0; e < EPL; ++e) { cv[e] = s_cs[w][j0 + e]; sv[e] = s_sn[w][j0 + e]; }
   const int nh = nq + nk;
   const bool norm = wq != nullptr;
-  for (int hb = 0; hb < nh; hb += HPW) {
-    const int head = hb + hh;
-    const bool valid = head < nh;
-    const bool isq = head < nq;
-    float dy[EPL];
-    if (valid) Vec16<T>::load(isq ? dq + ((int64_t)row * nq + head) * D + c0 : dk + ((int64_t)row * nk + (head - nq)) * D + c0, dy);
-    else {
+  float wqv[EPL], wkv[EPL];
+  if (norm) {
+    Vec16<T>::load(wq + c0, wqv);
+    Vec16<T>::load(wk + c0, wkv);
+  }
+  // As in the forward: each group's loads (upstream gradient, input row, rstd) go out before its
+  // arithmetic.
+  for (int hb0 = 0; hb0 < nh; hb0 += HPW * QKR_GROUP) {
+    uint4 rdy[QKR_GROUP], rx[QKR_GROUP];
+    float rs[QKR_GROUP];
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) dy[e] = 0.f;
+    for (int gi = 0; gi < QKR_GROUP; ++gi) {
+      const int head = hb0 + gi * HPW + hh;
+      const bool valid = head < nh;
+      const bool isq = head < nq;
+      rdy[gi] = valid ? *(const uint4*)(isq ? dq + ((int64_t)row * nq + head) * D + c0
+                                            : dk + ((int64_t)row * nk + (head - nq)) * D + c0)
+                      : make_uint4(0, 0, 0, 0);
+      rx[gi] = valid && norm ? *(const uint4*)(qkv + (int64_t)row * ld + (int64_t)head * D + c0) : make_uint4(0, 0, 0, 0);
+      rs[gi] = valid && norm ? rstd[(int64_t)row * nh + head] : 0.f;
     }
-    float g[EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const float y = __shfl_xor(dy[e], LPH / 2, 64);
-      g[e] = dy[e] * cv[e] + sgn * y * sv[e];
-    }
-    if (norm) {
-      const float r = valid ? rstd[(int64_t)row * nh + head] : 0.f;
-      float x[EPL], wv[EPL];
-      if (valid) {
-        Vec16<T>::load(qkv + (int64_t)row * ld + (int64_t)head * D + c0, x);
-        Vec16<T>::load((isq ? wq : wk) + c0, wv);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) { x[e] = 0.f; wv[e] = 0.f; }
-      }
-      float dot = 0.f;
+    for (int gi = 0; gi < QKR_GROUP; ++gi) {
+      const int head = hb0 + gi * HPW + hh;
+      const bool valid = head < nh;
+      const bool isq = head < nq;
+      float dy[EPL];
+      Vec16<T>::unpack(rdy[gi], dy);
+      float g[EPL];
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
-        x[e] *= r;            // x-hat
-        g[e] *= wv[e];
-        dot += g[e] * x[e];
+        const float y = __shfl_xor(dy[e], LPH / 2, 64);
+        g[e] = dy[e] * cv[e] + sgn * y * sv[e];
       }
+      if (norm) {
+        const float r = rs[gi];
+        float x[EPL];
+        Vec16<T>::unpack(rx[gi], x);
+        float dot = 0.f;
 #pragma unroll
-      for (int o = LPH / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
-      dot /= (float)D;
+        for (int e = 0; e < EPL; ++e) {
+          x[e] *= r;            // x-hat
+          g[e] *= valid ? (isq ? wqv[e] : wkv[e]) : 0.f;
+          dot += g[e] * x[e];
+        }
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) g[e] = r * (g[e] - x[e] * dot);
+        for (int o = LPH / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+        dot /= (float)D;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) g[e] = r * (g[e] - x[e] * dot);
+      }
+      if (valid) Vec16<T>::store(dqkv + (int64_t)row * ldd + (int64_t)head * D + c0, g);
     }
-    if (valid) Vec16<T>::store(dqkv + (int64_t)row * ldd + (int64_t)head * D + c0, g);
   }
 }
 
