@@ -1618,10 +1618,15 @@ static int tn_skinny_splits(int Mrows, int NX) {
 template <int NS, bool TOUT>
 __global__ __launch_bounds__(256, NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const GemmTNSkinny p) {
   constexpr int BK = 64, XB = 128, TS = NS / 32;
-  static_assert(NS == 64 || NS == 128, "swizzled transpose tiles are defined for 64 and 128 columns");
+  // The skinny operand's tile is one swizzled [64 x NSA] tile and, for NS = 192, a second
+  // [64 x 64] one holding columns 128 .. 191.
+  constexpr int NSA = NS > 128 ? 128 : NS, NSB = NS - NSA, TSA = NSA / 32;
+  constexpr int NSB_ = NSB > 0 ? NSB : 64;   // tile width for the helpers (unused when NSB = 0)
+  static_assert(NS == 64 || NS == 128 || NS == 192, "swizzled transpose tiles are defined for 64 and 128 columns");
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   bf16_t* Xs = smem;                   // [2][BK * XB]
-  bf16_t* Ss = smem + 2 * BK * XB;     // [2][BK * NS]
+  bf16_t* Ss = smem + 2 * BK * XB;     // [2][BK * NSA]
+  bf16_t* Sb = Ss + 2 * BK * NSA;      // [2][BK * NSB]
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, lq = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(w);
   const int nstrip = (p.NX + XB - 1) / XB;
@@ -1630,16 +1635,18 @@ __global__ __launch_bounds__(256, NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const
   const int mbeg = z * p.rows_per_split;
   const int mend = min(p.Mrows, mbeg + p.rows_per_split);
   const int nt = mend > mbeg ? (mend - mbeg + BK - 1) / BK : 0;
-  const uint32_t xo = dma_lane_off<XB>(p.ldx, x0, wid, lane), so = dma_lane_off<NS>(p.lds, 0, wid, lane);
+  const uint32_t xo = dma_lane_off<XB>(p.ldx, x0, wid, lane), so = dma_lane_off<NSA>(p.lds, 0, wid, lane);
+  const uint32_t sob = NSB > 0 ? dma_lane_off<NSB_>(p.lds, NSA, wid, lane) : 0u;
   auto fetch = [&](int t) {
     const int m0 = mbeg + t * BK;
     dma_tile<XB>(p.X, p.ldx, xo, m0, mend, Xs + (t & 1) * BK * XB, wid);
-    dma_tile<NS>(p.S, p.lds, so, m0, mend, Ss + (t & 1) * BK * NS, wid);
+    dma_tile<NSA>(p.S, p.lds, so, m0, mend, Ss + (t & 1) * BK * NSA, wid);
+    if constexpr (NSB > 0) dma_tile<NSB_>(p.S, p.lds, sob, m0, mend, Sb + (t & 1) * BK * NSB_, wid);
   };
   const int2 xoff = tr_frag_off<XB>(w, lane);
   int2 soff[TS];
 #pragma unroll
-  for (int i = 0; i < TS; ++i) soff[i] = tr_frag_off<NS>(i, lane);
+  for (int i = 0; i < TS; ++i) soff[i] = i < TSA ? tr_frag_off<NSA>(i, lane) : tr_frag_off<NSB_>(i - TSA, lane);
   f32x16_t acc[TS];
 #pragma unroll
   for (int i = 0; i < TS; ++i)
@@ -1652,15 +1659,18 @@ __global__ __launch_bounds__(256, NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();                       // tile t in LDS; every wave is done with tile t-1
     if (t + 1 < nt) fetch(t + 1);
-    const uint32_t xb = lds_addr(Xs + (t & 1) * BK * XB), sb = lds_addr(Ss + (t & 1) * BK * NS);
+    const uint32_t xb = lds_addr(Xs + (t & 1) * BK * XB), sb = lds_addr(Ss + (t & 1) * BK * NSA);
+    const uint32_t sbb = lds_addr(Sb + (t & 1) * BK * NSB_);
     // All operands of the tile's four 16-row steps, then one wait, then the MFMAs.
     u32x2_t xl[4], xh[4], sl[4][TS], sh[4][TS];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       tr_issue_p<XB>(make_uint2(xb + 2 * xoff.x, xb + 2 * xoff.y), q, xl[q], xh[q]);
 #pragma unroll
-      for (int i = 0; i < TS; ++i)
-        tr_issue_p<NS>(make_uint2(sb + 2 * soff[i].x, sb + 2 * soff[i].y), q, sl[q][i], sh[q][i]);
+      for (int i = 0; i < TS; ++i) {
+        if (i < TSA) tr_issue_p<NSA>(make_uint2(sb + 2 * soff[i].x, sb + 2 * soff[i].y), q, sl[q][i], sh[q][i]);
+        else tr_issue_p<NSB_>(make_uint2(sbb + 2 * soff[i].x, sbb + 2 * soff[i].y), q, sl[q][i], sh[q][i]);
+      }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -1754,6 +1764,7 @@ static void launch_tn_skinny_t(const GemmTNSkinny& p, int nz, bool tout, hipStre
 static void launch_tn_skinny(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
   if (p.NS == 64) { launch_tn_tr_t<64>(p, nz, tout, st); return; }
   if (p.NS == 128) { launch_tn_tr_t<128>(p, nz, tout, st); return; }
+  if (p.NS == 192) { launch_tn_tr_t<192>(p, nz, tout, st); return; }
   switch (p.NS) {
     case 32: launch_tn_skinny_t<32>(p, nz, tout, st); break;
     case 64: launch_tn_skinny_t<64>(p, nz, tout, st); break;
@@ -1785,7 +1796,7 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
     const void* X = a_small ? B : A;
     if (NS % 32 == 0 && NS <= 256 && NX >= TNS_QB && NX % 8 == 0 && lds_ % 8 == 0 && ldx % 8 == 0 &&
         aligned16(S) && aligned16(X)) {
-      const bool tr = NS == 64 || NS == 128;
+      const bool tr = NS == 64 || NS == 128 || NS == 192;
       const int nz0 = tr ? tn_tr_splits(Mrows, NX, NS) : tn_skinny_splits(Mrows, NX);
       int rps = (Mrows + nz0 - 1) / nz0;
       rps = ((rps + TNS_BK - 1) / TNS_BK) * TNS_BK;
