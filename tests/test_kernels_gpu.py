@@ -343,12 +343,14 @@ def test_distribution_losses_match_oracle(dev, kind, dtype):
 # ------------------------------------------------------------------------------------------
 # Optimizer
 # ------------------------------------------------------------------------------------------
-def test_fused_adamw_matches_torch(dev):
+@pytest.mark.parametrize("n", [100_003, 20_000_003])
+def test_fused_adamw_matches_torch(dev, n):
+    """Clip + AdamW + compute copy against torch; the larger size makes every thread of the grid
+    take several passes (both the two-group body and the single-group tail)."""
     from uno_amd import _native as N
     torch.manual_seed(7)
-    n = 100_003
     p0 = torch.randn(n, device=dev)
-    parts = [slice(0, 40_000), slice(40_000, 100_003)]
+    parts = [slice(0, 40_000), slice(40_000, n)]
     ref = [p0[s].clone().requires_grad_(True) for s in parts]
     opt = torch.optim.AdamW(ref, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
     p, m, v = p0.clone(), torch.zeros(n, device=dev), torch.zeros(n, device=dev)
@@ -366,6 +368,7 @@ def test_fused_adamw_matches_torch(dev):
         N.call("unok_adamw_step", n, N.ptr(p), N.ptr(gg), N.ptr(m), N.ptr(v), N.ptr(clip), 1e-3, 0.9, 0.999, 1e-8,
                0.01, step, N.BF16, N.ptr(copy), 40_000, 2.0, N.stream())
         assert abs(clip[0].item() - g.norm().item()) / g.norm().item() < 1e-5
+        assert torch.equal(gg, g * clip[1])
     mine = torch.cat([p[s] for s in parts])
     theirs = torch.cat([t.detach() for t in ref])
     assert (mine - theirs).abs().max().item() < 1e-6
