@@ -629,9 +629,11 @@ __device__ __forceinline__ void dma_rows32(const bf16_t* src, int64_t ld, int co
 // staging the Q and dO rows of a sub-tile into its own LDS region (no workgroup barriers).
 // Per sub-tile: S = Q K^T and dP = dO V^T with K, V in registers (lane = key), P and dS from
 // LSE and Dsum, then dV^T += dO^T P and dK^T += Q^T dS with the transposed operands read from the
-// row-major tiles by transpose loads in the accumulator's query order.
+// row-major tiles by transpose loads in the accumulator's query order. One workgroup per CU: the
+// K, V rows and the dK, dV accumulators need more than the 256 registers of two waves per SIMD,
+// and spilling them costs more than the halved occupancy (dK/dV at 4 x 4096, block 16: 109 -> 89 us).
 template <int D>
-__global__ __launch_bounds__(256, 2) void attn_dkv_bf16_kernel(const AttnArgs p) {
+__global__ __launch_bounds__(256, 1) void attn_dkv_bf16_kernel(const AttnArgs p) {
   constexpr int NKS = D / 16, NDT = D / 32, QT = 32;
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];   // per wave: Q [32*D], dO [32*D]
   __shared__ __attribute__((aligned(16))) float s_ld[4][2][QT];     // per wave: LSE, Dsum of the sub-tile
