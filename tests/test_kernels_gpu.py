@@ -67,11 +67,14 @@ def ref_qknorm_rope(qkv, nq, nk, d, wq, wk, pos, theta, eps):
     return (q * c + rot(q) * s).reshape(M, -1), (k * c + rot(k) * s).reshape(M, -1)
 
 
-@pytest.mark.parametrize("dtype,d,norm", [(torch.float32, 64, True), (torch.bfloat16, 128, True),
-                                          (torch.bfloat16, 128, False)])
-def test_qknorm_rope_fwd_bwd(dev, dtype, d, norm):
+@pytest.mark.parametrize("dtype,d,norm,nq,nk", [(torch.float32, 64, True, 4, 2), (torch.bfloat16, 128, True, 4, 2),
+                                                (torch.bfloat16, 128, False, 4, 2),
+                                                # several groups of head passes, whole and partial
+                                                (torch.bfloat16, 128, True, 32, 8), (torch.bfloat16, 128, False, 32, 32),
+                                                (torch.float32, 64, True, 12, 4)])
+def test_qknorm_rope_fwd_bwd(dev, dtype, d, norm, nq, nk):
     torch.manual_seed(1)
-    M, nq, nk, theta = 96, 4, 2, 1e6
+    M, theta = 96, 1e6
     qkv = torch.randn(M, (nq + 2 * nk) * d, device=dev).to(dtype)
     wq = (1 + 0.1 * torch.randn(d, device=dev)).to(dtype) if norm else None
     wk = (1 + 0.1 * torch.randn(d, device=dev)).to(dtype) if norm else None
