@@ -1614,7 +1614,8 @@ static int tn_skinny_splits(int Mrows, int NX) {
 // pair up). Wave w owns x columns x0 + 32 w .. + 31 and all NS / 32 row blocks. Partials are
 // written in the layout of gemm_tn_skinny_kernel, for the same split-K reduction. Three
 // workgroups per CU for NS = 64 (48 KB of LDS each), so the split counts of the LoRA shapes
-// (e.g. 96 strips x 6 splits for 12288 columns) run in one round.
+// (e.g. 96 strips x 6 splits for 12288 columns) run in one round; two for NS = 128 (64 KB) and
+// NS = 192 (80 KB).
 template <int NS, bool TOUT>
 __global__ __launch_bounds__(256, NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const GemmTNSkinny p) {
   constexpr int BK = 64, XB = 128, TS = NS / 32;
@@ -1622,7 +1623,7 @@ __global__ __launch_bounds__(256, NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const
   // [64 x 64] one holding columns 128 .. 191.
   constexpr int NSA = NS > 128 ? 128 : NS, NSB = NS - NSA, TSA = NSA / 32;
   constexpr int NSB_ = NSB > 0 ? NSB : 64;   // tile width for the helpers (unused when NSB = 0)
-  static_assert(NS == 64 || NS == 128 || NS == 192, "swizzled transpose tiles are defined for 64 and 128 columns");
+  static_assert(NS == 64 || NS == 128 || NS == 192, "skinny side of 64, 128 or 192 (128 + 64) columns");
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   bf16_t* Xs = smem;                   // [2][BK * XB]
   bf16_t* Ss = smem + 2 * BK * XB;     // [2][BK * NSA]
