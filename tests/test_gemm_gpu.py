@@ -24,6 +24,26 @@ def test_gemm_nt_plain(dev, M, N, Kd, dtype):
     assert _rel(out, ref) < (1e-6 if dtype == torch.float32 else 1e-5), (M, N, Kd)
 
 
+def test_gemm_nt_operand_beyond_4gib(dev):
+    """An operand whose rows lie 2^20 elements apart spans more than 4 GiB (the shape of the TV / KL
+    logit-gradient product, dz [rows, vocab] times the LM head): the 256x256 kernel addresses each
+    256-row strip from its own base, so its 32-bit buffer offsets still reach every row. Checked
+    against fp32 and, bit for bit, against the same rows as a compact operand."""
+    torch.manual_seed(11)
+    M, Kd, N, lda = 2304, 4096, 512, 1 << 20
+    big = torch.empty(M, lda, device=dev, dtype=torch.bfloat16)     # 4.8 GB
+    a = big[:, :Kd]
+    a.copy_(torch.randn(M, Kd, device=dev))
+    b = torch.randn(N, Kd, device=dev).bfloat16()
+    out = K.gemm_nt(a, b)
+    compact = K.gemm_nt(a.contiguous(), b)
+    ref = a.float() @ b.float().T
+    torch.cuda.synchronize()
+    assert _rel(out, ref) < 1e-2
+    assert torch.equal(out, compact)
+    del big
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_gemm_nt_lora_segments_gate_residual(dev, dtype):
     """Fused q|k|v-style product: per-segment LoRA extension, row gate, residual, alpha."""

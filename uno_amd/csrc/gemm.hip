@@ -856,16 +856,21 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
   const bool half_last = ext && (p.K2 % BK) != 0;
 
   const int lrowi = lane / CPR, slot = lane % CPR;
-  __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(((int64_t)(p.M - 1) * p.lda + p.K) * 2));
-  __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)(((int64_t)(p.N - 1) * p.ldb + p.K) * 2));
+  // Operand rows are addressed from this tile's first row, so the 32-bit buffer offsets span one
+  // 256-row strip rather than the whole operand (rows past the end clamp to its last row).
+  const int mrows = min(p.M - m0, BM), nrows = min(p.N - n0, BN);
+  __amdgpu_buffer_rsrc_t ra = make_rsrc((const bf16_t*)p.A + (int64_t)m0 * p.lda,
+                                        (uint32_t)(((int64_t)(mrows - 1) * p.lda + p.K) * 2));
+  __amdgpu_buffer_rsrc_t rb = make_rsrc((const bf16_t*)p.B + (int64_t)n0 * p.ldb,
+                                        (uint32_t)(((int64_t)(nrows - 1) * p.ldb + p.K) * 2));
   uint32_t a_vo[INS], b_vo[INS];
   auto set_offsets = [&](int64_t lda, int64_t ldb) {
 #pragma unroll
     for (int i = 0; i < INS; ++i) {
       const int r = (i * NW + wid) * RPI + lrowi;
       const int chunk = slot ^ dma_swz<BK>(r);
-      a_vo[i] = (uint32_t)(((int64_t)min(m0 + r, p.M - 1) * lda + chunk * 8) * 2);
-      b_vo[i] = (uint32_t)(((int64_t)min(n0 + r, p.N - 1) * ldb + chunk * 8) * 2);
+      a_vo[i] = (uint32_t)(((int64_t)min(r, mrows - 1) * lda + chunk * 8) * 2);
+      b_vo[i] = (uint32_t)(((int64_t)min(r, nrows - 1) * ldb + chunk * 8) * 2);
     }
   };
   set_offsets(p.lda, p.ldb);
@@ -874,8 +879,9 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
   // order) and returns its k byte offset.
   auto dma_tile = [&](int t) -> uint32_t {
     if (t == nk1) {
-      ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0), (uint32_t)(((int64_t)(p.M - 1) * p.lda2 + p.K2) * 2));
-      rb = make_rsrc(p.B2, (uint32_t)(((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2));
+      ra = make_rsrc((const bf16_t*)p.A2 + seg_col_of(p, n0) + (int64_t)m0 * p.lda2,
+                     (uint32_t)(((int64_t)(mrows - 1) * p.lda2 + p.K2) * 2));
+      rb = make_rsrc((const bf16_t*)p.B2 + (int64_t)n0 * p.ldb2, (uint32_t)(((int64_t)(nrows - 1) * p.ldb2 + p.K2) * 2));
       set_offsets(p.lda2, p.ldb2);
       kbase = nk1;
     }
@@ -1371,14 +1377,15 @@ static void launch_nt_w4m16(const GemmNT& p0, hipStream_t st) {
   hipLaunchKernelGGL((gemm_nt_bf16_w4m16_kernel<OutT, EPI>), dim3(nb), dim3(256), lds, st, p);
 }
 
-// The 4-wave kernel addresses operands through buffer resources with 32-bit byte offsets and
-// stores 4 output columns per vector (C and R rows aligned to 16 bytes, N a multiple of 4).
+// The 4-wave kernel addresses each tile's operand strips (256 rows from the tile's first) through
+// buffer resources with 32-bit byte offsets and stores 4 output columns per vector (C and R rows
+// aligned to 16 bytes, N a multiple of 4).
 static bool buffer_ranges_ok(const GemmNT& p) {
   const int64_t lim = 0xFFFFFFFFll;
   if (p.N % 4 || p.ldc % 4 || ((uintptr_t)p.C & 15) || (p.R && (p.ldr % 4 || ((uintptr_t)p.R & 15)))) return false;
-  if (((int64_t)(p.M - 1) * p.lda + p.K) * 2 > lim || ((int64_t)(p.N - 1) * p.ldb + p.K) * 2 > lim) return false;
-  if (p.A2 && (((int64_t)(p.M - 1) * p.lda2 + p.K2 + 4096) * 2 > lim || ((int64_t)(p.N - 1) * p.ldb2 + p.K2) * 2 > lim))
-    return false;
+  const int64_t mr = (p.M < 256 ? p.M : 256) - 1, nr = (p.N < 256 ? p.N : 256) - 1;
+  if ((mr * p.lda + p.K) * 2 > lim || (nr * p.ldb + p.K) * 2 > lim) return false;
+  if (p.A2 && ((mr * p.lda2 + p.K2 + 4096) * 2 > lim || (nr * p.ldb2 + p.K2) * 2 > lim)) return false;
   return true;
 }
 
