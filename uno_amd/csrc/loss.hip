@@ -20,6 +20,29 @@
 
 template <typename T> __device__ __forceinline__ float ldf(const T* p) { return Elem<T>::load(p); }
 
+// 16 bytes of a row as floats: 8 bf16 or 4 fp32 values.
+template <typename T> constexpr int VN16 = 16 / (int)sizeof(T);
+template <typename T> __device__ __forceinline__ void ld16(const T* p, float (&v)[VN16<T>]) {
+  const uint4 u = *(const uint4*)p;
+  if constexpr (std::is_same<T, float>::value) {
+    v[0] = __uint_as_float(u.x); v[1] = __uint_as_float(u.y); v[2] = __uint_as_float(u.z); v[3] = __uint_as_float(u.w);
+  } else {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[2 * i] = __uint_as_float(w[i] << 16); v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u); }
+  }
+}
+template <typename T> __device__ __forceinline__ void st16(T* p, const float (&v)[VN16<T>]) {
+  if constexpr (std::is_same<T, float>::value) {
+    *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    *(uint4*)p = make_uint4(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]), pack2_bf16(v[4], v[5]), pack2_bf16(v[6], v[7]));
+  }
+}
+// The row kernels below walk a row 16 bytes per thread and step when every row pointer involved
+// is 16-byte aligned, and the rest of the row (or a misaligned row) one element per thread.
+__device__ __forceinline__ bool al16p(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 // Running softmax statistics of a logits chunk z[R, Vc] (columns c0..c0+Vc of the vocab).
 // One pass over the row: each thread keeps its own (max, sum-exp), rescaled when its max grows,
 // with 16-byte loads for fp32 rows that allow them; the block then merges the pairs.
@@ -162,15 +185,35 @@ template <typename T>
 __global__ __launch_bounds__(256) void softmax_stats_kernel(const T* __restrict__ z, int64_t ldz, int V, float* mx,
                                                             float* se) {
   __shared__ float red[32];
+  constexpr int VN = VN16<T>;
   const int row = blockIdx.x;
   const T* zr = z + (int64_t)row * ldz;
-  float m = -INFINITY;
-  for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, ldf(zr + j));
-  m = block_max(m, red);
-  float s = 0.f;
-  for (int j = threadIdx.x; j < V; j += 256) s += fast_expf(ldf(zr + j) - m);
-  s = block_sum(s, red);
-  if (threadIdx.x == 0) { mx[row] = m; se[row] = fmaxf(s, 1.17549435e-38f); }
+  // One pass: each thread keeps its own (max, sum-exp), rescaled when its max grows, over 16-byte
+  // loads; the block then merges the pairs.
+  float m = -INFINITY, s = 0.f;
+  int j0 = 0;
+  if (al16p(zr)) {
+    const int nv = V / VN;
+    for (int q = threadIdx.x; q < nv; q += 256) {
+      float v[VN];
+      ld16(zr + q * VN, v);
+      float mv = v[0];
+#pragma unroll
+      for (int e = 1; e < VN; ++e) mv = fmaxf(mv, v[e]);
+      if (mv > m) { s *= fast_expf(m - mv); m = mv; }
+#pragma unroll
+      for (int e = 0; e < VN; ++e) s += fast_expf(v[e] - m);
+    }
+    j0 = nv * VN;
+  }
+  for (int j = j0 + threadIdx.x; j < V; j += 256) {
+    const float v = ldf(zr + j);
+    if (v > m) { s = s * fast_expf(m - v) + 1.f; m = v; }   // fast_expf(-inf) = 0 on the first value
+    else s += fast_expf(v - m);
+  }
+  const float mb = block_max(m, red);
+  s = block_sum(m == -INFINITY ? 0.f : s * fast_expf(m - mb), red);
+  if (threadIdx.x == 0) { mx[row] = mb; se[row] = fmaxf(s, 1.17549435e-38f); }
 }
 
 // TV forward: row_l1 = sum |ps - pt|, row_S = sum sign(ps - pt) * ps.
@@ -184,12 +227,26 @@ __global__ __launch_bounds__(256) void tv_fwd_kernel(const T* __restrict__ zs, i
   const T* s = zs + (int64_t)row * lds;
   const T* t = zt + (int64_t)row * ldt;
   float l1 = 0.f, S = 0.f;
-  for (int j = threadIdx.x; j < V; j += 256) {
-    const float ps = fast_expf(ldf(s + j) - a) * ia, pt = fast_expf(ldf(t + j) - b) * ib;
+  auto elem = [&](float zsv, float ztv) {
+    const float ps = fast_expf(zsv - a) * ia, pt = fast_expf(ztv - b) * ib;
     const float d = ps - pt;
     l1 += fabsf(d);
     S += (d > 0.f ? ps : (d < 0.f ? -ps : 0.f));
+  };
+  int j0 = 0;
+  if (al16p(s) && al16p(t)) {
+    constexpr int VN = VN16<T>;
+    const int nv = V / VN;
+    for (int q = threadIdx.x; q < nv; q += 256) {
+      float vs[VN], vt[VN];
+      ld16(s + q * VN, vs);
+      ld16(t + q * VN, vt);
+#pragma unroll
+      for (int e = 0; e < VN; ++e) elem(vs[e], vt[e]);
+    }
+    j0 = nv * VN;
   }
+  for (int j = j0 + threadIdx.x; j < V; j += 256) elem(ldf(s + j), ldf(t + j));
   l1 = block_sum(l1, red);
   S = block_sum(S, red);
   if (threadIdx.x == 0) { row_l1[row] = l1; row_S[row] = S; }
@@ -207,12 +264,27 @@ __global__ __launch_bounds__(256) void tv_bwd_kernel(const T* zs, int64_t lds, c
   const T* s = zs + (int64_t)row * lds;
   const T* t = zt + (int64_t)row * ldt;
   T* gr = grad + (int64_t)row * ldg;
-  for (int j = threadIdx.x; j < V; j += 256) {
-    const float ps = fast_expf(ldf(s + j) - a) * ia, pt = fast_expf(ldf(t + j) - b) * ib;
+  auto elem = [&](float zsv, float ztv) {
+    const float ps = fast_expf(zsv - a) * ia, pt = fast_expf(ztv - b) * ib;
     const float d = ps - pt;
     const float sg = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
-    Elem<T>::store(gr + j, ps * (sg - S) * c);
+    return ps * (sg - S) * c;
+  };
+  int j0 = 0;
+  if (al16p(s) && al16p(t) && al16p(gr)) {   // each thread reads its 16 bytes before writing them
+    constexpr int VN = VN16<T>;
+    const int nv = V / VN;
+    for (int q = threadIdx.x; q < nv; q += 256) {
+      float vs[VN], vt[VN];
+      ld16(s + q * VN, vs);
+      ld16(t + q * VN, vt);
+#pragma unroll
+      for (int e = 0; e < VN; ++e) vs[e] = elem(vs[e], vt[e]);
+      st16(gr + q * VN, vs);
+    }
+    j0 = nv * VN;
   }
+  for (int j = j0 + threadIdx.x; j < V; j += 256) Elem<T>::store(gr + j, elem(ldf(s + j), ldf(t + j)));
 }
 
 // Reverse KL forward: row_kl = sum ps * (ls - lt).
@@ -226,10 +298,24 @@ __global__ __launch_bounds__(256) void kl_fwd_kernel(const T* __restrict__ zs, i
   const T* s = zs + (int64_t)row * lds;
   const T* t = zt + (int64_t)row * ldt;
   float kl = 0.f;
-  for (int j = threadIdx.x; j < V; j += 256) {
-    const float ls = ldf(s + j) - la, lt = ldf(t + j) - lb;
+  auto elem = [&](float zsv, float ztv) {
+    const float ls = zsv - la, lt = ztv - lb;
     kl += fast_expf(ls) * (ls - lt);
+  };
+  int j0 = 0;
+  if (al16p(s) && al16p(t)) {
+    constexpr int VN = VN16<T>;
+    const int nv = V / VN;
+    for (int q = threadIdx.x; q < nv; q += 256) {
+      float vs[VN], vt[VN];
+      ld16(s + q * VN, vs);
+      ld16(t + q * VN, vt);
+#pragma unroll
+      for (int e = 0; e < VN; ++e) elem(vs[e], vt[e]);
+    }
+    j0 = nv * VN;
   }
+  for (int j = j0 + threadIdx.x; j < V; j += 256) elem(ldf(s + j), ldf(t + j));
   kl = block_sum(kl, red);
   if (threadIdx.x == 0) row_kl[row] = kl;
 }
@@ -246,10 +332,25 @@ __global__ __launch_bounds__(256) void kl_bwd_kernel(const T* zs, int64_t lds, c
   const T* s = zs + (int64_t)row * lds;
   const T* t = zt + (int64_t)row * ldt;
   T* gr = grad + (int64_t)row * ldg;
-  for (int j = threadIdx.x; j < V; j += 256) {
-    const float ls = ldf(s + j) - la, lt = ldf(t + j) - lb;
-    Elem<T>::store(gr + j, fast_expf(ls) * ((ls - lt) - k) * c);
+  auto elem = [&](float zsv, float ztv) {
+    const float ls = zsv - la, lt = ztv - lb;
+    return fast_expf(ls) * ((ls - lt) - k) * c;
+  };
+  int j0 = 0;
+  if (al16p(s) && al16p(t) && al16p(gr)) {
+    constexpr int VN = VN16<T>;
+    const int nv = V / VN;
+    for (int q = threadIdx.x; q < nv; q += 256) {
+      float vs[VN], vt[VN];
+      ld16(s + q * VN, vs);
+      ld16(t + q * VN, vt);
+#pragma unroll
+      for (int e = 0; e < VN; ++e) vs[e] = elem(vs[e], vt[e]);
+      st16(gr + q * VN, vs);
+    }
+    j0 = nv * VN;
   }
+  for (int j = j0 + threadIdx.x; j < V; j += 256) Elem<T>::store(gr + j, elem(ldf(s + j), ldf(t + j)));
 }
 
 // out[0] = scale * inv_n * sum x (single workgroup, fixed summation order).
