@@ -54,8 +54,9 @@ def _tied_logits(R, V, dtype, dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_argmax_ties_bit_exact(dev, dtype):
-    R, V = 60, 5003
+@pytest.mark.parametrize("V", [5003, 8192])   # rows at odd offsets (mostly element-wise) / all 16-byte walks
+def test_argmax_ties_bit_exact(dev, dtype, V):
+    R = 60
     z = _tied_logits(R, V, dtype, dev)
     ref = torch.argmax(z.float().cpu(), dim=-1)
     assert torch.equal(logits_argmax(z).cpu(), ref)

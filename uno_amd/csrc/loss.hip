@@ -106,10 +106,24 @@ __global__ __launch_bounds__(256) void row_argmax_update_kernel(const T* __restr
   const T* zr = z + (int64_t)row * ldz;
   float bv = -INFINITY;
   int bi = INT_MAX;                      // INT_MAX: this thread has seen no element
-  for (int j = threadIdx.x; j < Vc; j += 256) {
-    const float v = ldf(zr + j);
+  auto take = [&](float v, int j) {
     if (bi == INT_MAX || argmax_beats(v, j, bv, bi)) { bv = v; bi = j; }
+  };
+  // 16 bytes per thread and step (each thread still visits its columns in increasing order, and
+  // the merge below orders ties by column, so the result is the element-wise walk's)
+  int j0 = 0;
+  if (al16p(zr)) {
+    constexpr int VN = VN16<T>;
+    const int nv = Vc / VN;
+    for (int q = threadIdx.x; q < nv; q += 256) {
+      float v[VN];
+      ld16(zr + q * VN, v);
+#pragma unroll
+      for (int e = 0; e < VN; ++e) take(v[e], q * VN + e);
+    }
+    j0 = nv * VN;
   }
+  for (int j = j0 + threadIdx.x; j < Vc; j += 256) take(ldf(zr + j), j);
   sv[threadIdx.x] = bv;
   si[threadIdx.x] = bi;
   __syncthreads();
