@@ -137,7 +137,8 @@ def test_gemm_tn(dev, Mr, P, Q, dtype):
 
 @pytest.mark.parametrize("Mr,P,Q", [(1000, 192, 4096), (16384, 4096, 64), (777, 1000, 96), (4100, 64, 12288),
                                      (300, 1032, 256), (16384, 128, 4096), (2000, 64, 1000), (2000, 1000, 64),
-                                     (2000, 1000, 128), (16384, 192, 4096), (3000, 4104, 192)])
+                                     (2000, 1000, 128), (16384, 192, 4096), (3000, 4104, 192),
+                                     (4096, 32, 2048), (3000, 5640, 32)])
 def test_gemm_tn_skinny_bf16(dev, Mr, P, Q):
     """LoRA weight-gradient shapes (rank side <= 256 columns): dA = g^T x and dB = dY^T h, with
     ragged row counts and wide sides that are not a multiple of the 128- or 256-column strips."""
