@@ -403,3 +403,29 @@ def test_bf16_rounding_matches_torch(dev):
     # fp32-denormal inputs may be flushed to a signed zero by the hardware conversion
     flushed = diff & denormal
     assert ((mine[flushed] & 0x7FFF) == 0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_transpose_jobs(dev, dtype):
+    """Batched transposes over one flat buffer: sides that are multiples of 8 at 16-byte-aligned
+    offsets (the 16-byte path for bf16) next to ragged sides and odd offsets (the element path)."""
+    from uno_amd import _native as N
+    shapes = [(64, 64), (4096, 32), (32, 4104), (100, 37), (8, 8), (200, 136), (13, 8), (136, 40)]
+    offs, off = [], 0
+    for i, (r, c) in enumerate(shapes):
+        off += 3 if i % 3 == 2 else 0          # every third job starts at an odd element offset
+        offs.append(off)
+        off += r * c
+        off = (off + 7) // 8 * 8
+    src = torch.randn(off, device=dev).to(dtype)
+    dst = torch.full((off,), float("nan"), device=dev, dtype=dtype)
+    jobs, tile = [], 0
+    for (r, c), o in zip(shapes, offs):
+        jobs.append([o, r, c, o, tile, 0, 0, 0])
+        tile += ((r + 63) // 64) * ((c + 63) // 64)
+    jt = torch.tensor(jobs, dtype=torch.int64, device=dev)
+    N.call("unok_transpose_jobs", N.dtype_code(dtype), N.ptr(jt), len(jobs), tile, N.ptr(src), N.ptr(dst), N.stream())
+    torch.cuda.synchronize()
+    for (r, c), o in zip(shapes, offs):
+        want = src[o:o + r * c].view(r, c).t()
+        assert torch.equal(dst[o:o + r * c].view(c, r), want), (r, c, o)

@@ -137,6 +137,32 @@ __global__ __launch_bounds__(256) void transpose_jobs_kernel(const int64_t* __re
   const int64_t r0 = (t / tcols) * 64, c0 = (t % tcols) * 64;
   const T* s = src + j[0];
   T* d = dst + j[3];
+  if constexpr (sizeof(T) == 2) {
+    // bf16 matrices whose sides are multiples of 8 (and 16-byte aligned): 16-byte loads of 8
+    // source columns and 16-byte stores of 8 destination columns, the tile transposed in LDS.
+    if (rows % 8 == 0 && cols % 8 == 0 && (((uintptr_t)s | (uintptr_t)d) & 15) == 0) {
+      __shared__ __attribute__((aligned(16))) T tv[64][72];
+      for (int e = threadIdx.x; e < 64 * 8; e += 256) {
+        const int rr = e / 8, cc = (e % 8) * 8;
+        const int64_t r = r0 + rr, c = c0 + cc;
+        if (r < rows && c < cols) *(uint4*)&tv[rr][cc] = *(const uint4*)(s + r * cols + c);
+      }
+      __syncthreads();
+      for (int e = threadIdx.x; e < 64 * 8; e += 256) {
+        const int cc = e / 8, rr = (e % 8) * 8;
+        const int64_t r = r0 + rr, c = c0 + cc;
+        if (r < rows && c < cols) {
+          uint32_t w[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, tv[rr + 2 * i][cc]) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, tv[rr + 2 * i + 1][cc]) << 16);
+          *(uint4*)(d + c * rows + r) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+      return;
+    }
+  }
   for (int e = threadIdx.x; e < 64 * 64; e += 256) {
     const int rr = e / 64, cc = e % 64;
     const int64_t r = r0 + rr, c = c0 + cc;
