@@ -119,6 +119,10 @@ def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813, total_
         plan = BlockCurriculumPlan.fixed(wl["block_size"], total_steps, L, B)
     trainer = UnoTrainer(model=lm, objective=objective(wl.get("objective", "ce"))[0],
                          curriculum=plan, args=UnoTrainingArguments(learning_rate=1e-4))
+    # compute_loss logs every step through Trainer.log; HF's printer callback would write each
+    # record to stdout, where this script prints only its one JSON line
+    from transformers.trainer_callback import PrinterCallback
+    trainer.remove_callback(PrinterCallback)
     g = torch.Generator(device=device).manual_seed(seed + 2)
     ids = torch.randint(0, cfg.vocab_size - 1, (B, L), device=device, generator=g)
     labels = ids.clone()

@@ -68,12 +68,19 @@ def compute_loss(params, lora, cfg: Cfg, batch: dict, objective: Objective, *, b
 
 def train_steps(params, lora, cfg: Cfg, batch: dict, objective: Objective, *, block_size: int,
                 mask_token_id: int, seed: int, steps: int, lr: float = 1e-4, first_step: int = 0,
-                max_grad_norm: float = 1.0, block_sizes: list[int] | None = None):
+                max_grad_norm: float = 1.0, block_sizes: list[int] | None = None,
+                micro_batches: list[dict] | None = None, grad_accum: int = 1):
     """Runs `steps` optimizer steps; returns (losses, first-step grads, final lora).
 
     `block_sizes[s]`, when given, is the block size of step s (a curriculum that switches block
     size between optimizer steps, training/trainer.py:182-184 with training/curriculum.py:109-112);
-    otherwise every step uses `block_size`."""
+    otherwise every step uses `block_size`.
+
+    With `grad_accum` > 1, optimizer step s accumulates the gradients of `grad_accum` micro-batches
+    (`micro_batches[s * grad_accum + i]`, or `batch` for every one), each loss divided by
+    `grad_accum` as HF's Trainer does when the model takes no loss kwargs
+    (training/trainer.py:161 sets model_accepts_loss_kwargs = False); each micro-batch draws the
+    next noise step. `losses` then holds every micro-batch's unscaled loss, in order."""
     leaves = {k: v.detach().clone().float().requires_grad_(True) for k, v in lora.items()}
     opt = torch.optim.AdamW(list(leaves.values()), lr=lr, betas=(0.9, 0.999), eps=1e-8,
                             weight_decay=0.0)
@@ -81,12 +88,18 @@ def train_steps(params, lora, cfg: Cfg, batch: dict, objective: Objective, *, bl
     for s in range(steps):
         opt.zero_grad(set_to_none=True)
         bs = block_sizes[s] if block_sizes is not None else block_size
-        loss, _ = compute_loss(params, leaves, cfg, batch, objective, block_size=bs,
-                               mask_token_id=mask_token_id, seed=seed, step=first_step + s)
-        loss.backward()
+        for i in range(grad_accum):
+            j = s * grad_accum + i
+            mb = micro_batches[j] if micro_batches is not None else batch
+            loss, _ = compute_loss(params, leaves, cfg, mb, objective, block_size=bs,
+                                   mask_token_id=mask_token_id, seed=seed, step=first_step + j)
+            (loss / grad_accum if grad_accum > 1 else loss).backward()
+            if grad_accum > 1:
+                hist.append(float(loss.detach()))
         if first_grads is None:
             first_grads = {k: v.grad.detach().clone() for k, v in leaves.items()}
         torch.nn.utils.clip_grad_norm_(list(leaves.values()), max_grad_norm)
         opt.step()
-        hist.append(float(loss.detach()))
+        if grad_accum == 1:
+            hist.append(float(loss.detach()))
     return hist, first_grads, {k: v.detach() for k, v in leaves.items()}

@@ -20,6 +20,7 @@ from uno_amd.training.curriculum import BlockCurriculumPlan
 from uno_amd.training.data import UnoDataCollator
 from uno_amd.training.lora import create_lora_model
 from uno_amd.training.trainer import UnoTrainer, UnoTrainingArguments
+from transformers import TrainerCallback
 
 pytestmark = pytest.mark.gpu
 
@@ -68,6 +69,37 @@ def _compare(lm, final, tol=1e-3):
     assert worst < tol
 
 
+STEP_KEYS = ("train/ce_loss", "train/reverse_kl_loss", "train/tv_loss", "train/combined_loss", "train/alpha",
+             "train/beta", "train/gamma", "train/block_size", "train/transformer_forwards")
+
+
+class _LogRecorder(TrainerCallback):
+    """Records what HF hands to on_log (the path W&B and other reporters take)."""
+
+    def __init__(self):
+        self.logs = []
+
+    def on_log(self, args, state, control, logs=None, **kwargs):
+        self.logs.append(dict(logs or {}))
+
+
+def _check_step_logs(trainer, seen, steps, accum):
+    """compute_loss logs the reference's per-step keys through Trainer.log (training/trainer.py:288-300):
+    one entry per micro-batch in state.log_history (with the global step it ran in) and in on_log."""
+    hist = [r for r in trainer.state.log_history if "train/combined_loss" in r]
+    cb = [r for r in seen.logs if "train/combined_loss" in r]
+    assert len(hist) == len(cb) == steps * accum
+    for i, r in enumerate(hist):
+        assert set(STEP_KEYS) <= set(r)
+        assert r["step"] == i // accum
+        assert r["train/block_size"] == SPEC["block"] and r["train/transformer_forwards"] == 1
+        assert (r["train/alpha"], r["train/beta"], r["train/gamma"]) == (1.0, 0.0, 0.0)
+        assert r["train/ce_loss"] == r["train/combined_loss"] and r["train/tv_loss"] == 0.0
+        assert all(isinstance(r[k], (int, float)) for k in STEP_KEYS)
+    assert [r["train/combined_loss"] for r in cb] == [r["train/combined_loss"] for r in hist]
+    return [r["train/combined_loss"] for r in hist]
+
+
 def test_torch_adamw_over_lm_parameters(dev, tmp_path):
     print("[drop-in] torch.optim.AdamW over lm.parameters()", flush=True)
     ocfg, params, lora, batch, lm = _fixture(dev, B=2)
@@ -104,14 +136,15 @@ def test_hf_trainer_train_reference_constructor(dev, tmp_path):
     dataset = [{"input_ids": batch["input_ids"][0].tolist(), "labels": batch["labels"][0].tolist()}]
     args = UnoTrainingArguments(output_dir=str(tmp_path), max_steps=STEPS, per_device_train_batch_size=1,
                                 learning_rate=1e-4, logging_strategy="no", dataloader_num_workers=0)
+    seen = _LogRecorder()
     trainer = UnoTrainer(model=lm, args=args, train_dataset=dataset,
                          data_collator=UnoDataCollator(Tok(), sequence_length=SPEC["L"]), objective=OBJ[0],
-                         curriculum=BlockCurriculumPlan.fixed(SPEC["block"], STEPS, SPEC["L"], 1))
+                         curriculum=BlockCurriculumPlan.fixed(SPEC["block"], STEPS, SPEC["L"], 1), callbacks=[seen])
     trainer.train()
     torch.cuda.synchronize()
     assert trainer.state.global_step == STEPS
     losses, final = _oracle(ocfg, params, lora, batch)
-    mine = [r["train/combined_loss"] for r in trainer.logged()]
+    mine = _check_step_logs(trainer, seen, STEPS, 1)
     print(f"   losses {mine} vs oracle {losses}", flush=True)
     for a, b in zip(mine, losses):
         assert abs(a - b) / abs(b) < 1e-4
@@ -143,3 +176,75 @@ def test_gradient_edits_are_adopted(dev, tmp_path):
     assert torch.allclose(g[names[0]].grad, base[names[0]] + 3.0, rtol=1e-5, atol=1e-6)
     assert torch.allclose(g[names[1]].grad, base[names[1]], rtol=1e-5, atol=1e-7)
     assert torch.allclose(g[names[2]].grad, 2 * base[names[2]], rtol=1e-5, atol=1e-7)
+
+
+def test_hf_trainer_gradient_accumulation(dev, tmp_path):
+    """HF train() with gradient_accumulation_steps=4 over four different rows: each optimizer step
+    sums four micro-batch gradients, each loss divided by 4 (the reference trainer's
+    model_accepts_loss_kwargs = False, training/trainer.py:161), every micro-batch draws the next
+    noise step, and every micro-batch logs its losses. The rows reach compute_loss in the order of
+    HF's shuffling sampler; the oracle replays that order."""
+    print("[drop-in] UnoTrainer.train() with gradient_accumulation_steps=4", flush=True)
+    accum = 4
+    ocfg, params, lora, batch, lm = _fixture(dev, B=accum)
+
+    class Tok:
+        pad_token_id = 0
+        padding_side = "right"
+
+    class Recording(UnoTrainer):
+        order = []
+
+        def compute_loss(self, model, inputs, return_outputs=False, num_items_in_batch=None):
+            self.order.append(inputs["input_ids"].detach().cpu().clone())
+            return super().compute_loss(model, inputs, return_outputs, num_items_in_batch)
+
+    dataset = [{"input_ids": batch["input_ids"][b].tolist(), "labels": batch["labels"][b].tolist()}
+               for b in range(accum)]
+    args = UnoTrainingArguments(output_dir=str(tmp_path), max_steps=STEPS, per_device_train_batch_size=1,
+                                gradient_accumulation_steps=accum, learning_rate=1e-4, logging_strategy="no",
+                                dataloader_num_workers=0)
+    seen = _LogRecorder()
+    trainer = Recording(model=lm, args=args, train_dataset=dataset,
+                        data_collator=UnoDataCollator(Tok(), sequence_length=SPEC["L"]), objective=OBJ[0],
+                        curriculum=BlockCurriculumPlan.fixed(SPEC["block"], STEPS, SPEC["L"], accum),
+                        callbacks=[seen])
+    trainer.train()
+    torch.cuda.synchronize()
+    assert trainer.state.global_step == STEPS
+    assert len(trainer.order) == STEPS * accum
+    rows = {tuple(batch["input_ids"][b].tolist()): b for b in range(accum)}
+    micro = []
+    for ids in trainer.order:
+        b = rows[tuple(ids[0].tolist())]
+        micro.append({"input_ids": batch["input_ids"][b:b + 1], "labels": batch["labels"][b:b + 1]})
+    print(f"   row order {[rows[tuple(i[0].tolist())] for i in trainer.order]}", flush=True)
+    losses, _, final = ostep.train_steps(params, lora, ocfg, batch, OBJ[1], block_size=SPEC["block"],
+                                         mask_token_id=ocfg.vocab_size - 1, seed=20260813, steps=STEPS, lr=1e-4,
+                                         micro_batches=micro, grad_accum=accum)
+    mine = _check_step_logs(trainer, seen, STEPS, accum)
+    print(f"   losses {mine} vs oracle {losses}", flush=True)
+    for a, b in zip(mine, losses):
+        assert abs(a - b) / abs(b) < 1e-4
+    _compare(lm, final)
+
+
+def test_ce_only_batch_without_ce_rows_backpropagates(dev, tmp_path):
+    """A CE-only objective on a micro-batch with no CE rows (every label -100) still returns a loss
+    connected to the graph, as the reference's noisy_hidden.sum() * 0.0 (training/trainer.py:249):
+    backward() runs and leaves every LoRA gradient at zero."""
+    print("[drop-in] CE-only step on a batch with no CE rows", flush=True)
+    _, _, _, batch, lm = _fixture(dev, B=2)
+    trainer = UnoTrainer(model=lm, objective=OBJ[0],
+                         curriculum=BlockCurriculumPlan.fixed(SPEC["block"], 100, SPEC["L"], 2),
+                         args=UnoTrainingArguments(output_dir=str(tmp_path), learning_rate=1e-4))
+    gb = {k: v.to(dev) for k, v in batch.items()}
+    gb["labels"] = torch.full_like(gb["labels"], -100)
+    loss = trainer.compute_loss(lm, gb)
+    assert loss.requires_grad and loss.grad_fn is not None
+    loss.backward()
+    torch.cuda.synchronize()
+    assert loss.item() == 0.0
+    for name, p in lm.lora_tensors().items():
+        assert p.grad is not None and torch.count_nonzero(p.grad).item() == 0, name
+    assert trainer.state.log_history[-1]["train/ce_loss"] == 0.0

@@ -344,6 +344,46 @@ def test_distribution_losses_match_oracle(dev, kind, dtype, V):
     assert rel(sv.grad.cpu(), so.grad) < (1e-4 if dtype == torch.float32 else 1e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_distribution_losses_rows_with_neg_inf(dev, dtype):
+    """Rows holding -inf logits, where a thread's first 16-byte groups are all -inf (the first 2048
+    columns), scattered -inf columns, and -inf at the same column on both sides (p = q = 0, sign 0):
+    TV stays finite and matches the reference's chunked algorithm, which takes the row max before any
+    exponential (training/losses.py:76-160); reverse KL is NaN exactly where the reference's
+    F.kl_div(log_target=True) is (0 * -inf at a -inf student column)."""
+    from uno_amd.training.losses import token_normalized_reverse_kl, token_normalized_total_variation
+    torch.manual_seed(7)
+    R, V = 24, 8200
+    s = torch.randn(R, V) * 2
+    t = torch.randn(R, V) * 2
+    s[0, :2048] = -float("inf")
+    t[1, :2048] = -float("inf")
+    s[2, :2048] = t[2, :2048] = -float("inf")
+    s[3, 5000:5100] = -float("inf")
+    s[4, ::7] = -float("inf")
+    t[4, ::7] = -float("inf")
+    s, t = s.to(dtype), t.to(dtype)
+    sv = s.to(dev).requires_grad_(True)
+    val = token_normalized_total_variation(sv, t.to(dev), 11)
+    val.backward()
+    ref, ref_grad = olosses.chunked_tv_reference_algorithm(s.float(), t.float(), 11)
+    print(f"[-inf rows] TV {val.item():.6f} vs reference algorithm {ref.item():.6f}", flush=True)
+    assert torch.isfinite(val).item() and torch.isfinite(sv.grad).all().item()
+    assert abs(val.item() - ref.item()) / abs(ref.item()) < (1e-5 if dtype == torch.float32 else 1e-4)
+    assert rel(sv.grad.float().cpu(), ref_grad) < (1e-4 if dtype == torch.float32 else 1e-2)
+    # reverse KL per row: the reference's value is NaN on rows 0, 2, 3, 4 (student -inf columns)
+    for r in range(6):
+        kv = token_normalized_reverse_kl(s[r:r + 1].to(dev), t[r:r + 1].to(dev), 1).item()
+        kr = torch.nn.functional.kl_div(torch.log_softmax(t[r:r + 1].float(), -1),
+                                        torch.log_softmax(s[r:r + 1].float(), -1), log_target=True,
+                                        reduction="sum").item()
+        assert (kv != kv) == (kr != kr), (r, kv, kr)
+        if math.isfinite(kr):
+            assert abs(kv - kr) <= 1e-4 * max(1.0, abs(kr)), (r, kv, kr)
+        elif kr == kr:
+            assert kv == kr, (r, kv, kr)     # +inf: a -inf teacher column under a live student one
+
+
 # ------------------------------------------------------------------------------------------
 # Optimizer
 # ------------------------------------------------------------------------------------------

@@ -48,15 +48,19 @@ class _Slot:
 class LoraState:
     def __init__(self, cfg, rank: int, alpha: float, device, compute_dtype: torch.dtype,
                  targets=MODULES):
-        if tuple(sorted(targets)) != tuple(sorted(MODULES)):
-            raise NotImplementedError(
-                "The fused MI355X path adapts all seven projections (q,k,v,o,gate,up,down); "
-                f"got targets {tuple(targets)}.")
+        targets = tuple(targets)
+        unknown = [t for t in targets if t not in MODULES]
+        if not targets or unknown or len(set(targets)) != len(targets):
+            raise ValueError(f"LoRA targets must be distinct names from {list(MODULES)}; got {list(targets)}.")
         self.cfg = cfg
         self.rank = int(rank)
         self.alpha = float(alpha)
         self.scale = self.alpha / self.rank
-        self.targets = tuple(MODULES)
+        # Every projection keeps its slot in the flat layout, so each fused group's adapters stay
+        # contiguous; an untargeted projection's slot holds zeros and is never exposed as a
+        # parameter. Its forward term s B (x A^T) and its gradients are then exactly zero, and
+        # AdamW (no weight decay on a zero weight, zero moments) keeps it at zero.
+        self.targets = targets
         self.compute_dtype = compute_dtype
         self.device = torch.device(device)
         dims = module_dims(cfg)
@@ -94,6 +98,14 @@ class LoraState:
         # autograd anchor: the decoder's stream Functions take it as an input so that backward
         # runs; the LoRA gradients are accumulated straight into ``grad`` by the kernels.
         self.anchor = torch.zeros(1, **f32).requires_grad_(True)
+
+    # ---- targets ----------------------------------------------------------------------
+    def is_target(self, name: str) -> bool:
+        return name in self.targets
+
+    def group_active(self, group: str) -> bool:
+        """Whether any projection of a fused group carries an adapter."""
+        return any(n in self.targets for n in GROUPS[group])
 
     # ---- views of the fp32 master / grad ----------------------------------------------
     def a_view(self, buf: torch.Tensor, layer: int, name: str) -> torch.Tensor:

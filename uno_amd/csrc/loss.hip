@@ -54,9 +54,11 @@ __global__ __launch_bounds__(256) void row_lse_update_kernel(const T* __restrict
   const int row = blockIdx.x;
   const T* zr = z + (int64_t)row * ldz;
   float m = -INFINITY, s = 0.f;
+  // A -inf value adds nothing; skipping it also keeps exp(-inf - -inf) = NaN out of the sum while
+  // this thread has seen nothing else.
   auto add = [&](float v) {
     if (v > m) { s = s * fast_expf(m - v) + 1.f; m = v; }   // fast_expf(-inf) = 0 on the first value
-    else s += fast_expf(v - m);
+    else if (v != -INFINITY) s += fast_expf(v - m);
   };
   int j0 = 0;
   if constexpr (std::is_same<T, float>::value) {
@@ -65,6 +67,7 @@ __global__ __launch_bounds__(256) void row_lse_update_kernel(const T* __restrict
       for (int q = threadIdx.x; q < nv; q += 256) {
         const float4 v = *(const float4*)(zr + 4 * q);
         const float mv = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+        if (mv == -INFINITY) continue;   // four -inf values add nothing
         if (mv > m) { s *= fast_expf(m - mv); m = mv; }
         s += fast_expf(v.x - m) + fast_expf(v.y - m) + fast_expf(v.z - m) + fast_expf(v.w - m);
       }
@@ -214,6 +217,7 @@ __global__ __launch_bounds__(256) void softmax_stats_kernel(const T* __restrict_
       float mv = v[0];
 #pragma unroll
       for (int e = 1; e < VN; ++e) mv = fmaxf(mv, v[e]);
+      if (mv == -INFINITY) continue;   // a group of -inf values adds nothing (and m may still be -inf)
       if (mv > m) { s *= fast_expf(m - mv); m = mv; }
 #pragma unroll
       for (int e = 0; e < VN; ++e) s += fast_expf(v[e] - m);
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(256) void softmax_stats_kernel(const T* __restrict_
   for (int j = j0 + threadIdx.x; j < V; j += 256) {
     const float v = ldf(zr + j);
     if (v > m) { s = s * fast_expf(m - v) + 1.f; m = v; }   // fast_expf(-inf) = 0 on the first value
-    else s += fast_expf(v - m);
+    else if (v != -INFINITY) s += fast_expf(v - m);
   }
   const float mb = block_max(m, red);
   s = block_sum(m == -INFINITY ? 0.f : s * fast_expf(m - mb), red);

@@ -105,27 +105,31 @@ def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: St
     recompute policy relies on. ``need_output=False`` (recompute) skips the down projection's output."""
     r = lora.rank
     q_end, k_end = g.q, g.q + g.kv
+    on = lora.group_active     # a fused group with no adapter runs as a plain product
     x1, rstd1 = K.rmsnorm_fwd(h0, lw.ln_in, g.eps)
-    h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv"))
-    qkv = K.gemm_nt(x1, lw.w_qkv, a2=h_qkv, b2=lora.sb_c(li, "qkv"),
-                    segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)])
+    h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv")) if on("qkv") else None
+    qkv = K.gemm_nt(x1, lw.w_qkv, a2=h_qkv, b2=lora.sb_c(li, "qkv") if on("qkv") else None,
+                    segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)] if on("qkv") else None)
     q, k, rstd_qk = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
     v = qkv[:, k_end:]
     o, lse = K.attn_fwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, g.nq, g.nk, g.d, k2=k, v2=v)
-    h_o = K.gemm_nt(o, lora.a_c(li, "o"))
-    h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o"), residual=h0)
+    h_o = K.gemm_nt(o, lora.a_c(li, "o")) if on("o") else None
+    h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o") if on("o") else None, residual=h0)
     x2, rstd2 = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
-    h_gu = K.gemm_nt(x2, lora.a_c(li, "gu"))
-    sb_gu_i = lora.sb_gu_i(li) if lw.w_gu_i is not None and x2.dtype == torch.bfloat16 else None
-    if sb_gu_i is not None and (2 * r) % 32 == 0 and K.swiglu_fused_ok(x2.shape[0], g.F, x2.shape[1]):
+    h_gu = K.gemm_nt(x2, lora.a_c(li, "gu")) if on("gu") else None
+    fused = lw.w_gu_i is not None and x2.dtype == torch.bfloat16 and K.swiglu_fused_ok(x2.shape[0], g.F, x2.shape[1])
+    sb_gu_i = lora.sb_gu_i(li) if fused and on("gu") else None
+    if fused and (not on("gu") or (sb_gu_i is not None and (2 * r) % 32 == 0)):
         # gate/up product with its LoRA terms, SwiGLU in the epilogue; [gate | up] kept for backward
         gu = torch.empty((x2.shape[0], 2 * g.F), device=x2.device, dtype=x2.dtype)
         s = K.gemm_nt_swiglu(x2, lw.w_gu_i, a2=h_gu, b2_interleaved=sb_gu_i, gu=gu)
     else:
-        gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu"), segments=[(g.F, 0), (2 * g.F, r)])
+        gu = K.gemm_nt(x2, lw.w_gu, a2=h_gu, b2=lora.sb_c(li, "gu") if on("gu") else None,
+                       segments=[(g.F, 0), (2 * g.F, r)] if on("gu") else None)
         s = K.swiglu_fwd(gu, g.F)
-    h_d = K.gemm_nt(s, lora.a_c(li, "d"))
-    h2 = K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d"), residual=h1) if need_output else None
+    h_d = K.gemm_nt(s, lora.a_c(li, "d")) if on("d") else None
+    h2 = K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d") if on("d") else None, residual=h1) \
+        if need_output else None
     return h2, (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d)
 
 
@@ -133,6 +137,27 @@ def saved_bytes_per_row(g: Geometry, rank: int, elem: int) -> int:
     """Bytes of activations one noisy-stream layer keeps per token row for its backward."""
     stored = 4 * g.H + (g.q + 2 * g.kv) + g.q + g.kv + g.q + 3 * g.F + 7 * rank
     return stored * elem + 4 * (2 + g.nq + g.nk + g.nq)
+
+
+def _lora_inner_grads(lora, li: int, group: str, dy, h, cols, scale):
+    """For a fused group [c0, c1) column ranges of its output gradient dy: the inner gradients
+    g = dy (s B) (columns of the returned [M, parts * r]) and dB += s dy^T h. Projections without
+    an adapter get zero columns (their A rows are zero, so g A adds nothing, but unset memory
+    could hold non-finite values) and no weight gradient. None when the group has no adapter."""
+    from .adapter import GROUPS
+    if not lora.group_active(group):
+        return None
+    r = lora.rank
+    out = torch.empty((dy.shape[0], len(cols) * r), device=dy.device, dtype=dy.dtype)
+    sbt = lora.sb_t(li, group)
+    gbg = lora.grad_b(li, group)
+    for j, ((c0, c1), name) in enumerate(zip(cols, GROUPS[group])):
+        if not lora.is_target(name):
+            out[:, j * r:(j + 1) * r].zero_()
+            continue
+        K.gemm_nt(dy[:, c0:c1], sbt[:, c0:c1], out=out[:, j * r:(j + 1) * r])
+        K.gemm_tn(dy[:, c0:c1], h[:, j * r:(j + 1) * r], out=gbg[c0:c1], alpha=scale, beta=1.0)
+    return out
 
 
 class NoisyLayer(torch.autograd.Function):
@@ -164,34 +189,36 @@ class NoisyLayer(torch.autograd.Function):
         r, sc_l = lora.rank, lora.scale
         q_end, k_end = g.q, g.q + g.kv
         ga, gb = lora.grad_a, lora.grad_b
+        on = lora.group_active
         # ---- down projection ----------------------------------------------------------
-        g_d = K.gemm_nt(dh2, lora.sb_t(li, "d"))                              # [M, r]
-        K.gemm_tn(dh2, h_d, out=gb(li, "d"), alpha=sc_l, beta=1.0)            # dB_d
+        g_d = K.gemm_nt(dh2, lora.sb_t(li, "d")) if on("d") else None                 # [M, r]
+        if on("d"):
+            K.gemm_tn(dh2, h_d, out=gb(li, "d"), alpha=sc_l, beta=1.0)                # dB_d
+        a_t_d = lora.a_t(li, "d") if on("d") else None
         if dh2.dtype == torch.bfloat16 and M % 256 == 0 and g.F % 256 == 0 and g.H % 64 == 0 and r % 32 == 0:
             # dS = dh2 W_d + g_d A_d never leaves the GEMM: its epilogue applies the SwiGLU backward
-            dgu = K.gemm_nt_swiglu_bwd(dh2, lw.w_d_t, g_d, lora.a_t(li, "d"), gu)
+            dgu = K.gemm_nt_swiglu_bwd(dh2, lw.w_d_t, g_d, a_t_d, gu)
         else:
-            ds = K.gemm_nt(dh2, lw.w_d_t, a2=g_d, b2=lora.a_t(li, "d"))       # [M, F]
+            ds = K.gemm_nt(dh2, lw.w_d_t, a2=g_d, b2=a_t_d)                            # [M, F]
             dgu = K.swiglu_bwd(ds, gu, g.F)
             del ds
-        K.gemm_tn(g_d, s, out=ga(li, "d"), beta=1.0)                          # dA_d
+        if on("d"):
+            K.gemm_tn(g_d, s, out=ga(li, "d"), beta=1.0)                              # dA_d
         # ---- gate | up -----------------------------------------------------------------
-        g_gu = torch.empty((M, 2 * r), device=dh2.device, dtype=dh2.dtype)
-        sbt = lora.sb_t(li, "gu")
-        gbgu = gb(li, "gu")
-        for j, (c0, c1) in enumerate(((0, g.F), (g.F, 2 * g.F))):
-            K.gemm_nt(dgu[:, c0:c1], sbt[:, c0:c1], out=g_gu[:, j * r:(j + 1) * r])
-            K.gemm_tn(dgu[:, c0:c1], h_gu[:, j * r:(j + 1) * r], out=gbgu[c0:c1], alpha=sc_l, beta=1.0)
-        dx2 = K.gemm_nt(dgu, lw.w_gu_t, a2=g_gu, b2=lora.a_t(li, "gu"))
-        K.gemm_tn(g_gu, x2, out=ga(li, "gu"), beta=1.0)
+        g_gu = _lora_inner_grads(lora, li, "gu", dgu, h_gu, ((0, g.F), (g.F, 2 * g.F)), sc_l)
+        dx2 = K.gemm_nt(dgu, lw.w_gu_t, a2=g_gu, b2=lora.a_t(li, "gu") if on("gu") else None)
+        if on("gu"):
+            K.gemm_tn(g_gu, x2, out=ga(li, "gu"), beta=1.0)
         del dgu
         dh1 = K.rmsnorm_bwd(dx2, h1, lw.ln_post, rstd2, dres=dh2)
         del dx2
         # ---- o projection --------------------------------------------------------------
-        g_o = K.gemm_nt(dh1, lora.sb_t(li, "o"))
-        K.gemm_tn(dh1, h_o, out=gb(li, "o"), alpha=sc_l, beta=1.0)
-        do = K.gemm_nt(dh1, lw.w_o_t, a2=g_o, b2=lora.a_t(li, "o"))
-        K.gemm_tn(g_o, o, out=ga(li, "o"), beta=1.0)
+        g_o = K.gemm_nt(dh1, lora.sb_t(li, "o")) if on("o") else None
+        if on("o"):
+            K.gemm_tn(dh1, h_o, out=gb(li, "o"), alpha=sc_l, beta=1.0)
+        do = K.gemm_nt(dh1, lw.w_o_t, a2=g_o, b2=lora.a_t(li, "o") if on("o") else None)
+        if on("o"):
+            K.gemm_tn(g_o, o, out=ga(li, "o"), beta=1.0)
         # ---- attention -----------------------------------------------------------------
         dqkv = torch.empty_like(qkv)
         dk = torch.empty((M, g.kv), device=dh2.device, dtype=dh2.dtype)
@@ -201,16 +228,13 @@ class NoisyLayer(torch.autograd.Function):
         K.qknorm_rope_bwd(dq, dk, qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, rstd_qk, dqkv)
         del dq, dk
         # ---- q | k | v -----------------------------------------------------------------
-        g_qkv = torch.empty((M, 3 * r), device=dh2.device, dtype=dh2.dtype)
-        sbt = lora.sb_t(li, "qkv")
-        gbqkv = gb(li, "qkv")
-        for j, (c0, c1) in enumerate(((0, q_end), (q_end, k_end), (k_end, k_end + g.kv))):
-            K.gemm_nt(dqkv[:, c0:c1], sbt[:, c0:c1], out=g_qkv[:, j * r:(j + 1) * r])
-            K.gemm_tn(dqkv[:, c0:c1], h_qkv[:, j * r:(j + 1) * r], out=gbqkv[c0:c1], alpha=sc_l, beta=1.0)
-        K.gemm_tn(g_qkv, x1, out=ga(li, "qkv"), beta=1.0)
+        g_qkv = _lora_inner_grads(lora, li, "qkv", dqkv, h_qkv, ((0, q_end), (q_end, k_end), (k_end, k_end + g.kv)),
+                                  sc_l)
+        if on("qkv"):
+            K.gemm_tn(g_qkv, x1, out=ga(li, "qkv"), beta=1.0)
         dh0 = None
         if ctx.needs_input_grad[0]:
-            dx1 = K.gemm_nt(dqkv, lw.w_qkv_t, a2=g_qkv, b2=lora.a_t(li, "qkv"))
+            dx1 = K.gemm_nt(dqkv, lw.w_qkv_t, a2=g_qkv, b2=lora.a_t(li, "qkv") if on("qkv") else None)
             dh0 = K.rmsnorm_bwd(dx1, h0, lw.ln_in, rstd1, dres=dh1)
         return dh0, None, None, None, None, None, None, None
 

@@ -554,17 +554,17 @@ class UnoLoraModel(nn.Module):
     named ``base_model.model.model.layers.N.{self_attn,mlp}.X_proj.lora_{A,B}.default.weight``."""
 
     def __init__(self, base: UnoQwen3ForCausalLM, rank: int, alpha: float, dropout: float = 0.0,
-                 init: str = "gaussian_b", seed: int = 0, b_std: float = 0.02):
+                 init: str = "gaussian_b", seed: int = 0, b_std: float = 0.02, targets=MODULES):
         super().__init__()
         if dropout != 0.0:
             raise NotImplementedError("LoRA dropout is not supported by the fused path (Uno uses 0.0).")
         self.base_model = LoraAdapterModel(base)
-        self.state = LoraState(base.config, rank, alpha, base.device, base.dtype)
+        self.state = LoraState(base.config, rank, alpha, base.device, base.dtype, targets=targets)
         self.state.token_mask = None
         base.model._uno_lora = self.state
         st = self.state
         for li, layer in enumerate(base.model.layers):
-            for name in MODULES:
+            for name in st.targets:
                 mod = getattr(layer.self_attn if name in ("q_proj", "k_proj", "v_proj", "o_proj") else layer.mlp, name)
                 mod.lora_A = nn.ModuleDict({"default": _LoraWeight(st.a_view(st.master, li, name),
                                                                    st.a_view(st.grad, li, name), st)})
@@ -581,7 +581,7 @@ class UnoLoraModel(nn.Module):
         st = self.state
         gen = torch.Generator(device=st.device).manual_seed(seed)
         for li in range(len(st.slots)):
-            for name in MODULES:
+            for name in st.targets:
                 a = st.a_view(st.master, li, name)
                 bound = 1.0 / a.shape[1] ** 0.5
                 a.uniform_(-bound, bound, generator=gen)

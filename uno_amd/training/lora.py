@@ -23,34 +23,39 @@ _LETTER_TARGETS = {"q": "q_proj", "k": "k_proj", "v": "v_proj", "o": "o_proj"}
 
 def resolve_lora_targets(specification: str) -> tuple[str, ...]:
     """Projection names from a target specification: "all", a string of attention letters
-    ("qv", "qkvo"), or a comma-separated list of projection names."""
+    ("qv", "qkvo"), or a comma-separated list of projection names. Errors and their text follow
+    training/lora.py:14-43."""
     text = specification.strip().lower()
     if text == "all":
         return tuple(SUPPORTED_LORA_MODULES)
     if text and set(text) <= _LETTER_TARGETS.keys():
-        names = [_LETTER_TARGETS[c] for c in text]
-    else:
-        names = [part.strip() for part in specification.split(",") if part.strip()]
-        if not names:
-            raise ValueError(f"No LoRA targets in {specification!r}.")
-        unknown = [n for n in names if n not in SUPPORTED_LORA_MODULES]
-        if unknown:
-            raise ValueError(f"Unknown LoRA target(s) {unknown}; choose from {list(SUPPORTED_LORA_MODULES)}.")
-    if len(names) != len(set(names)):
-        raise ValueError(f"LoRA targets repeat in {specification!r}.")
-    return tuple(names)
+        if len(set(text)) != len(text):
+            raise ValueError(f"LoRA target shorthand contains duplicates: {specification!r}.")
+        return tuple(_LETTER_TARGETS[c] for c in text)
+    names = tuple(part.strip() for part in specification.split(",") if part.strip())
+    if not names:
+        raise ValueError("LoRA targets cannot be empty.")
+    unknown = sorted(set(names) - set(SUPPORTED_LORA_MODULES))
+    if unknown:
+        raise ValueError(f"Unsupported LoRA target(s): {unknown}. Supported projection names are "
+                         f"{list(SUPPORTED_LORA_MODULES)}.")
+    if len(set(names)) != len(names):
+        raise ValueError(f"LoRA target list contains duplicates: {specification!r}.")
+    return names
 
 
 def validate_target_modules(model, targets: Iterable[str]) -> dict[str, int]:
-    """Every target must name exactly one module per decoder layer; returns the counts."""
+    """Every target must name exactly one module per decoder layer; returns the counts
+    (training/lora.py:46-63)."""
     layers = getattr(getattr(model, "config", None), "num_hidden_layers", None)
     if type(layers) is not int or layers <= 0:
-        raise RuntimeError("The base model config must give a positive num_hidden_layers.")
+        raise RuntimeError("The base model must declare config.num_hidden_layers.")
     leaf_names = Counter(name.rsplit(".", 1)[-1] for name, _ in model.named_modules() if name)
     counts = {t: leaf_names.get(t, 0) for t in targets}
     off = {t: c for t, c in counts.items() if c != layers}
     if off:
-        raise RuntimeError(f"LoRA targets must occur once in each of the {layers} layers; found {off}.")
+        raise RuntimeError("Requested LoRA projections are not present exactly once per transformer "
+                           f"layer (expected {layers} each): {off}.")
     return counts
 
 
@@ -61,9 +66,8 @@ def create_lora_model(model, settings: LoraSettings, *, init: str = "gaussian_b"
     settings.validate()
     targets = resolve_lora_targets(settings.target)
     validate_target_modules(model, targets)
-    lora_model = UnoLoraModel(model, settings.rank, settings.resolved_alpha, settings.dropout, init=init, seed=seed)
-    if tuple(sorted(targets)) != tuple(sorted(lora_model.state.targets)):
-        raise NotImplementedError(f"targets {targets} are not supported by the fused path")
+    lora_model = UnoLoraModel(model, settings.rank, settings.resolved_alpha, settings.dropout, init=init, seed=seed,
+                              targets=targets)
     validate_only_lora_trainable(lora_model)
     return lora_model, targets
 
@@ -73,10 +77,10 @@ def validate_only_lora_trainable(model) -> tuple[int, int]:
     params = list(model.named_parameters())
     trainable = [(n, p) for n, p in params if p.requires_grad]
     if not trainable:
-        raise RuntimeError("The model has no trainable LoRA tensors.")
+        raise RuntimeError("No trainable LoRA tensors were found.")
     other = [n for n, _ in trainable if "lora_A" not in n and "lora_B" not in n]
     if other:
-        raise RuntimeError(f"Only LoRA A/B tensors may be trainable; also trainable: {other[:5]}.")
+        raise RuntimeError(f"Only LoRA A/B tensors may be trainable; found {other[:5]}.")
     return sum(p.numel() for _, p in trainable), sum(p.numel() for _, p in params)
 
 

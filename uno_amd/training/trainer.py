@@ -165,7 +165,6 @@ class UnoTrainer(Trainer):
         self.curriculum = curriculum
         validate_uno_model(self.model)
         self._lora_router = TokenwiseLoraRouter(self.model)
-        self._step_metrics: list[dict] = []
         self.add_callback(SchedulerSyncCallback())
         self.add_callback(CurriculumCheckpointCallback(curriculum))
 
@@ -228,7 +227,9 @@ class UnoTrainer(Trainer):
         token_count, ce_count = (int(x) for x in torch.stack([supervised_mask.sum(), ce_mask.sum()]).tolist())
         dev = noisy_hidden.device
         inv_n = torch.full((), 1.0 / max(token_count, 1), device=dev, dtype=torch.float32)
-        zero_loss = torch.zeros((), device=dev, dtype=torch.float32)
+        # inactive or empty terms stay connected to the graph (training/trainer.py:249), so that
+        # backward() works, with zero gradients, on a micro-batch that has no rows for the loss
+        zero_loss = noisy_hidden.sum() * 0.0
         hdim = noisy_hidden.shape[-1]
         flat_noisy = noisy_hidden.reshape(-1, hdim)
         flat_clean = clean_hidden.reshape(-1, hdim)
@@ -261,13 +262,15 @@ class UnoTrainer(Trainer):
             ce_loss = zero_loss
 
         combined_loss = combine_objective_losses(ce_loss, kl_loss, tv_loss, self.objective)
-        # Kept as device scalars (no host synchronisation per step); ``logged()`` converts them.
-        self._step_metrics.append({
-            "train/ce_loss": ce_loss.detach(), "train/reverse_kl_loss": kl_loss.detach(),
-            "train/tv_loss": tv_loss.detach(), "train/combined_loss": combined_loss.detach(),
-            "train/alpha": self.objective.ce_weight, "train/beta": self.objective.kl_weight,
-            "train/gamma": self.objective.tv_weight, "train/block_size": block_size,
-            "train/transformer_forwards": 1,
+        # Per-step metrics through Trainer.log (state.log_history, on_log callbacks, reporters),
+        # as training/trainer.py:288-300; one device-to-host copy for the four values.
+        ce_v, kl_v, tv_v, comb_v = torch.stack([t.detach().float().reshape(()) for t in
+                                                (ce_loss, kl_loss, tv_loss, combined_loss)]).tolist()
+        self.log({
+            "train/ce_loss": ce_v, "train/reverse_kl_loss": kl_v, "train/tv_loss": tv_v,
+            "train/combined_loss": comb_v, "train/alpha": self.objective.ce_weight,
+            "train/beta": self.objective.kl_weight, "train/gamma": self.objective.tv_weight,
+            "train/block_size": block_size, "train/transformer_forwards": 1,
         })
         if return_outputs:
             return combined_loss, {"loss": combined_loss, "ce_loss": ce_loss, "reverse_kl_loss": kl_loss,
@@ -278,10 +281,6 @@ class UnoTrainer(Trainer):
         """Whether the losses read the clean stream's hidden states (TV, KL, clean-argmax CE targets)."""
         o = self.objective
         return o.kl_weight > 0 or o.tv_weight > 0 or (o.ce_weight > 0 and o.internal_ce_target != "data")
-
-    def logged(self) -> list[dict]:
-        """The per-step objective metrics of compute_loss, as floats."""
-        return [{k: (float(v) if torch.is_tensor(v) else v) for k, v in rec.items()} for rec in self._step_metrics]
 
     # ---- one optimizer step outside HF's loop ---------------------------------------------------
     def _ensure_optimizer(self) -> None:
