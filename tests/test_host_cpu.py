@@ -53,6 +53,29 @@ def test_curriculum_rejects_bad_plans(mutate):
         ucur.BlockCurriculumPlan.from_dict(raw)
 
 
+def test_curriculum_hash_matches_reference_vectors(tmp_path):
+    """sha256() of the released schedule and of synthetic schedules equals the reference's own
+    (tests/golden/curriculum_vectors.json, written by tests/golden/make_curriculum_vectors.py from the
+    reference's training/curriculum.py): boundary checkpoints of either implementation validate in the
+    other. Also the stage boundaries and the manifest, key for key; from_yaml and from_dict agree."""
+    from pathlib import Path
+
+    import yaml
+    vec = json.loads((Path(__file__).parent / "golden" / "curriculum_vectors.json").read_text())
+    cases = [vec["released"], *vec["synthetic"]]
+    assert len({c["sha256"] for c in cases}) == len(cases)
+    for i, case in enumerate(cases):
+        plan = ucur.BlockCurriculumPlan.from_dict(case["input"])
+        assert [s.end_step for s in plan.stages] == case["end_steps"]
+        assert plan.max_steps == case["max_steps"]
+        assert plan.manifest() == case["manifest"]
+        assert plan.sha256() == case["sha256"]
+        path = tmp_path / f"plan{i}.yaml"
+        path.write_text(yaml.safe_dump(case["input"]))
+        assert ucur.BlockCurriculumPlan.from_yaml(path).sha256() == case["sha256"]
+    assert ucur.BlockCurriculumPlan.from_dict(RELEASED).sha256() == vec["released"]["sha256"]
+
+
 def test_curriculum_yaml_missing_file(tmp_path):
     with pytest.raises(FileNotFoundError):
         ucur.BlockCurriculumPlan.from_yaml(tmp_path / "nope.yaml")
