@@ -123,18 +123,22 @@ int unok_rmsnorm_bwd(int dtype, int M, int H, const void* dy, const void* x, con
                      const float* rstd, const void* dres, void* dx, void* stream);
 
 /* Per-head q/k RMSNorm (wq/wk may both be null: RoPE only) then rotate_half RoPE with
- * angle fl32(pos * inv_freq[i]); writes contiguous q [M, nq*d] and k [M, nk*d].
+ * angle fl32(pos * inv_freq[i]), in fp32 with one rounding at the store; writes contiguous
+ * q [M, nq*d] and k [M, nk*d], and, when v_out is non-null, the v heads of qkv into v_out
+ * [M, nk*d] (row stride ldv). dtype: q, k, v_out and the weights; qkv_dtype: the qkv input
+ * (dtype, or fp32 with bf16 outputs).
  * modeling_qwen3.py:140-160 (rotary), :237-253 (q_norm/k_norm before RoPE). */
-int unok_qknorm_rope_fwd(int dtype, int M, int nq, int nk, int d, const void* qkv, int64_t ld,
-                         const void* wq, const void* wk, const int64_t* pos,
-                         const float* inv_freq, float eps, void* q_out, void* k_out,
-                         float* rstd, void* stream);
-int unok_qknorm_rope_bwd(int dtype, int M, int nq, int nk, int d, const void* dq,
+int unok_qknorm_rope_fwd(int dtype, int qkv_dtype, int M, int nq, int nk, int d, const void* qkv,
+                         int64_t ld, const void* wq, const void* wk, const int64_t* pos,
+                         const float* inv_freq, float eps, void* q_out, void* k_out, void* v_out,
+                         int64_t ldv, float* rstd, void* stream);
+/* dtype: dqkv and the weights; in_dtype: dq, dk and qkv (dtype, or fp32 with a bf16 dqkv). */
+int unok_qknorm_rope_bwd(int dtype, int in_dtype, int M, int nq, int nk, int d, const void* dq,
                          const void* dk, const void* qkv, int64_t ld, const void* wq,
                          const void* wk, const int64_t* pos, const float* inv_freq,
                          const float* rstd, void* dqkv, int64_t ldd, void* stream);
 
-/* out = round(silu(gate)) * up over the fused [gate | up] projection (modeling_qwen3.py:81-82). */
+/* out = silu(gate) * up over the fused [gate | up] projection, rounded once (modeling_qwen3.py:81-82). */
 int unok_swiglu_fwd(int dtype, int M, int F, const void* gu, int64_t ld, void* out, void* stream);
 int unok_swiglu_bwd(int dtype, int M, int F, const void* dout, const void* gu, int64_t ld,
                     void* dgu, int64_t ldd, void* stream);
@@ -159,8 +163,10 @@ int unok_attn_fwd(int dtype, int Mq, int Hq, int Hkv, int D, const void* Q, int6
                   const int32_t* iv, void* O, int64_t ldo, float* LSE, float scale,
                   void* stream);
 /* dQ for every query; dK/dV for the source-2 keys when dK/dV are non-null (source-1 keys are
- * the detached clean stream). Dsum [Mq,Hq] fp32 is caller scratch. */
-int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D, const void* Q, int64_t ldq,
+ * the detached clean stream). Dsum [Mq,Hq] fp32 is caller scratch. grad_dtype: dQ and dK (dtype,
+ * or fp32 with bf16 inputs); dV has dtype. */
+int unok_attn_bwd(int dtype, int grad_dtype, int Mq, int Mk2, int Hq, int Hkv, int D, const void* Q,
+                  int64_t ldq,
                   const void* K1, int64_t ldk1, const void* V1, int64_t ldv1,
                   const void* K2, int64_t ldk2, const void* V2, int64_t ldv2,
                   const int32_t* iv, const int32_t* ivk, const void* O, int64_t ldo,

@@ -11,9 +11,11 @@ layer each, against the fp32 oracle on the same bf16-rounded weights:
             (16 r), one 4096-token row, at block 16 and at every block size of the 4 -> 32 curriculum.
 
 The GPU step keeps bf16 weights, adapters and activations. Bars: loss within
-1e-3 relative, LoRA gradient cosine >= 0.999 per tensor; the relative L2 error of every tensor is
-printed, and bounded by max(1e-2, 1.3 x the reference's own bf16 arithmetic on the same inputs)
-(the oracle run with bf16 weights, adapters and activations).
+1e-3 relative, LoRA gradient cosine >= 0.999 and relative L2 error <= 1e-2 per tensor against the
+fp32 oracle. The 7B MHA configuration (alpha = 16 r) is held to max(1e-2, 1.3 x the reference's own
+bf16 arithmetic on the same inputs) instead: there the error that bf16 storage of the forward
+activations alone causes (no gradient rounding, every op in fp32) is above 1e-2 at these widths, so
+no bf16 step can meet the literal bar. The per-tensor errors are printed with the reference's.
 """
 import pytest
 import torch
@@ -33,10 +35,10 @@ SEED = 20260813
 CONFIGS = {
     "qwen3_8b": dict(cfg=dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_attention_heads=32,
                               num_key_value_heads=8, head_dim=128, qk_norm=True),
-                     rank=64, alpha=128, B=1, L=4096, prompt=512, blocks=[16]),
+                     rank=64, alpha=128, B=1, L=4096, prompt=512, blocks=[16], literal=True),
     "dense_1b": dict(cfg=dict(vocab_size=151936, hidden_size=2048, intermediate_size=5632, num_attention_heads=16,
                               num_key_value_heads=8, head_dim=128, qk_norm=True),
-                     rank=32, alpha=64, B=4, L=2048, prompt=256, blocks=[8]),
+                     rank=32, alpha=64, B=4, L=2048, prompt=256, blocks=[8], literal=True),
     "mha_7b": dict(cfg=dict(vocab_size=32000, hidden_size=4096, intermediate_size=11008, num_attention_heads=32,
                             num_key_value_heads=32, head_dim=128, qk_norm=False),
                    rank=64, alpha=1024, B=1, L=4096, prompt=512, blocks=[16]),
@@ -44,6 +46,15 @@ CONFIGS = {
                                        num_attention_heads=32, num_key_value_heads=32, head_dim=128, qk_norm=False),
                               rank=64, alpha=1024, B=1, L=4096, prompt=512, blocks=[4, 8, 32]),
 }
+
+
+STORED = {"x1", "qkv", "qk", "o", "resid", "x2", "gu", "sw", "final", "lora_w", "lora_h"}
+
+
+def _stored_bf16(x, point):
+    """Rounds the forward value stored at a named oracle point to bf16 and passes the gradient through
+    unrounded: the error of bf16 activation storage alone, with every op and gradient in fp32."""
+    return x + (x.bfloat16().float() - x).detach() if point in STORED else x
 
 
 def _errors(grads, ref):
@@ -107,6 +118,14 @@ def test_bf16_step_full_width(dev, name):
         loss16, _ = ostep.compute_loss({k: v.bfloat16() for k, v in params.items()}, leaves16, cfg, batch, obj, **kw)
         loss16.backward()
 
+        floor = None
+        if step == 0:
+            print(f"[full size] {name}: fp32 oracle with bf16-stored activations", flush=True)
+            leaves_f = {k: v.clone().requires_grad_(True) for k, v in lora.items()}
+            loss_f, _ = ostep.compute_loss(params, leaves_f, cfg, batch, obj, rnd=_stored_bf16, **kw)
+            loss_f.backward()
+            floor = _errors({k: v.grad for k, v in leaves_f.items()}, ref)
+
         lrel = abs(mine_loss - ref_loss.item()) / abs(ref_loss.item())
         err = _errors(mine, ref)
         theirs = _errors({k: v.grad for k, v in leaves16.items()}, ref)
@@ -118,7 +137,14 @@ def test_bf16_step_full_width(dev, name):
         print(f"[full size] {name} block {block}: worst rel L2 {max(r for _, r in err.values()):.3e}, RMS "
               f"{rms(err):.3e} (bf16 reference {max(r for _, r in theirs.values()):.3e}, RMS {rms(theirs):.3e})",
               flush=True)
+        if floor is not None:
+            worst_floor = max(r for _, r in floor.values())
+            print(f"[full size] {name}: bf16 activation storage alone: worst rel L2 {worst_floor:.3e}, RMS "
+                  f"{rms(floor):.3e}", flush=True)
+            # the relative bar is kept only where that floor itself is above the literal one
+            assert spec.get("literal") or worst_floor > 1e-2
         assert lrel < 1e-3
         assert min(cc for cc, _ in err.values()) >= 0.999
         for k, (_, r) in err.items():
-            assert r <= max(1e-2, 1.3 * theirs[k][1]), (k, r, theirs[k][1])
+            bar = 1e-2 if spec.get("literal") else max(1e-2, 1.3 * theirs[k][1])
+            assert r <= bar, (k, r, theirs[k][1])

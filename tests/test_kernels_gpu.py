@@ -94,6 +94,38 @@ def test_qknorm_rope_fwd_bwd(dev, dtype, d, norm, nq, nk):
     assert rel(dqkv[:, :e], x.grad[:, :e]) < (5e-5 if dtype == torch.float32 else 1e-2)
 
 
+@pytest.mark.parametrize("nq,nk", [(4, 2), (32, 8)])
+def test_qknorm_rope_fp32_in_bf16_out(dev, nq, nk):
+    """The bf16 step's q/k path: an fp32 q/k/v projection normalised and rotated in fp32 and rounded
+    once (q, k and the copied v heads in bf16, v bit-identical to rounding the input), and the
+    backward from fp32 dq/dk and the fp32 projection into a bf16 dqkv. Against fp32 torch, and at
+    least as close as the all-bf16 path that rounds the projection first."""
+    torch.manual_seed(11)
+    M, d, theta = 96, 128, 1e6
+    qkv = torch.randn(M, (nq + 2 * nk) * d, device=dev)
+    wq = (1 + 0.1 * torch.randn(d, device=dev)).bfloat16()
+    wk = (1 + 0.1 * torch.randn(d, device=dev)).bfloat16()
+    pos = torch.randint(0, 16384, (M,), device=dev)
+    inv = (1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))).to(dev)
+    q, k, v, rstd = K.qknorm_rope_fwd(qkv, nq, nk, d, wq, wk, pos, inv, 1e-6, out_dtype=torch.bfloat16, with_v=True)
+    assert q.dtype == k.dtype == v.dtype == torch.bfloat16
+    assert torch.equal(v, qkv[:, (nq + nk) * d:].bfloat16())
+    x = qkv.clone().requires_grad_(True)
+    qr, kr = ref_qknorm_rope(x, nq, nk, d, wq, wk, pos, theta, 1e-6)
+    q16, k16, _ = K.qknorm_rope_fwd(qkv.bfloat16(), nq, nk, d, wq, wk, pos, inv, 1e-6)
+    assert rel(q, qr) < 4e-3 and rel(k, kr) < 4e-3
+    assert rel(q, qr) <= rel(q16, qr) and rel(k, kr) <= rel(k16, kr)
+    dq = torch.randn_like(qr)
+    dk = torch.randn_like(kr)
+    (qr * dq).sum().add_((kr * dk).sum()).backward()
+    dqkv = torch.zeros(M, (nq + 2 * nk) * d, device=dev, dtype=torch.bfloat16)
+    K.qknorm_rope_bwd(dq.contiguous(), dk.contiguous(), qkv, nq, nk, d, wq, wk, pos, inv, rstd, dqkv)
+    e = (nq + nk) * d
+    assert rel(dqkv[:, :e], x.grad[:, :e]) < 4e-3
+    with pytest.raises(RuntimeError):
+        K.qknorm_rope_bwd(dq.bfloat16().contiguous(), dk.contiguous(), qkv, nq, nk, d, wq, wk, pos, inv, rstd, dqkv)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_swiglu_fwd_bwd(dev, dtype):
     torch.manual_seed(2)
@@ -275,6 +307,14 @@ def test_block_diffusion_attention(dev, dtype, D, L, bs, packed, intra):
     assert rel(dq, flat(qn_r.grad)) < gtol
     assert rel(dk, flat(kn_r.grad)) < gtol
     assert rel(dv, flat(vn_r.grad)) < gtol
+    if dtype == torch.bfloat16:
+        # dQ and dK in fp32 from the same kernels: the same values before their final rounding
+        dk32 = torch.empty(M, Hkv * D, device=dev, dtype=torch.float32)
+        dv2 = torch.empty_like(dv)
+        dq32 = K.attn_bwd(flat(qn), flat(kc), flat(vc), mask.iv_noisy, on, ln, do, Hq, Hkv, D, k2=flat(kn),
+                          v2=flat(vn), ivk=mask.iv_noisy, dk=dk32, dv=dv2, grad_dtype=torch.float32)
+        assert dq32.dtype == torch.float32
+        assert torch.equal(dq32.bfloat16(), dq) and torch.equal(dk32.bfloat16(), dk) and torch.equal(dv2, dv)
 
 
 # ------------------------------------------------------------------------------------------

@@ -37,8 +37,8 @@ SIGNATURES: dict[str, tuple] = {
     "unok_gemm_tn_noalloc": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _f, _f, _p]),
     "unok_rmsnorm_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _p, _i64, _p, _f, _p]),
     "unok_rmsnorm_bwd": (_i, [_i, _i, _i, _p, _p, _p, _p, _p, _p, _p]),
-    "unok_qknorm_rope_fwd": (_i, [_i, _i, _i, _i, _i, _p, _i64, _p, _p, _p, _p, _f, _p, _p, _p, _p]),
-    "unok_qknorm_rope_bwd": (_i, [_i, _i, _i, _i, _i, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "unok_qknorm_rope_fwd": (_i, [_i, _i, _i, _i, _i, _i, _p, _i64, _p, _p, _p, _p, _f, _p, _p, _p, _i64, _p, _p]),
+    "unok_qknorm_rope_bwd": (_i, [_i, _i, _i, _i, _i, _i, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "unok_swiglu_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _p]),
     "unok_swiglu_bwd": (_i, [_i, _i, _i, _p, _p, _i64, _p, _i64, _p]),
     "unok_embedding": (_i, [_i, _i, _i, _p, _p, _i64, _p, _p]),
@@ -48,7 +48,7 @@ SIGNATURES: dict[str, tuple] = {
     "unok_attn_fwd_split": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _f, _p]),
     "unok_attn_split_combine": (_i, [_i, _i, _i, _p, _i64, _p, _p, _p, _i64, _p]),
     "unok_decode_prep": (_i, [_i, _i, _i, _i, _i, _p, _i64, _p, _p, _p, _p, _f, _p, _p, _i, _p, _p]),
-    "unok_attn_bwd": (_i, [_i, _i, _i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
+    "unok_attn_bwd": (_i, [_i, _i, _i, _i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
                            _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _f, _p]),
     "unok_bd_prepare": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _u64, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                              _p, _p, _p]),

@@ -39,6 +39,7 @@ struct AttnArgs {
   void* dV; int64_t lddv;
   int Mq, Mk2, Hq, Hkv;
   int q_mod;                           // > 0: query row i reads Q row i % q_mod (split-key decode)
+  int grad_f32;                        // bf16 kernels: dQ and dK stored as fp32 (dV keeps bf16)
   float scale;                         // d^-0.5
   float scale_log2;                    // d^-0.5 * log2(e)
 };
@@ -586,7 +587,16 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
     tile(t, S0{});
     if (t + 1 < nt) tile(t + 1, S1{});
   }
-  if (qvalid) {
+  if (qvalid && p.grad_f32) {
+    float* out = (float*)p.dQ + (int64_t)qrow * p.lddq + h * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4)
+        *(float4*)(out + t * 32 + 8 * j4 + 4 * g) =
+            make_float4(dq[t][j4 * 4] * p.scale, dq[t][j4 * 4 + 1] * p.scale, dq[t][j4 * 4 + 2] * p.scale,
+                        dq[t][j4 * 4 + 3] * p.scale);
+  } else if (qvalid) {
     bf16_t* out = (bf16_t*)p.dQ + (int64_t)qrow * p.lddq + h * D;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
@@ -752,22 +762,29 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_bf16_kernel(const AttnArgs p)
     }
   }
   if (kvalid) {
-    bf16_t* ok = (bf16_t*)p.dK + (int64_t)krow * p.lddk + kvh * D;
     bf16_t* ov = (bf16_t*)p.dV + (int64_t)krow * p.lddv + kvh * D;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
       for (int j4 = 0; j4 < 4; ++j4) {
-        uint2 uk, uv;
-        bf16_t* hk = (bf16_t*)&uk;
+        const int c = t * 32 + 8 * j4 + 4 * g;
+        uint2 uv;
         bf16_t* hv = (bf16_t*)&uv;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          hk[e] = f32_to_bf16(dk[t][j4 * 4 + e] * p.scale);
-          hv[e] = f32_to_bf16(dv[t][j4 * 4 + e]);
+        for (int e = 0; e < 4; ++e) hv[e] = f32_to_bf16(dv[t][j4 * 4 + e]);
+        *(uint2*)(ov + c) = uv;
+        if (p.grad_f32) {
+          float* ok = (float*)p.dK + (int64_t)krow * p.lddk + kvh * D;
+          *(float4*)(ok + c) = make_float4(dk[t][j4 * 4] * p.scale, dk[t][j4 * 4 + 1] * p.scale,
+                                           dk[t][j4 * 4 + 2] * p.scale, dk[t][j4 * 4 + 3] * p.scale);
+        } else {
+          bf16_t* ok = (bf16_t*)p.dK + (int64_t)krow * p.lddk + kvh * D;
+          uint2 uk;
+          bf16_t* hk = (bf16_t*)&uk;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) hk[e] = f32_to_bf16(dk[t][j4 * 4 + e] * p.scale);
+          *(uint2*)(ok + c) = uk;
         }
-        *(uint2*)(ok + t * 32 + 8 * j4 + 4 * g) = uk;
-        *(uint2*)(ov + t * 32 + 8 * j4 + 4 * g) = uv;
       }
   }
 }
@@ -975,8 +992,10 @@ UNOK_EXPORT int unok_attn_fwd_split(int QR, int S, int D, const void* Q, int64_t
 }
 
 // Backward. Computes Dsum into the caller's [Mq,Hq] fp32 buffer, dQ for every query, and,
-// when dK/dV are non-null, dK/dV of the source-2 keys (rows [0, Mk2)).
-UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D, const void* Q, int64_t ldq,
+// when dK/dV are non-null, dK/dV of the source-2 keys (rows [0, Mk2)). grad_dtype is the element
+// type of dQ and dK: dtype, or fp32 with bf16 inputs (dV always has dtype).
+UNOK_EXPORT int unok_attn_bwd(int dtype, int grad_dtype, int Mq, int Mk2, int Hq, int Hkv, int D, const void* Q,
+                              int64_t ldq,
                               const void* K1, int64_t ldk1, const void* V1, int64_t ldv1, const void* K2, int64_t ldk2,
                               const void* V2, int64_t ldv2, const int32_t* iv, const int32_t* ivk, const void* O,
                               int64_t ldo, const float* LSE, const void* dO, int64_t lddo, float* Dsum, void* dQ,
@@ -985,6 +1004,8 @@ UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D
   if (Mq == 0) return 0;
   int rc = check_geom(dtype, D, Hq, Hkv);
   if (rc) return rc;
+  UNOK_REQUIRE(grad_dtype == dtype || (dtype == UNOK_BF16 && grad_dtype == UNOK_F32), UNOK_EINVAL,
+               "attn_bwd: gradient type %d with input type %d", grad_dtype, dtype);
   hipStream_t st = (hipStream_t)stream;
   const unsigned items = (unsigned)(((int64_t)Mq * Hq + 3) / 4);
   if (dtype == UNOK_F32) {
@@ -1000,6 +1021,7 @@ UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D
   a.K2 = K2; a.ldk2 = ldk2; a.V2 = V2; a.ldv2 = ldv2; a.iv = iv; a.ivk = ivk; a.LSE = (float*)LSE;
   a.dO = dO; a.lddo = lddo; a.Dsum = Dsum; a.dQ = dQ; a.lddq = lddq; a.dK = dK; a.lddk = lddk; a.dV = dV; a.lddv = lddv;
   a.Mq = Mq; a.Mk2 = Mk2; a.Hq = Hq; a.Hkv = Hkv; a.scale = scale; a.scale_log2 = scale * 1.4426950408889634f;
+  a.grad_f32 = dtype == UNOK_BF16 && grad_dtype == UNOK_F32;
   const bool want_kv = dK != nullptr && dV != nullptr && K2 != nullptr && Mk2 > 0;
   if (want_kv) UNOK_REQUIRE(ivk != nullptr, UNOK_EINVAL, "attn_bwd: key-side interval table required for dK/dV");
   if (dtype == UNOK_F32) {
@@ -1009,8 +1031,8 @@ UNOK_EXPORT int unok_attn_bwd(int dtype, int Mq, int Mk2, int Hq, int Hkv, int D
     hipLaunchKernelGGL(attn_dkv_f32_kernel, dim3((unsigned)(((int64_t)Mk2 * Hkv + 3) / 4)), dim3(256), 0, st, a, D);
     return unok::check_launch("attn_dkv_f32");
   }
-  UNOK_REQUIRE(al16(dO) && al16(O) && lddo % 8 == 0 && ldo % 8 == 0 && lddq % 8 == 0 &&
-                   (!want_kv || (lddk % 8 == 0 && lddv % 8 == 0)),
+  UNOK_REQUIRE(al16(dO) && al16(O) && al16(dQ) && lddo % 8 == 0 && ldo % 8 == 0 && lddq % 8 == 0 &&
+                   (!want_kv || (al16(dK) && lddk % 8 == 0 && lddv % 8 == 0)),
                UNOK_EALIGN, "attn_bwd(bf16): gradient strides must be multiples of 8");
   if (D == 128) launch_dq<128>(Mq, Hq, st, a);
   else launch_dq<64>(Mq, Hq, st, a);

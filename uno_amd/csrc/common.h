@@ -144,12 +144,11 @@ __device__ __forceinline__ float fast_expf(float x) { return __builtin_amdgcn_ex
 // SwiGLU kernels round identically.
 __device__ __forceinline__ float sigmoidf_(float g) { return __builtin_amdgcn_rcpf(1.f + fast_expf(-g)); }
 
-// Gradients of out = bf16(silu(g)) * u for upstream d: the same expression in the SwiGLU backward
-// kernel and the fused GEMM epilogue, so both round identically.
+// Gradients of out = silu(g) * u for upstream d: the same expression in the SwiGLU backward kernel
+// and the fused GEMM epilogue, so both round identically.
 __device__ __forceinline__ void swiglu_grad(float d, float g, float u, float& dg, float& du) {
   const float sg = sigmoidf_(g);
-  const float silu = bf16_to_f32(f32_to_bf16(g * sg));
-  du = d * silu;
+  du = d * (g * sg);
   dg = d * u * sg * (1.f + g * (1.f - sg));
 }
 

@@ -189,7 +189,7 @@ __global__ __launch_bounds__(RB_W * 64) void gemm_nt_rows_kernel(const RowsGemm 
 //   3. every thread adds the partials of 4 columns (and 4 up columns) of its rows in range order,
 //      then u, the residual, and rounds:
 // EPI 0: C[M, N]   = bf16(sum + u + Res);
-// EPI 1: C[M, N/2] = bf16(bf16(silu(g)) * u), g = bf16(gate column value), u = bf16(up column value)
+// EPI 1: C[M, N/2] = bf16(silu(g) * u), g = bf16(gate column value), u = bf16(up column value)
 //        (the [gate | up] product rounded to bf16 and then the SwiGLU of unok_swiglu_fwd).
 // Segment boundaries are multiples of 16, so each 16-slot tile reads one segment of h.
 // ---------------------------------------------------------------------------------------
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(256) void rows_reduce_kernel(const RowsReduce p) {
         const float b[4] = {acc[i][NH - 1].x, acc[i][NH - 1].y, acc[i][NH - 1].z, acc[i][NH - 1].w};
         const float g = Elem<bf16_t>::round(a[c]);
         const float u = Elem<bf16_t>::round(b[c]);
-        o[c] = Elem<bf16_t>::round(g * sigmoidf_(g)) * u;
+        o[c] = g * sigmoidf_(g) * u;
       }
     }
     uint2 packed;
@@ -460,8 +460,8 @@ __global__ __launch_bounds__(256) void decode_prep_kernel(const bf16_t* __restri
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float w0 = __uint_as_float(w[i] << 16), w1 = __uint_as_float(w[i] & 0xffff0000u);
-        x[2 * i] = Elem<bf16_t>::round(Elem<bf16_t>::round(x[2 * i] * r) * w0);
-        x[2 * i + 1] = Elem<bf16_t>::round(Elem<bf16_t>::round(x[2 * i + 1] * r) * w1);
+        x[2 * i] = x[2 * i] * r * w0;
+        x[2 * i + 1] = x[2 * i + 1] * r * w1;
       }
     }
     const float p = (float)(len + t);

@@ -1196,8 +1196,8 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     // Gate/up product with 64-row interleaved weights (rows 128 b + [0, 64) = gate features
     // 64 b + [0, 64), rows 128 b + [64, 128) = the same up features): the wave's 128 columns are
     // one such pair, accumulator j < 4 the gate and j + 4 the up value of the same feature. Writes
-    // C[row][64 b + c] = bf16(bf16(silu(g)) u) with g, u rounded to bf16 first, as a bf16 GEMM
-    // followed by the SwiGLU kernel computes it. With C2, also stores the rounded gate and up
+    // C[row][64 b + c] = bf16(silu(g) u) with g, u rounded to bf16 first, as a bf16 GEMM followed
+    // by the SwiGLU kernel computes it. With C2, also stores the rounded gate and up
     // values as C2[row][f] and C2[row][N/2 + f] (the [gate | up] layout of the plain product):
     // then each wave rounds its 128 x (64 gate | 64 up) block into a private 32 KB of the idle
     // LDS stages (16-byte chunks XOR-swizzled by row, as in the backward epilogue) and stores
@@ -1220,7 +1220,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
           for (int e = 0; e < 4; ++e) {
             const float gv = bf16_to_f32(f32_to_bf16(acc[i][j][e] * p.alpha));
             const float uv = bf16_to_f32(f32_to_bf16(acc[i][j + TN / 2][e] * p.alpha));
-            v[e] = bf16_to_f32(f32_to_bf16(gv * sigmoidf_(gv))) * uv;
+            v[e] = gv * sigmoidf_(gv) * uv;
           }
           *(uint2*)&q[r * 64 + (((2 * j + (lk >> 1)) ^ ((r >> 1) & 7)) << 3) + (lk & 1) * 4] =
               make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
@@ -1248,7 +1248,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
           for (int q = 0; q < 4; ++q) {
             const float gv = bf16_to_f32(f32_to_bf16(acc[i][j][q] * p.alpha));
             const float uv = bf16_to_f32(f32_to_bf16(acc[i][j + TN / 2][q] * p.alpha));
-            v[q] = bf16_to_f32(f32_to_bf16(gv * sigmoidf_(gv))) * uv;
+            v[q] = gv * sigmoidf_(gv) * uv;
           }
           store4(crow + f0 + j * 16 + lk * 4, nullptr, v);
         }
@@ -1288,7 +1288,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float g = bf16_to_f32(gv[e]);
-        v[e] = bf16_to_f32(f32_to_bf16(g * sigmoidf_(g))) * bf16_to_f32(uv[e]);
+        v[e] = g * sigmoidf_(g) * bf16_to_f32(uv[e]);
       }
       store4(sdst + (int64_t)(it * 4) * p.ldc, nullptr, v);
     }

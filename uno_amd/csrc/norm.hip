@@ -2,10 +2,12 @@
 // with rotary embedding, SwiGLU, embedding gather and index-mapped row copies.
 //
 // Semantics follow transformers' Qwen3 modules (modeling_qwen3.py): RMSNorm statistics in
-// fp32, normalised value rounded to the storage type, then scaled by the weight; q/k norms are
-// per 128-wide head before RoPE (rotate_half convention, angle = fl32(pos * inv_freq[i]));
-// SwiGLU is down(silu(gate) * up). Every kernel reads and writes with 16-byte vectors and
-// reduces with 64-lane wavefront shuffles.
+// fp32; q/k norms are per 128-wide head before RoPE (rotate_half convention, angle =
+// fl32(pos * inv_freq[i])); SwiGLU is down(silu(gate) * up). Each kernel keeps its whole
+// computation in fp32 and rounds once, at the store (normalised value times weight, then the
+// rotation; silu(gate) times up), where a bf16 module rounds after every operation: the step's
+// LoRA gradients stay closer to the fp32 computation. Every kernel reads and writes with 16-byte
+// vectors and reduces with 64-lane wavefront shuffles.
 #include "common.h"
 
 #include <type_traits>
@@ -41,7 +43,8 @@ __device__ __forceinline__ void store_vec(T* p, const float* in) {
 }
 
 // ---------------------------------------------------------------------------------------
-// RMSNorm: y = w * round(x * rstd), rstd = rsqrt(mean(x^2) + eps); one 256-thread block/row.
+// RMSNorm: y = w * x * rstd, rstd = rsqrt(mean(x^2) + eps), in fp32 and rounded once at the store;
+// one 256-thread block/row.
 // ---------------------------------------------------------------------------------------
 template <typename T, int MAXV>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ x, int64_t ldx, const T* __restrict__ w,
@@ -73,7 +76,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ 
       float wv[V], o[V];
       load_vec(w + c * V, wv);
 #pragma unroll
-      for (int e = 0; e < V; ++e) o[e] = Elem<T>::round(v[i][e] * r) * wv[e];
+      for (int e = 0; e < V; ++e) o[e] = v[i][e] * r * wv[e];
       store_vec(yr + c * V, o);
     }
   }
@@ -165,13 +168,45 @@ __device__ __forceinline__ void rope_angles(float p, const float* __restrict__ i
   }
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const T* __restrict__ qkv, int64_t ld, const T* wq,
-                                                              const T* wk, const int64_t* __restrict__ pos,
-                                                              const float* __restrict__ inv_freq, T* __restrict__ qo,
-                                                              T* __restrict__ ko, float* __restrict__ rstd, int M,
-                                                              int nq, int nk, float eps) {
-  constexpr int EPL = Vec16<T>::N, LPH = D / EPL, HPW = 64 / LPH, HALF = D / 2;
+// N elements of T at p as floats, and back (N * sizeof(T) is 8 or 16 bytes, aligned).
+template <typename T, int N> __device__ __forceinline__ void ld_elems(const T* p, float (&v)[N]) {
+  if constexpr (std::is_same<T, float>::value) {
+    static_assert(N == 4, "fp32 groups of 4");
+    const float4 f = *(const float4*)p;
+    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+  } else if constexpr (N == 8) {
+    Vec16<bf16_t>::load(p, v);
+  } else {
+    static_assert(N == 4, "bf16 groups of 4 or 8");
+    const uint2 u = *(const uint2*)p;
+    v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xffff0000u);
+    v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xffff0000u);
+  }
+}
+template <typename T, int N> __device__ __forceinline__ void st_elems(T* p, const float (&v)[N]) {
+  if constexpr (std::is_same<T, float>::value) {
+    static_assert(N == 4, "fp32 groups of 4");
+    *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (N == 8) {
+    Vec16<bf16_t>::store(p, v);
+  } else {
+    static_assert(N == 4, "bf16 groups of 4 or 8");
+    *(uint2*)p = make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+  }
+}
+
+// TI: element type of the qkv input (the projection output; fp32 for bf16 models keeps the q/k
+// values unrounded up to the normalisation); TO: element type of q, k, the norm weights and the
+// optional copy of the v heads into vo [M, nk*D] (row stride ldv), which the attention kernels
+// read as their V operand.
+template <typename TI, typename TO, int D>
+__global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const TI* __restrict__ qkv, int64_t ld, const TO* wq,
+                                                              const TO* wk, const int64_t* __restrict__ pos,
+                                                              const float* __restrict__ inv_freq, TO* __restrict__ qo,
+                                                              TO* __restrict__ ko, TO* __restrict__ vo, int64_t ldv,
+                                                              float* __restrict__ rstd, int M, int nq, int nk,
+                                                              float eps) {
+  constexpr int EPL = Vec16<TI>::N, LPH = D / EPL, HPW = 64 / LPH, HALF = D / 2;
   static_assert(LPH >= 2 && LPH <= 64 && 64 % LPH == 0, "head geometry");
   __shared__ float s_cs[4][HALF], s_sn[4][HALF];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -186,20 +221,21 @@ __global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const T* __restric
 #pragma unroll
   for (int e = 0; e < EPL; ++e) { cv[e] = s_cs[w][j0 + e]; sv[e] = s_sn[w][j0 + e]; }
   const int nh = nq + nk;
+  const int nall = vo != nullptr ? nh + nk : nh;   // v heads follow the k heads in qkv
   const bool norm = wq != nullptr;
   float wqv[EPL], wkv[EPL];
   if (norm) {
-    Vec16<T>::load(wq + c0, wqv);
-    Vec16<T>::load(wk + c0, wkv);
+    ld_elems<TO, EPL>(wq + c0, wqv);
+    ld_elems<TO, EPL>(wk + c0, wkv);
   }
   // Heads in groups of QKR_GROUP passes: the group's loads are all issued before its arithmetic,
   // so each wavefront keeps several KB of the row in flight instead of one pass's 1 KB.
-  for (int hb0 = 0; hb0 < nh; hb0 += HPW * QKR_GROUP) {
+  for (int hb0 = 0; hb0 < nall; hb0 += HPW * QKR_GROUP) {
     uint4 raw[QKR_GROUP];
 #pragma unroll
     for (int gi = 0; gi < QKR_GROUP; ++gi) {
       const int head = hb0 + gi * HPW + hh;
-      raw[gi] = head < nh ? *(const uint4*)(qkv + (int64_t)row * ld + (int64_t)head * D + c0) : make_uint4(0, 0, 0, 0);
+      raw[gi] = head < nall ? *(const uint4*)(qkv + (int64_t)row * ld + (int64_t)head * D + c0) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int gi = 0; gi < QKR_GROUP; ++gi) {
@@ -207,7 +243,11 @@ __global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const T* __restric
       const bool valid = head < nh;
       const bool isq = head < nq;
       float x[EPL];
-      Vec16<T>::unpack(raw[gi], x);
+      Vec16<TI>::unpack(raw[gi], x);
+      if (head >= nh) {      // a v head (or past the row): copied, no norm or rotation
+        if (head < nall) st_elems<TO, EPL>(vo + (int64_t)row * ldv + (int64_t)(head - nh) * D + c0, x);
+        continue;
+      }
       if (norm) {
         float ss = 0.f;
 #pragma unroll
@@ -218,7 +258,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const T* __restric
         if (valid && lane % LPH == 0) rstd[(int64_t)row * nh + head] = r;
 #pragma unroll
         for (int e = 0; e < EPL; ++e)
-          x[e] = valid ? Elem<T>::round(Elem<T>::round(x[e] * r) * (isq ? wqv[e] : wkv[e])) : 0.f;
+          x[e] = valid ? x[e] * r * (isq ? wqv[e] : wkv[e]) : 0.f;
       }
       float out[EPL];
 #pragma unroll
@@ -227,21 +267,22 @@ __global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const T* __restric
         out[e] = x[e] * cv[e] + sgn * y * sv[e];
       }
       if (valid) {
-        T* dst = isq ? qo + ((int64_t)row * nq + head) * D : ko + ((int64_t)row * nk + (head - nq)) * D;
-        Vec16<T>::store(dst + c0, out);
+        TO* dst = isq ? qo + ((int64_t)row * nq + head) * D : ko + ((int64_t)row * nk + (head - nq)) * D;
+        st_elems<TO, EPL>(dst + c0, out);
       }
     }
   }
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk,
-                                                              const T* __restrict__ qkv, int64_t ld, const T* wq,
-                                                              const T* wk, const int64_t* __restrict__ pos,
+// TI: element type of dq, dk and the qkv input; TO: element type of dqkv and the norm weights.
+template <typename TI, typename TO, int D>
+__global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const TI* __restrict__ dq, const TI* __restrict__ dk,
+                                                              const TI* __restrict__ qkv, int64_t ld, const TO* wq,
+                                                              const TO* wk, const int64_t* __restrict__ pos,
                                                               const float* __restrict__ inv_freq,
-                                                              const float* __restrict__ rstd, T* __restrict__ dqkv,
+                                                              const float* __restrict__ rstd, TO* __restrict__ dqkv,
                                                               int64_t ldd, int M, int nq, int nk) {
-  constexpr int EPL = Vec16<T>::N, LPH = D / EPL, HPW = 64 / LPH, HALF = D / 2;
+  constexpr int EPL = Vec16<TI>::N, LPH = D / EPL, HPW = 64 / LPH, HALF = D / 2;
   static_assert(LPH >= 2 && LPH <= 64 && 64 % LPH == 0, "head geometry");
   __shared__ float s_cs[4][HALF], s_sn[4][HALF];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -260,8 +301,8 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const T* __restric
   const bool norm = wq != nullptr;
   float wqv[EPL], wkv[EPL];
   if (norm) {
-    Vec16<T>::load(wq + c0, wqv);
-    Vec16<T>::load(wk + c0, wkv);
+    ld_elems<TO, EPL>(wq + c0, wqv);
+    ld_elems<TO, EPL>(wk + c0, wkv);
   }
   // As in the forward: each group's loads (upstream gradient, input row, rstd) go out before its
   // arithmetic.
@@ -285,7 +326,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const T* __restric
       const bool valid = head < nh;
       const bool isq = head < nq;
       float dy[EPL];
-      Vec16<T>::unpack(rdy[gi], dy);
+      Vec16<TI>::unpack(rdy[gi], dy);
       float g[EPL];
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
@@ -295,7 +336,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const T* __restric
       if (norm) {
         const float r = rs[gi];
         float x[EPL];
-        Vec16<T>::unpack(rx[gi], x);
+        Vec16<TI>::unpack(rx[gi], x);
         float dot = 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
@@ -309,13 +350,13 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const T* __restric
 #pragma unroll
         for (int e = 0; e < EPL; ++e) g[e] = r * (g[e] - x[e] * dot);
       }
-      if (valid) Vec16<T>::store(dqkv + (int64_t)row * ldd + (int64_t)head * D + c0, g);
+      if (valid) st_elems<TO, EPL>(dqkv + (int64_t)row * ldd + (int64_t)head * D + c0, g);
     }
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// SwiGLU on the fused gate|up projection: out = round(silu(g)) * u.
+// SwiGLU on the fused gate|up projection: out = silu(g) * u in fp32, rounded once at the store.
 // ---------------------------------------------------------------------------------------
 
 template <typename T>
@@ -330,7 +371,7 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const T* __restrict__ g
     load_vec(gu + row * ld + c, g);
     load_vec(gu + row * ld + F + c, u);
 #pragma unroll
-    for (int e = 0; e < V; ++e) o[e] = Elem<T>::round(g[e] * sigmoidf_(g[e])) * u[e];
+    for (int e = 0; e < V; ++e) o[e] = g[e] * sigmoidf_(g[e]) * u[e];
     store_vec(out + row * F + c, o);
   }
 }
@@ -453,31 +494,44 @@ UNOK_EXPORT int unok_rmsnorm_bwd(int dtype, int M, int H, const void* dy, const 
   DISPATCH_T(dtype, return rmsnorm_bwd_t<T>(M, H, dy, x, w, rstd, dres, dx, (hipStream_t)stream));
 }
 
-UNOK_EXPORT int unok_qknorm_rope_fwd(int dtype, int M, int nq, int nk, int d, const void* qkv, int64_t ld,
-                                     const void* wq, const void* wk, const int64_t* pos, const float* inv_freq,
-                                     float eps, void* q_out, void* k_out, float* rstd, void* stream) {
+// Input / output element-type pairs of the q/k-norm kernels: (fp32, fp32), (bf16, bf16) and
+// (fp32 in, bf16 out).
+#define QKR_DISPATCH(TO_CODE, TI_CODE, ...)                                                          \
+  do {                                                                                              \
+    if ((TO_CODE) == UNOK_F32 && (TI_CODE) == UNOK_F32) { using TO = float; using TI = float; __VA_ARGS__; }  \
+    else if ((TO_CODE) == UNOK_BF16 && (TI_CODE) == UNOK_BF16) { using TO = bf16_t; using TI = bf16_t; __VA_ARGS__; } \
+    else if ((TO_CODE) == UNOK_BF16 && (TI_CODE) == UNOK_F32) { using TO = bf16_t; using TI = float; __VA_ARGS__; } \
+    else return unok::set_error(UNOK_EINVAL, "qknorm_rope: unsupported element types (out %d, in %d)", \
+                                (int)(TO_CODE), (int)(TI_CODE));                                    \
+  } while (0)
+
+UNOK_EXPORT int unok_qknorm_rope_fwd(int dtype, int qkv_dtype, int M, int nq, int nk, int d, const void* qkv,
+                                     int64_t ld, const void* wq, const void* wk, const int64_t* pos,
+                                     const float* inv_freq, float eps, void* q_out, void* k_out, void* v_out,
+                                     int64_t ldv, float* rstd, void* stream) {
   if (M == 0) return 0;
   UNOK_REQUIRE((d == 64 || d == 128) && nq > 0 && nk >= 0, UNOK_EINVAL, "qknorm_rope: head dim %d not in {64,128}", d);
   UNOK_REQUIRE((wq == nullptr) == (wk == nullptr), UNOK_EINVAL, "qknorm_rope: q and k norms must both be given");
-  UNOK_REQUIRE(ld % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)q_out & 15) == 0 && ((uintptr_t)k_out & 15) == 0,
+  UNOK_REQUIRE(ld % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)q_out & 15) == 0 && ((uintptr_t)k_out & 15) == 0 &&
+                   (v_out == nullptr || (ldv % 8 == 0 && ((uintptr_t)v_out & 15) == 0)),
                UNOK_EALIGN, "qknorm_rope: rows must be 16-byte aligned");
   const int blocks = (M + 3) / 4;
   hipStream_t st = (hipStream_t)stream;
   if (d == 128)
-    DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_fwd_kernel<T, 128>), dim3(blocks), dim3(256), 0, st, (const T*)qkv,
-                                         ld, (const T*)wq, (const T*)wk, pos, inv_freq, (T*)q_out, (T*)k_out, rstd, M,
-                                         nq, nk, eps));
+    QKR_DISPATCH(dtype, qkv_dtype, hipLaunchKernelGGL((qknorm_rope_fwd_kernel<TI, TO, 128>), dim3(blocks), dim3(256), 0,
+                                                      st, (const TI*)qkv, ld, (const TO*)wq, (const TO*)wk, pos, inv_freq,
+                                                      (TO*)q_out, (TO*)k_out, (TO*)v_out, ldv, rstd, M, nq, nk, eps));
   else
-    DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_fwd_kernel<T, 64>), dim3(blocks), dim3(256), 0, st, (const T*)qkv,
-                                         ld, (const T*)wq, (const T*)wk, pos, inv_freq, (T*)q_out, (T*)k_out, rstd, M,
-                                         nq, nk, eps));
+    QKR_DISPATCH(dtype, qkv_dtype, hipLaunchKernelGGL((qknorm_rope_fwd_kernel<TI, TO, 64>), dim3(blocks), dim3(256), 0,
+                                                      st, (const TI*)qkv, ld, (const TO*)wq, (const TO*)wk, pos, inv_freq,
+                                                      (TO*)q_out, (TO*)k_out, (TO*)v_out, ldv, rstd, M, nq, nk, eps));
   return unok::check_launch("qknorm_rope_fwd");
 }
 
-UNOK_EXPORT int unok_qknorm_rope_bwd(int dtype, int M, int nq, int nk, int d, const void* dq, const void* dk,
-                                     const void* qkv, int64_t ld, const void* wq, const void* wk, const int64_t* pos,
-                                     const float* inv_freq, const float* rstd, void* dqkv, int64_t ldd,
-                                     void* stream) {
+UNOK_EXPORT int unok_qknorm_rope_bwd(int dtype, int in_dtype, int M, int nq, int nk, int d, const void* dq,
+                                     const void* dk, const void* qkv, int64_t ld, const void* wq, const void* wk,
+                                     const int64_t* pos, const float* inv_freq, const float* rstd, void* dqkv,
+                                     int64_t ldd, void* stream) {
   if (M == 0) return 0;
   UNOK_REQUIRE(d == 64 || d == 128, UNOK_EINVAL, "qknorm_rope_bwd: head dim %d not in {64,128}", d);
   UNOK_REQUIRE(ld % 8 == 0 && ldd % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)dqkv & 15) == 0 &&
@@ -486,13 +540,13 @@ UNOK_EXPORT int unok_qknorm_rope_bwd(int dtype, int M, int nq, int nk, int d, co
   const int blocks = (M + 3) / 4;
   hipStream_t st = (hipStream_t)stream;
   if (d == 128)
-    DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<T, 128>), dim3(blocks), dim3(256), 0, st, (const T*)dq,
-                                         (const T*)dk, (const T*)qkv, ld, (const T*)wq, (const T*)wk, pos, inv_freq, rstd,
-                                         (T*)dqkv, ldd, M, nq, nk));
+    QKR_DISPATCH(dtype, in_dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<TI, TO, 128>), dim3(blocks), dim3(256), 0,
+                                                     st, (const TI*)dq, (const TI*)dk, (const TI*)qkv, ld, (const TO*)wq,
+                                                     (const TO*)wk, pos, inv_freq, rstd, (TO*)dqkv, ldd, M, nq, nk));
   else
-    DISPATCH_T(dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<T, 64>), dim3(blocks), dim3(256), 0, st, (const T*)dq,
-                                         (const T*)dk, (const T*)qkv, ld, (const T*)wq, (const T*)wk, pos, inv_freq, rstd,
-                                         (T*)dqkv, ldd, M, nq, nk));
+    QKR_DISPATCH(dtype, in_dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<TI, TO, 64>), dim3(blocks), dim3(256), 0,
+                                                     st, (const TI*)dq, (const TI*)dk, (const TI*)qkv, ld, (const TO*)wq,
+                                                     (const TO*)wk, pos, inv_freq, rstd, (TO*)dqkv, ldd, M, nq, nk));
   return unok::check_launch("qknorm_rope_bwd");
 }
 

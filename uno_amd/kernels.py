@@ -254,28 +254,36 @@ def rmsnorm_bwd(dy, x, w, rstd, dres=None, out=None):
     return dx
 
 
-def qknorm_rope_fwd(qkv, nq, nk, d, wq, wk, pos, inv_freq, eps):
-    """Per-head q/k RMSNorm (when wq/wk are given) then RoPE; returns (q, k, rstd)."""
+def qknorm_rope_fwd(qkv, nq, nk, d, wq, wk, pos, inv_freq, eps, *, out_dtype=None, with_v=False):
+    """Per-head q/k RMSNorm (when wq/wk are given) then RoPE; returns (q, k, rstd), or (q, k, v, rstd)
+    with ``with_v`` (v: the v heads of qkv as a contiguous [M, nk*d] copy). ``out_dtype`` (default:
+    qkv's) may be bf16 for an fp32 qkv: the normalisation then sees the unrounded projection."""
     _rowmajor(qkv, "qkv")
     M = qkv.shape[0]
-    q = torch.empty((M, nq * d), device=qkv.device, dtype=qkv.dtype)
-    k = torch.empty((M, nk * d), device=qkv.device, dtype=qkv.dtype)
+    out_dtype = out_dtype or qkv.dtype
+    q = torch.empty((M, nq * d), device=qkv.device, dtype=out_dtype)
+    k = torch.empty((M, nk * d), device=qkv.device, dtype=out_dtype)
+    v = torch.empty((M, nk * d), device=qkv.device, dtype=out_dtype) if with_v else None
     rstd = torch.empty((M, nq + nk), device=qkv.device, dtype=torch.float32)
     if pos.dtype != torch.int64 or pos.numel() != M:
         raise RuntimeError("qknorm_rope: pos must be int64 [M]")
-    N.call("unok_qknorm_rope_fwd", N.dtype_code(qkv.dtype), M, nq, nk, d, N.ptr(qkv), _ld(qkv), N.ptr(wq),
-           N.ptr(wk), N.ptr(pos), N.ptr(inv_freq), float(eps), N.ptr(q), N.ptr(k), N.ptr(rstd), N.stream())
-    return q, k, rstd
+    N.call("unok_qknorm_rope_fwd", N.dtype_code(out_dtype), N.dtype_code(qkv.dtype), M, nq, nk, d, N.ptr(qkv),
+           _ld(qkv), N.ptr(wq), N.ptr(wk), N.ptr(pos), N.ptr(inv_freq), float(eps), N.ptr(q), N.ptr(k), N.ptr(v),
+           _ld(v) if v is not None else 0, N.ptr(rstd), N.stream())
+    return (q, k, v, rstd) if with_v else (q, k, rstd)
 
 
 def qknorm_rope_bwd(dq, dk, qkv, nq, nk, d, wq, wk, pos, inv_freq, rstd, dqkv):
-    """Writes the q and k column blocks of ``dqkv`` ([M, (nq+2nk)*d])."""
+    """Writes the q and k column blocks of ``dqkv`` ([M, (nq+2nk)*d]); dq, dk and qkv share one
+    dtype, dqkv's or fp32."""
     _contig(dq, "dq")
     _contig(dk, "dk")
+    if dq.dtype != qkv.dtype or dk.dtype != qkv.dtype:
+        raise RuntimeError("qknorm_rope_bwd: dq, dk and qkv must share a dtype")
     M = qkv.shape[0]
-    N.call("unok_qknorm_rope_bwd", N.dtype_code(qkv.dtype), M, nq, nk, d, N.ptr(dq), N.ptr(dk), N.ptr(qkv),
-           _ld(qkv), N.ptr(wq), N.ptr(wk), N.ptr(pos), N.ptr(inv_freq), N.ptr(rstd), N.ptr(dqkv), _ld(dqkv),
-           N.stream())
+    N.call("unok_qknorm_rope_bwd", N.dtype_code(dqkv.dtype), N.dtype_code(qkv.dtype), M, nq, nk, d, N.ptr(dq),
+           N.ptr(dk), N.ptr(qkv), _ld(qkv), N.ptr(wq), N.ptr(wk), N.ptr(pos), N.ptr(inv_freq), N.ptr(rstd),
+           N.ptr(dqkv), _ld(dqkv), N.stream())
     return dqkv
 
 
@@ -466,15 +474,20 @@ def decode_prep(qkv, wq, wk, lengths, inv_freq, eps: float, kc, vc, qd, B: int, 
 
 
 def attn_bwd(q, k1, v1, iv, o, lse, do, Hq, Hkv, D, *, k2=None, v2=None, ivk=None, dk=None, dv=None,
-             scale=None):
-    """Returns dQ; writes dK/dV of source-2 keys into ``dk``/``dv`` when given."""
+             scale=None, grad_dtype=None):
+    """Returns dQ; writes dK/dV of source-2 keys into ``dk``/``dv`` when given. ``grad_dtype`` (default
+    q's) is the dtype of dQ and dK, fp32 allowed for bf16 inputs; dV has q's dtype."""
     Mq = q.shape[0]
     scale = D ** -0.5 if scale is None else scale
+    grad_dtype = grad_dtype or q.dtype
     _contig(do, "do")
-    dq = torch.empty((Mq, Hq * D), device=q.device, dtype=q.dtype)
+    if dk is not None and dk.dtype != grad_dtype:
+        raise RuntimeError("attn_bwd: dk must have the gradient dtype")
+    dq = torch.empty((Mq, Hq * D), device=q.device, dtype=grad_dtype)
     dsum = torch.empty((Mq, Hq), device=q.device, dtype=torch.float32)
     Mk2 = k2.shape[0] if k2 is not None else 0
-    N.call("unok_attn_bwd", N.dtype_code(q.dtype), Mq, Mk2, Hq, Hkv, D, N.ptr(q), _ld(q), N.ptr(k1), _ld(k1),
+    N.call("unok_attn_bwd", N.dtype_code(q.dtype), N.dtype_code(grad_dtype), Mq, Mk2, Hq, Hkv, D, N.ptr(q), _ld(q),
+           N.ptr(k1), _ld(k1),
            N.ptr(v1), _ld(v1), N.ptr(k2), _ld(k2) if k2 is not None else 0, N.ptr(v2),
            _ld(v2) if v2 is not None else 0, N.ptr(iv), N.ptr(ivk), N.ptr(o), _ld(o), N.ptr(lse), N.ptr(do),
            _ld(do), N.ptr(dsum), N.ptr(dq), _ld(dq), N.ptr(dk), _ld(dk) if dk is not None else 0, N.ptr(dv),

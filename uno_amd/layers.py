@@ -72,13 +72,30 @@ class StreamContext:
     clean_v: list
 
 
+def _qkv_dtype(x: torch.Tensor):
+    """Element type of the q/k/v projection output. A bf16 step keeps it in fp32: the q/k
+    normalisation and rotation then round once, at their output (the step's LoRA gradients are most
+    sensitive to the precision of q and k); v is copied out in bf16 for the attention kernels."""
+    return torch.float32 if x.dtype == torch.bfloat16 else x.dtype
+
+
+def project_qk_v(x1, lw: LayerWeights, g: Geometry, sc: StreamContext, a2=None, b2=None, segments=None):
+    """q/k/v projection (with its LoRA extension), q/k norm and RoPE: (qkv, q, k, v, rstd)."""
+    qkv = K.gemm_nt(x1, lw.w_qkv, a2=a2, b2=b2, segments=segments, out_dtype=_qkv_dtype(x1))
+    if qkv.dtype == x1.dtype:
+        q, k, rstd = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
+        v = qkv[:, g.q + g.kv:]   # a strided view: the attention kernels take V's row stride, no copy
+    else:
+        q, k, v, rstd = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps,
+                                          out_dtype=x1.dtype, with_v=True)
+    return qkv, q, k, v, rstd
+
+
 def clean_layer(h: torch.Tensor, lw: LayerWeights, g: Geometry, sc: StreamContext):
     """Forward-only clean-stream layer; returns (h_out, k, v) with k/v kept for the noisy stream."""
     M = h.shape[0]
     x1, _ = K.rmsnorm_fwd(h, lw.ln_in, g.eps)
-    qkv = K.gemm_nt(x1, lw.w_qkv)
-    q, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
-    v = qkv[:, g.q + g.kv:]   # a strided view: the attention kernels take V's row stride, no copy
+    _, q, k, v, _ = project_qk_v(x1, lw, g, sc)
     o, _ = K.attn_fwd(q, k, v, sc.iv_clean, g.nq, g.nk, g.d)
     h1 = K.gemm_nt(o, lw.w_o, residual=h)
     x2, _ = K.rmsnorm_fwd(h1, lw.ln_post, g.eps)
@@ -94,9 +111,8 @@ def clean_layer_kv(h: torch.Tensor, lw: LayerWeights, g: Geometry, sc: StreamCon
     """The K and V a clean-stream layer hands the noisy stream, without the layer's output (its
     attention, o projection and MLP): the same kernels and values as clean_layer's k and v."""
     x1, _ = K.rmsnorm_fwd(h, lw.ln_in, g.eps)
-    qkv = K.gemm_nt(x1, lw.w_qkv)
-    _, k, _ = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
-    return k, qkv[:, g.q + g.kv:]
+    _, _, k, v, _ = project_qk_v(x1, lw, g, sc)
+    return k, v
 
 
 def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: StreamContext, need_output: bool = True):
@@ -108,10 +124,9 @@ def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: St
     on = lora.group_active     # a fused group with no adapter runs as a plain product
     x1, rstd1 = K.rmsnorm_fwd(h0, lw.ln_in, g.eps)
     h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv")) if on("qkv") else None
-    qkv = K.gemm_nt(x1, lw.w_qkv, a2=h_qkv, b2=lora.sb_c(li, "qkv") if on("qkv") else None,
-                    segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)] if on("qkv") else None)
-    q, k, rstd_qk = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
-    v = qkv[:, k_end:]
+    qkv, q, k, v, rstd_qk = project_qk_v(
+        x1, lw, g, sc, a2=h_qkv, b2=lora.sb_c(li, "qkv") if on("qkv") else None,
+        segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)] if on("qkv") else None)
     o, lse = K.attn_fwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, g.nq, g.nk, g.d, k2=k, v2=v)
     h_o = K.gemm_nt(o, lora.a_c(li, "o")) if on("o") else None
     h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o") if on("o") else None, residual=h0)
@@ -130,13 +145,14 @@ def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: St
     h_d = K.gemm_nt(s, lora.a_c(li, "d")) if on("d") else None
     h2 = K.gemm_nt(s, lw.w_d, a2=h_d, b2=lora.sb_c(li, "d") if on("d") else None, residual=h1) \
         if need_output else None
-    return h2, (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d)
+    return h2, (h0, x1, rstd1, h_qkv, qkv, q, k, v, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d)
 
 
 def saved_bytes_per_row(g: Geometry, rank: int, elem: int) -> int:
     """Bytes of activations one noisy-stream layer keeps per token row for its backward."""
-    stored = 4 * g.H + (g.q + 2 * g.kv) + g.q + g.kv + g.q + 3 * g.F + 7 * rank
-    return stored * elem + 4 * (2 + g.nq + g.nk + g.nq)
+    stored = 4 * g.H + g.q + g.kv + g.q + 3 * g.F + 7 * rank
+    qkv = (g.q + 2 * g.kv) * (4 if elem == 2 else elem) + (g.kv * elem if elem == 2 else 0)
+    return stored * elem + qkv + 4 * (2 + g.nq + g.nk + g.nq)
 
 
 def _lora_inner_grads(lora, li: int, group: str, dy, h, cols, scale):
@@ -182,7 +198,7 @@ class NoisyLayer(torch.autograd.Function):
         bufs = ctx.bufs
         if bufs is None:
             _, bufs = noisy_layer_forward(ctx.h0, lw, lora, li, g, sc, need_output=False)
-        (h0, x1, rstd1, h_qkv, qkv, q, k, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d) = bufs
+        (h0, x1, rstd1, h_qkv, qkv, q, k, v, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d) = bufs
         ctx.bufs = ctx.h0 = bufs = None
         dh2 = dh2.contiguous()
         M = dh2.shape[0]
@@ -220,10 +236,12 @@ class NoisyLayer(torch.autograd.Function):
         if on("o"):
             K.gemm_tn(g_o, o, out=ga(li, "o"), beta=1.0)
         # ---- attention -----------------------------------------------------------------
-        dqkv = torch.empty_like(qkv)
-        dk = torch.empty((M, g.kv), device=dh2.device, dtype=dh2.dtype)
+        # dq and dk in the q/k/v projection's precision (fp32 for a bf16 step) up to the q/k norm
+        # backward, which writes the bf16 q/k gradient blocks of dqkv; dv goes straight into dqkv
+        dqkv = torch.empty((M, g.q + 2 * g.kv), device=dh2.device, dtype=dh2.dtype)
+        dk = torch.empty((M, g.kv), device=dh2.device, dtype=qkv.dtype)
         dq = K.attn_bwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, o, lse, do, g.nq, g.nk, g.d,
-                        k2=k, v2=qkv[:, k_end:], ivk=sc.iv_noisy, dk=dk, dv=dqkv[:, k_end:])
+                        k2=k, v2=v, ivk=sc.iv_noisy, dk=dk, dv=dqkv[:, k_end:], grad_dtype=qkv.dtype)
         del do
         K.qknorm_rope_bwd(dq, dk, qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, rstd_qk, dqkv)
         del dq, dk
