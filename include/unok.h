@@ -132,11 +132,27 @@ int unok_qknorm_rope_fwd(int dtype, int qkv_dtype, int M, int nq, int nk, int d,
                          int64_t ld, const void* wq, const void* wk, const int64_t* pos,
                          const float* inv_freq, float eps, void* q_out, void* k_out, void* v_out,
                          int64_t ldv, float* rstd, void* stream);
-/* dtype: dqkv and the weights; in_dtype: dq, dk and qkv (dtype, or fp32 with a bf16 dqkv). */
-int unok_qknorm_rope_bwd(int dtype, int in_dtype, int M, int nq, int nk, int d, const void* dq,
-                         const void* dk, const void* qkv, int64_t ld, const void* wq,
+/* dtype: dqkv and the weights; grad_dtype: dq and dk (dtype, or fp32 with a bf16 dqkv); x_dtype:
+ * the pre-norm q/k columns read from qkv (row stride ld): grad_dtype, or bf16 beside fp32 gradients. */
+int unok_qknorm_rope_bwd(int dtype, int grad_dtype, int x_dtype, int M, int nq, int nk, int d,
+                         const void* dq, const void* dk, const void* qkv, int64_t ld, const void* wq,
                          const void* wk, const int64_t* pos, const float* inv_freq,
                          const float* rstd, void* dqkv, int64_t ldd, void* stream);
+/* cos_tab / sin_tab [P, half] = cos / sin of fl32(p * inv_freq[j]): the RoPE angles of the fused
+ * q|k|v projection epilogue (modeling_qwen3.py:140-160). */
+int unok_rope_table(int P, int half, const float* inv_freq, float* cos_tab, float* sin_tab, void* stream);
+
+/* q|k|v projection (+ LoRA extension) with the q/k RMSNorm and RoPE in the GEMM epilogue, bf16, head
+ * dim 128: the product stays fp32 until each q/k head is normalised (wq / wk, or both null), scaled
+ * and rotated, then q [M, 128 nq], k and v [M, 128 nk] are stored in bf16; rstd [M, nq+nk] and the
+ * pre-norm q/k columns in bf16, qk_pre [M, 128 (nq+nk)], when non-null. Replaces the q/k/v
+ * projections of the remote Qwen3 attention with their gated LoRA (modeling_qwen3.py:237-253,
+ * training/lora.py:164-174). M and 128 (nq + 2 nk) multiples of 256, K of 64, K2 of 32. */
+int unok_gemm_nt_qkv_rope(int M, int K, int nq, int nk, const void* A, int64_t lda, const void* B,
+                          int64_t ldb, const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,
+                          int nseg, const int* seg_end, const int* seg_col, const void* wq, const void* wk,
+                          const int64_t* pos, const float* cos_tab, const float* sin_tab, int P, float eps,
+                          void* q_out, void* k_out, void* v_out, float* rstd, void* qk_pre, void* stream);
 
 /* out = silu(gate) * up over the fused [gate | up] projection, rounded once (modeling_qwen3.py:81-82). */
 int unok_swiglu_fwd(int dtype, int M, int F, const void* gu, int64_t ld, void* out, void* stream);
@@ -218,9 +234,11 @@ int unok_bd_prepare(int B, int L, const int64_t* ids, const int64_t* pos, const 
  * calculate_token_nums + _build_noisy_region_mask of prepare_uno_layout
  * (training/modeling.py:65-81,84-98). */
 int unok_bd_region(int B, int L, const int64_t* pos, uint8_t* region, void* stream);
-/* p_mask = noise level of every noised token in row-major order (training/trainer.py:278). */
-int unok_bd_compact(int64_t n, const uint8_t* noised, const float* tfull, float* p_mask,
-                    int32_t* count, void* stream);
+/* p_mask = noise level of every noised token in row-major order (training/trainer.py:278);
+ * count[0] = their number and, when pos [n] is non-null, count[1] = the largest position (clamped to
+ * [0, 2^31 - 1]), which sizes the RoPE tables. */
+int unok_bd_compact(int64_t n, const uint8_t* noised, const float* tfull, const int64_t* pos,
+                    float* p_mask, int32_t* count, void* stream);
 
 /* ---- Objectives ------------------------------------------------------------------------------ */
 

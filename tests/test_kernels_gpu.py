@@ -126,6 +126,52 @@ def test_qknorm_rope_fp32_in_bf16_out(dev, nq, nk):
         K.qknorm_rope_bwd(dq.bfloat16().contiguous(), dk.contiguous(), qkv, nq, nk, d, wq, wk, pos, inv, rstd, dqkv)
 
 
+@pytest.mark.parametrize("nq,nk,norm,lora", [(32, 8, True, True), (16, 8, True, False), (8, 8, False, True)])
+def test_qkv_projection_rope_epilogue(dev, nq, nk, norm, lora):
+    """The q|k|v GEMM with q/k norm + RoPE in its epilogue against the same GEMM into fp32 followed by
+    the stand-alone q/k-norm kernel: v and the bf16 pre-norm q/k bit-identical to rounding the fp32
+    product, q and k within one bf16 step of the two-kernel path, rstd to fp32 rounding; the q/k-norm
+    backward from those bf16 pre-norm columns close to the one from the fp32 product."""
+    torch.manual_seed(12)
+    M, H, r, d = 8192, 1024, 32, 128     # both paths on the 256 x 256 kernel (the same accumulation)
+    q_end, k_end, N = nq * d, (nq + nk) * d, (nq + 2 * nk) * d
+    x = (torch.randn(M, H, device=dev) * 0.5).bfloat16()
+    w = (torch.randn(N, H, device=dev) * 0.03).bfloat16()
+    kw = {}
+    if lora:
+        kw = dict(a2=(torch.randn(M, 3 * r, device=dev) * 0.3).bfloat16(),
+                  b2=(torch.randn(N, r, device=dev) * 0.05).bfloat16(), segments=[(q_end, 0), (k_end, r), (N, 2 * r)])
+    wq = (1 + 0.1 * torch.randn(d, device=dev)).bfloat16() if norm else None
+    wk = (1 + 0.1 * torch.randn(d, device=dev)).bfloat16() if norm else None
+    pos = (torch.arange(M, device=dev) % 3000) + 7      # segment-like resets, largest position 3006
+    inv = (1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))).to(dev)
+    cos, sin = K.rope_table(int(pos.max()) + 1, inv)
+    qf, kf, vf, rf, pre = K.gemm_nt_qkv_rope(x, w, nq, nk, wq, wk, pos, cos, sin, 1e-6, want_pre=True, **kw)
+    qkv = K.gemm_nt(x, w, out_dtype=torch.float32, **kw)
+    q2, k2, v2, r2 = K.qknorm_rope_fwd(qkv, nq, nk, d, wq, wk, pos, inv, 1e-6, out_dtype=torch.bfloat16, with_v=True)
+    assert torch.equal(vf, v2) and torch.equal(vf, qkv[:, k_end:].bfloat16())
+    assert torch.equal(pre, qkv[:, :k_end].bfloat16())
+
+    # the two paths contract the rotation's multiply-adds differently: the same values up to fp32
+    # rounding before the one bf16 rounding (a bf16 step apart where that rounding tips, more steps
+    # only where the rotated value cancels to near zero)
+    for a, b in ((qf, q2), (kf, k2)):
+        diff = (a.float() - b.float()).abs()
+        step = b.float().abs().clamp_min(b.float().abs().max() * 2 ** -8) * 2 ** -7
+        print(f"[qkv epilogue] rel L2 {rel(a, b):.2e}; elements more than one bf16 step apart at their "
+              f"magnitude: {int((diff > step).sum())} of {diff.numel()}", flush=True)
+        assert rel(a, b) < 2e-3 and bool((diff <= step).all())
+    if norm:
+        assert torch.allclose(rf, r2, rtol=1e-6, atol=0)
+    dq = torch.randn(M, q_end, device=dev)
+    dk = torch.randn(M, k_end - q_end, device=dev)
+    d1 = torch.zeros(M, N, device=dev, dtype=torch.bfloat16)
+    d2 = torch.zeros_like(d1)
+    K.qknorm_rope_bwd(dq, dk, pre, nq, nk, d, wq, wk, pos, inv, rf, d1)
+    K.qknorm_rope_bwd(dq, dk, qkv, nq, nk, d, wq, wk, pos, inv, r2, d2)
+    assert rel(d1[:, :k_end], d2[:, :k_end]) < 5e-3
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_swiglu_fwd_bwd(dev, dtype):
     torch.manual_seed(2)

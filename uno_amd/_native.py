@@ -38,7 +38,10 @@ SIGNATURES: dict[str, tuple] = {
     "unok_rmsnorm_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _p, _i64, _p, _f, _p]),
     "unok_rmsnorm_bwd": (_i, [_i, _i, _i, _p, _p, _p, _p, _p, _p, _p]),
     "unok_qknorm_rope_fwd": (_i, [_i, _i, _i, _i, _i, _i, _p, _i64, _p, _p, _p, _p, _f, _p, _p, _p, _i64, _p, _p]),
-    "unok_qknorm_rope_bwd": (_i, [_i, _i, _i, _i, _i, _i, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "unok_qknorm_rope_bwd": (_i, [_i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "unok_rope_table": (_i, [_i, _i, _p, _p, _p, _p]),
+    "unok_gemm_nt_qkv_rope": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i, _i, _ip, _ip, _p, _p,
+                                   _p, _p, _p, _i, _f, _p, _p, _p, _p, _p, _p]),
     "unok_swiglu_fwd": (_i, [_i, _i, _i, _p, _i64, _p, _p]),
     "unok_swiglu_bwd": (_i, [_i, _i, _i, _p, _p, _i64, _p, _i64, _p]),
     "unok_embedding": (_i, [_i, _i, _i, _p, _p, _i64, _p, _p]),
@@ -53,7 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "unok_bd_prepare": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _u64, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                              _p, _p, _p]),
     "unok_bd_region": (_i, [_i, _i, _p, _p, _p]),
-    "unok_bd_compact": (_i, [_i64, _p, _p, _p, _p, _p]),
+    "unok_bd_compact": (_i, [_i64, _p, _p, _p, _p, _p, _p]),
     "unok_row_lse_update": (_i, [_i, _i, _i, _p, _i64, _i, _p, _p, _p, _p, _i, _p]),
     "unok_lmhead_ce_stats": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i, _p, _p, _i64, _p, _p]),
     "unok_ce_parts_reduce": (_i, [_i, _i, _p, _p, _i64, _p, _p, _p]),

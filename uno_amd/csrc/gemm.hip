@@ -46,6 +46,17 @@ struct GemmNT {
   const float* ce_lse;             // EPI 4: [M] log-sum-exp over the whole vocabulary
   const float* ce_w;               // EPI 4: [M] row weights; scaled by *ce_g * *ce_inv_n
   const float* ce_g; const float* ce_inv_n;
+  // q|k|v projection epilogue (EPI 5): head dim 128; columns [0, 128 nq) are q heads, then nk k
+  // heads, then nk v heads. q/k heads are normalised (when qk_wq is set), scaled by the weight and
+  // rotated in fp32, then rounded once into qk_q / qk_k; v heads are rounded into qk_v.
+  void* qk_q; void* qk_k; void* qk_v;
+  void* qk_pre;                    // [M, 128 (nq+nk)] bf16 q/k before the norm, or null
+  float* qk_rstd;                  // [M, nq+nk] 1/rms per row and q/k head, or null
+  const void* qk_wq; const void* qk_wk;
+  const int64_t* qk_pos;           // [M] position of each row
+  const float* qk_cos; const float* qk_sin;   // [qk_P, 64] cos / sin of fl32(position * inv_freq[j])
+  int qk_P, qk_nq, qk_nk;
+  float qk_eps;
 };
 
 template <typename T> __device__ __forceinline__ float ld_f(const T* p);
@@ -1294,6 +1305,95 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     }
     return;
   }
+  if constexpr (EPI == 5) {
+    // q|k|v projection: each wave's 128 columns are one head. The quadrant is staged through LDS
+    // in fp32 as for the plain epilogue; each row is then handled by 16 lanes of 8 columns: sum
+    // of squares over the head (lane shuffles), normalisation and weight, rotate_half RoPE (the
+    // partner column +-64 sits 8 lanes away), one rounding, 16-byte stores. Interior tiles only
+    // (the caller requires M and N to be multiples of 256).
+    const int rsub = lane >> 4, c16 = lane & 15;
+    const int64_t rowb = m0 + wm * 128 + rsub;
+    const int head = (n0 + wn * 128) >> 7;
+    const int nq = p.qk_nq, nqk = p.qk_nq + p.qk_nk;
+    const bool isv = head >= nqk, isq = head < nq;
+    const int c0 = 8 * c16;
+    bf16_t* dst;
+    int64_t ldd;
+    if (isq) { dst = (bf16_t*)p.qk_q + (int64_t)head * 128 + c0; ldd = (int64_t)nq * 128; }
+    else if (!isv) { dst = (bf16_t*)p.qk_k + (int64_t)(head - nq) * 128 + c0; ldd = (int64_t)p.qk_nk * 128; }
+    else { dst = (bf16_t*)p.qk_v + (int64_t)(head - nqk) * 128 + c0; ldd = (int64_t)p.qk_nk * 128; }
+    const bool norm = !isv && p.qk_wq != nullptr;
+    float wv[8];
+    if (norm) {
+      const uint4 u = *(const uint4*)((const bf16_t*)(isq ? p.qk_wq : p.qk_wk) + c0);
+      const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { wv[2 * e] = __uint_as_float(w4[e] << 16); wv[2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u); }
+    }
+    const int f0 = c0 & 63;                   // angle index of this lane's first column
+    const float sgn = c0 < 64 ? -1.f : 1.f;   // rotate_half: -x[c+64] in the first half, x[c-64] in the second
+    asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed
+    float* q = (float*)smem + wid * 64 * 128;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int r = i * 16 + lr;
+          f32x4_t v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[4 * h + i][j][e] * p.alpha;
+          *(f32x4_t*)&q[r * 128 + (((4 * j + lk) ^ (r & 15)) << 2)] = v;
+        }
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll 2
+      for (int it = 0; it < 16; ++it) {
+        const int r = it * 4 + rsub;
+        const f32x4_t v0 = *(const f32x4_t*)&q[r * 128 + (((2 * c16) ^ (r & 15)) << 2)];
+        const f32x4_t v1 = *(const f32x4_t*)&q[r * 128 + (((2 * c16 + 1) ^ (r & 15)) << 2)];
+        const int64_t row = rowb + 64 * h + it * 4;
+        float x[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        float out[8];
+        if (isv) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out[e] = x[e];
+        } else {
+          if (p.qk_pre)
+            *(uint4*)((bf16_t*)p.qk_pre + row * ((int64_t)nqk * 128) + (int64_t)head * 128 + c0) =
+                make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
+          int64_t pr = p.qk_pos[row];
+          pr = pr < 0 ? 0 : (pr >= p.qk_P ? p.qk_P - 1 : pr);
+          const float4 ca = *(const float4*)(p.qk_cos + pr * 64 + f0), cb = *(const float4*)(p.qk_cos + pr * 64 + f0 + 4);
+          const float4 sa = *(const float4*)(p.qk_sin + pr * 64 + f0), sb = *(const float4*)(p.qk_sin + pr * 64 + f0 + 4);
+          const float cv[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+          const float sv[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+          if (norm) {
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            const float rs = rsqrtf(ss / 128.f + p.qk_eps);
+            if (c16 == 0 && p.qk_rstd) p.qk_rstd[row * nqk + head] = rs;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = x[e] * rs * wv[e];
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float y = __shfl_xor(x[e], 8, 64);   // partner column +- 64
+            out[e] = x[e] * cv[e] + sgn * y * sv[e];
+          }
+        }
+        *(uint4*)(dst + row * ldd) = make_uint4(pack2_bf16(out[0], out[1]), pack2_bf16(out[2], out[3]),
+                                                pack2_bf16(out[4], out[5]), pack2_bf16(out[6], out[7]));
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);     // the half's reads are done before the next overwrites
+      __builtin_amdgcn_wave_barrier();
+    }
+    return;
+  }
   const bool interior = m0 + BM <= p.M && n0 + BN <= p.N && p.gate == nullptr;
   if constexpr (EPI == 0 && std::is_same<OutT, bf16_t>::value) {
     if (interior && (p.ldc & 7) == 0 && (!R || (p.ldr & 7) == 0)) {
@@ -1442,6 +1542,55 @@ UNOK_EXPORT int unok_gemm_nt_swiglu(int M, int N, int K, const void* A, int64_t 
   UNOK_REQUIRE(buffer_ranges_ok(p), UNOK_EINVAL, "gemm_nt_swiglu: operands exceed 32-bit buffer offsets");
   launch_nt_w4m16<bf16_t, 1>(p, (hipStream_t)stream);
   return unok::check_launch("gemm_nt_swiglu");
+}
+
+// q|k|v projection with the q/k RMSNorm and RoPE in its epilogue (bf16, head dim 128): the product
+// A[M,K] B[N,K]^T (+ the LoRA extension, up to 4 segments as in unok_gemm_nt), N = 128 (nq + 2 nk),
+// stays in fp32 until each q/k head is normalised (wq / wk, or neither), scaled by the weight and
+// rotated; q [M, 128 nq], k and v [M, 128 nk] are written contiguous in bf16, rstd [M, nq+nk] (when
+// non-null), and the q/k columns before the norm in bf16 into qk_pre [M, 128 (nq+nk)] (when
+// non-null). cos_tab / sin_tab [P, 64] hold cos / sin of fl32(p * inv_freq[j]) (unok_rope_table);
+// positions are clamped to [0, P). Same values as unok_gemm_nt into fp32 followed by
+// unok_qknorm_rope_fwd. M and N multiples of 256, K of 64, K2 of 32.
+UNOK_EXPORT int unok_gemm_nt_qkv_rope(int M, int K, int nq, int nk, const void* A, int64_t lda, const void* B,
+                                      int64_t ldb, const void* A2, int64_t lda2, const void* B2, int64_t ldb2, int K2,
+                                      int nseg, const int* seg_end, const int* seg_col, const void* wq, const void* wk,
+                                      const int64_t* pos, const float* cos_tab, const float* sin_tab, int P, float eps,
+                                      void* q_out, void* k_out, void* v_out, float* rstd, void* qk_pre, void* stream) {
+  UNOK_REQUIRE(M >= 0 && K >= 0 && K2 >= 0 && nq > 0 && nk > 0 && P > 0, UNOK_EINVAL,
+               "gemm_nt_qkv_rope: bad sizes M=%d K=%d nq=%d nk=%d P=%d", M, K, nq, nk, P);
+  if (M == 0) return 0;
+  const int N = 128 * (nq + 2 * nk);
+  const bool ext = A2 != nullptr && K2 > 0;
+  UNOK_REQUIRE(M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && K > 0 && (!ext || K2 % 32 == 0) && nseg >= 0 &&
+                   nseg <= 4 && (wq == nullptr) == (wk == nullptr),
+               UNOK_EINVAL, "gemm_nt_qkv_rope: M=%d and N=%d must be multiples of 256, K=%d of 64, K2=%d of 32", M, N,
+               K, K2);
+  UNOK_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(q_out) && aligned16(k_out) &&
+                   aligned16(v_out) && (qk_pre == nullptr || aligned16(qk_pre)) && aligned16(cos_tab) &&
+                   aligned16(sin_tab) && (!ext || (lda2 % 8 == 0 && ldb2 % 8 == 0 && aligned16(A2) && aligned16(B2))),
+               UNOK_EALIGN, "gemm_nt_qkv_rope: row strides must be multiples of 8 and rows 16-byte aligned");
+  GemmNT p{};
+  p.A = A; p.lda = lda; p.B = B; p.ldb = ldb;
+  p.A2 = ext ? A2 : nullptr; p.lda2 = lda2; p.B2 = B2; p.ldb2 = ldb2;
+  p.C = q_out; p.ldc = 128 * nq;
+  p.M = M; p.N = N; p.K = K; p.K2 = ext ? K2 : 0; p.alpha = 1.f;
+  p.nseg = p.A2 ? (nseg > 0 ? nseg : 1) : 1;
+  for (int i = 0; i < 4; ++i) { p.seg_end[i] = N; p.seg_col[i] = 0; }
+  if (p.A2 && nseg > 0) {
+    for (int i = 0; i < nseg; ++i) {
+      p.seg_end[i] = seg_end[i]; p.seg_col[i] = seg_col[i];
+      UNOK_REQUIRE(seg_col[i] % 8 == 0 && (i + 1 == nseg || seg_end[i] % 256 == 0), UNOK_EINVAL,
+                   "gemm_nt_qkv_rope: segment %d (end %d, column %d) not tile-aligned", i, seg_end[i], seg_col[i]);
+    }
+    UNOK_REQUIRE(p.seg_end[nseg - 1] == N, UNOK_EINVAL, "gemm_nt_qkv_rope: last segment must end at N");
+  }
+  p.qk_q = q_out; p.qk_k = k_out; p.qk_v = v_out; p.qk_pre = qk_pre; p.qk_rstd = rstd;
+  p.qk_wq = wq; p.qk_wk = wk; p.qk_pos = pos; p.qk_cos = cos_tab; p.qk_sin = sin_tab; p.qk_P = P;
+  p.qk_nq = nq; p.qk_nk = nk; p.qk_eps = eps;
+  UNOK_REQUIRE(buffer_ranges_ok(p), UNOK_EINVAL, "gemm_nt_qkv_rope: operands exceed 32-bit buffer offsets");
+  launch_nt_w4m16<bf16_t, 5>(p, (hipStream_t)stream);
+  return unok::check_launch("gemm_nt_qkv_rope");
 }
 
 // dgu[M, 2F] = SwiGLU backward of dS = A[M,K] B[F,K]^T + A2[M,K2] B2[F,K2]^T (bf16, never stored)

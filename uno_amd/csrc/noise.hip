@@ -137,22 +137,31 @@ __global__ __launch_bounds__(1024) void bd_prepare_kernel(const BdArgs a) {
   }
 }
 
-// p_mask compaction over the row-major [B*L] noised flags (single workgroup, chunked scan).
+// p_mask compaction over the row-major [B*L] noised flags (single workgroup, chunked scan); with
+// positions, also their maximum (clamped to [0, 2^31 - 1]) into count[1], read back with the count.
 __global__ __launch_bounds__(1024) void bd_compact_kernel(const uint8_t* __restrict__ noised,
-                                                          const float* __restrict__ tfull, int64_t n,
+                                                          const float* __restrict__ tfull,
+                                                          const int64_t* __restrict__ pos, int64_t n,
                                                           float* __restrict__ p_mask, int32_t* __restrict__ count) {
   __shared__ int32_t part[1024];
+  __shared__ int64_t pmax[1024];
   const int tid = threadIdx.x;
   const int64_t chunk = (n + 1023) / 1024;
   const int64_t c0 = min(n, tid * chunk), c1 = min(n, c0 + chunk);
   int32_t cnt = 0;
+  int64_t mx = 0;
   for (int64_t i = c0; i < c1; ++i) cnt += noised[i] ? 1 : 0;
+  if (pos)
+    for (int64_t i = c0; i < c1; ++i) mx = max(mx, pos[i]);
   part[tid] = cnt;
+  pmax[tid] = mx;
   __syncthreads();
   if (tid == 0) {
     int32_t run = 0;
-    for (int i = 0; i < 1024; ++i) { const int32_t v = part[i]; part[i] = run; run += v; }
+    int64_t m = 0;
+    for (int i = 0; i < 1024; ++i) { const int32_t v = part[i]; part[i] = run; run += v; m = max(m, pmax[i]); }
     count[0] = run;
+    if (pos) count[1] = (int32_t)min(m, (int64_t)0x7fffffff);
   }
   __syncthreads();
   int32_t o = part[tid];
@@ -187,9 +196,10 @@ UNOK_EXPORT int unok_bd_region(int B, int L, const int64_t* pos, uint8_t* region
   return unok::check_launch("bd_region");
 }
 
-UNOK_EXPORT int unok_bd_compact(int64_t n, const uint8_t* noised, const float* tfull, float* p_mask, int32_t* count,
-                                void* stream) {
+UNOK_EXPORT int unok_bd_compact(int64_t n, const uint8_t* noised, const float* tfull, const int64_t* pos,
+                                float* p_mask, int32_t* count, void* stream) {
   UNOK_REQUIRE(n >= 0, UNOK_EINVAL, "bd_compact: negative size");
-  hipLaunchKernelGGL(bd_compact_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, noised, tfull, n, p_mask, count);
+  hipLaunchKernelGGL(bd_compact_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, noised, tfull, pos, n, p_mask,
+                     count);
   return unok::check_launch("bd_compact");
 }

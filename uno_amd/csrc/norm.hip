@@ -274,10 +274,11 @@ __global__ __launch_bounds__(256) void qknorm_rope_fwd_kernel(const TI* __restri
   }
 }
 
-// TI: element type of dq, dk and the qkv input; TO: element type of dqkv and the norm weights.
-template <typename TI, typename TO, int D>
+// TI: element type of dq and dk; TX: of the pre-norm input (the q/k columns of qkv, row stride
+// ld); TO: of dqkv and the norm weights.
+template <typename TI, typename TX, typename TO, int D>
 __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const TI* __restrict__ dq, const TI* __restrict__ dk,
-                                                              const TI* __restrict__ qkv, int64_t ld, const TO* wq,
+                                                              const TX* __restrict__ qkv, int64_t ld, const TO* wq,
                                                               const TO* wk, const int64_t* __restrict__ pos,
                                                               const float* __restrict__ inv_freq,
                                                               const float* __restrict__ rstd, TO* __restrict__ dqkv,
@@ -307,7 +308,8 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const TI* __restri
   // As in the forward: each group's loads (upstream gradient, input row, rstd) go out before its
   // arithmetic.
   for (int hb0 = 0; hb0 < nh; hb0 += HPW * QKR_GROUP) {
-    uint4 rdy[QKR_GROUP], rx[QKR_GROUP];
+    uint4 rdy[QKR_GROUP];
+    float rx[QKR_GROUP][EPL];
     float rs[QKR_GROUP];
 #pragma unroll
     for (int gi = 0; gi < QKR_GROUP; ++gi) {
@@ -317,7 +319,11 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const TI* __restri
       rdy[gi] = valid ? *(const uint4*)(isq ? dq + ((int64_t)row * nq + head) * D + c0
                                             : dk + ((int64_t)row * nk + (head - nq)) * D + c0)
                       : make_uint4(0, 0, 0, 0);
-      rx[gi] = valid && norm ? *(const uint4*)(qkv + (int64_t)row * ld + (int64_t)head * D + c0) : make_uint4(0, 0, 0, 0);
+      if (valid && norm) ld_elems<TX, EPL>(qkv + (int64_t)row * ld + (int64_t)head * D + c0, rx[gi]);
+      else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) rx[gi][e] = 0.f;
+      }
       rs[gi] = valid && norm ? rstd[(int64_t)row * nh + head] : 0.f;
     }
 #pragma unroll
@@ -336,7 +342,8 @@ __global__ __launch_bounds__(256) void qknorm_rope_bwd_kernel(const TI* __restri
       if (norm) {
         const float r = rs[gi];
         float x[EPL];
-        Vec16<TI>::unpack(rx[gi], x);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) x[e] = rx[gi][e];
         float dot = 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
@@ -528,10 +535,10 @@ UNOK_EXPORT int unok_qknorm_rope_fwd(int dtype, int qkv_dtype, int M, int nq, in
   return unok::check_launch("qknorm_rope_fwd");
 }
 
-UNOK_EXPORT int unok_qknorm_rope_bwd(int dtype, int in_dtype, int M, int nq, int nk, int d, const void* dq,
-                                     const void* dk, const void* qkv, int64_t ld, const void* wq, const void* wk,
-                                     const int64_t* pos, const float* inv_freq, const float* rstd, void* dqkv,
-                                     int64_t ldd, void* stream) {
+UNOK_EXPORT int unok_qknorm_rope_bwd(int dtype, int grad_dtype, int x_dtype, int M, int nq, int nk, int d,
+                                     const void* dq, const void* dk, const void* qkv, int64_t ld, const void* wq,
+                                     const void* wk, const int64_t* pos, const float* inv_freq, const float* rstd,
+                                     void* dqkv, int64_t ldd, void* stream) {
   if (M == 0) return 0;
   UNOK_REQUIRE(d == 64 || d == 128, UNOK_EINVAL, "qknorm_rope_bwd: head dim %d not in {64,128}", d);
   UNOK_REQUIRE(ld % 8 == 0 && ldd % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)dqkv & 15) == 0 &&
@@ -539,15 +546,48 @@ UNOK_EXPORT int unok_qknorm_rope_bwd(int dtype, int in_dtype, int M, int nq, int
                UNOK_EALIGN, "qknorm_rope_bwd: rows must be 16-byte aligned");
   const int blocks = (M + 3) / 4;
   hipStream_t st = (hipStream_t)stream;
-  if (d == 128)
-    QKR_DISPATCH(dtype, in_dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<TI, TO, 128>), dim3(blocks), dim3(256), 0,
-                                                     st, (const TI*)dq, (const TI*)dk, (const TI*)qkv, ld, (const TO*)wq,
-                                                     (const TO*)wk, pos, inv_freq, rstd, (TO*)dqkv, ldd, M, nq, nk));
+#define QKR_BWD(TX_T)                                                                                          \
+  do {                                                                                                         \
+    if (d == 128)                                                                                              \
+      hipLaunchKernelGGL((qknorm_rope_bwd_kernel<TI, TX_T, TO, 128>), dim3(blocks), dim3(256), 0, st, (const TI*)dq, \
+                         (const TI*)dk, (const TX_T*)qkv, ld, (const TO*)wq, (const TO*)wk, pos, inv_freq, rstd,  \
+                         (TO*)dqkv, ldd, M, nq, nk);                                                          \
+    else                                                                                                       \
+      hipLaunchKernelGGL((qknorm_rope_bwd_kernel<TI, TX_T, TO, 64>), dim3(blocks), dim3(256), 0, st, (const TI*)dq, \
+                         (const TI*)dk, (const TX_T*)qkv, ld, (const TO*)wq, (const TO*)wk, pos, inv_freq, rstd,  \
+                         (TO*)dqkv, ldd, M, nq, nk);                                                          \
+  } while (0)
+  // the pre-norm input is either of the gradient's type, or bf16 beside fp32 gradients
+  UNOK_REQUIRE(x_dtype == grad_dtype || (x_dtype == UNOK_BF16 && grad_dtype == UNOK_F32 && dtype == UNOK_BF16),
+               UNOK_EINVAL, "qknorm_rope_bwd: input type %d with gradient type %d", x_dtype, grad_dtype);
+  if (x_dtype == grad_dtype)
+    QKR_DISPATCH(dtype, grad_dtype, QKR_BWD(TI));
   else
-    QKR_DISPATCH(dtype, in_dtype, hipLaunchKernelGGL((qknorm_rope_bwd_kernel<TI, TO, 64>), dim3(blocks), dim3(256), 0,
-                                                     st, (const TI*)dq, (const TI*)dk, (const TI*)qkv, ld, (const TO*)wq,
-                                                     (const TO*)wk, pos, inv_freq, rstd, (TO*)dqkv, ldd, M, nq, nk));
+    QKR_DISPATCH(dtype, grad_dtype, QKR_BWD(bf16_t));
+#undef QKR_BWD
   return unok::check_launch("qknorm_rope_bwd");
+}
+
+// cos_tab / sin_tab [P, half]: cos and sin of fl32(p * inv_freq[j]), the angles unok_qknorm_rope_fwd
+// evaluates per row, tabulated for the fused q|k|v projection epilogue.
+__global__ __launch_bounds__(256) void rope_table_kernel(int P, int half, const float* __restrict__ inv_freq,
+                                                         float* __restrict__ cs, float* __restrict__ sn) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)P * half) return;
+  const int p = (int)(i / half), j = (int)(i % half);
+  float sv, cv;
+  sincosf((float)p * inv_freq[j], &sv, &cv);
+  cs[i] = cv;
+  sn[i] = sv;
+}
+
+UNOK_EXPORT int unok_rope_table(int P, int half, const float* inv_freq, float* cos_tab, float* sin_tab, void* stream) {
+  UNOK_REQUIRE(P >= 0 && half > 0, UNOK_EINVAL, "rope_table: P=%d half=%d", P, half);
+  if (P == 0) return 0;
+  const int64_t n = (int64_t)P * half;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, P, half,
+                     inv_freq, cos_tab, sin_tab);
+  return unok::check_launch("rope_table");
 }
 
 UNOK_EXPORT int unok_swiglu_fwd(int dtype, int M, int F, const void* gu, int64_t ld, void* out, void* stream) {

@@ -274,17 +274,82 @@ def qknorm_rope_fwd(qkv, nq, nk, d, wq, wk, pos, inv_freq, eps, *, out_dtype=Non
 
 
 def qknorm_rope_bwd(dq, dk, qkv, nq, nk, d, wq, wk, pos, inv_freq, rstd, dqkv):
-    """Writes the q and k column blocks of ``dqkv`` ([M, (nq+2nk)*d]); dq, dk and qkv share one
-    dtype, dqkv's or fp32."""
+    """Writes the q and k column blocks of ``dqkv`` ([M, (nq+2nk)*d]). dq and dk share a dtype,
+    dqkv's or fp32; ``qkv`` holds the pre-norm q/k columns first (the projection output, or its q/k
+    block alone) in that dtype, or in bf16 beside fp32 gradients."""
     _contig(dq, "dq")
     _contig(dk, "dk")
-    if dq.dtype != qkv.dtype or dk.dtype != qkv.dtype:
-        raise RuntimeError("qknorm_rope_bwd: dq, dk and qkv must share a dtype")
+    if dq.dtype != dk.dtype:
+        raise RuntimeError("qknorm_rope_bwd: dq and dk must share a dtype")
     M = qkv.shape[0]
-    N.call("unok_qknorm_rope_bwd", N.dtype_code(dqkv.dtype), N.dtype_code(qkv.dtype), M, nq, nk, d, N.ptr(dq),
-           N.ptr(dk), N.ptr(qkv), _ld(qkv), N.ptr(wq), N.ptr(wk), N.ptr(pos), N.ptr(inv_freq), N.ptr(rstd),
-           N.ptr(dqkv), _ld(dqkv), N.stream())
+    N.call("unok_qknorm_rope_bwd", N.dtype_code(dqkv.dtype), N.dtype_code(dq.dtype), N.dtype_code(qkv.dtype), M, nq,
+           nk, d, N.ptr(dq), N.ptr(dk), N.ptr(qkv), _ld(qkv), N.ptr(wq), N.ptr(wk), N.ptr(pos), N.ptr(inv_freq),
+           N.ptr(rstd), N.ptr(dqkv), _ld(dqkv), N.stream())
     return dqkv
+
+
+def rope_table(P: int, inv_freq: torch.Tensor):
+    """cos / sin [P, len(inv_freq)] of fl32(p * inv_freq[j]) for positions p < P."""
+    half = inv_freq.numel()
+    cos = torch.empty((P, half), device=inv_freq.device, dtype=torch.float32)
+    sin = torch.empty((P, half), device=inv_freq.device, dtype=torch.float32)
+    N.call("unok_rope_table", P, half, N.ptr(inv_freq), N.ptr(cos), N.ptr(sin), N.stream())
+    return cos, sin
+
+
+def qkv_rope_fused_ok(M: int, K: int, K2: int, nq: int, nk: int, d: int, dtype) -> bool:
+    """Whether gemm_nt_qkv_rope takes this q|k|v projection (the 256 x 256 kernel's shapes)."""
+    return (dtype == torch.bfloat16 and d == 128 and M % 256 == 0 and (128 * (nq + 2 * nk)) % 256 == 0
+            and K % 64 == 0 and K2 % 32 == 0 and M * (nq + 2 * nk) >= 256 * 2)
+
+
+def gemm_nt_qkv_rope(x, w_qkv, nq, nk, wq, wk, pos, cos_tab, sin_tab, eps, *, a2=None, b2=None, segments=None,
+                     want_rstd=True, want_pre=False):
+    """q|k|v projection (+ LoRA extension) with q/k RMSNorm + RoPE in the GEMM epilogue (bf16, head dim
+    128). Returns (q, k, v, rstd or None, pre or None); ``pre`` = the pre-norm q/k columns in bf16."""
+    _rowmajor(x, "x")
+    _rowmajor(w_qkv, "w_qkv")
+    M, Kd = x.shape
+    if w_qkv.shape != (128 * (nq + 2 * nk), Kd):
+        raise RuntimeError("gemm_nt_qkv_rope: w_qkv must be [128 (nq + 2 nk), K]")
+    K2 = 0
+    seg_end, seg_col = [], []
+    if a2 is not None:
+        _rowmajor(a2, "a2")
+        _rowmajor(b2, "b2")
+        K2 = b2.shape[1]
+        segs = list(segments) if segments else [(w_qkv.shape[0], 0)]
+        for _, col in segs:
+            if col + K2 > a2.shape[1]:
+                raise RuntimeError("gemm_nt_qkv_rope: extension segment exceeds a2 columns")
+        seg_end = [s[0] for s in segs]
+        seg_col = [s[1] for s in segs]
+    if not qkv_rope_fused_ok(M, Kd, K2, nq, nk, 128, x.dtype):
+        raise RuntimeError("gemm_nt_qkv_rope: shape outside the fused kernel")
+    if pos.dtype != torch.int64 or pos.numel() != M:
+        raise RuntimeError("gemm_nt_qkv_rope: pos must be int64 [M]")
+    e = dict(device=x.device, dtype=x.dtype)
+    q = torch.empty((M, 128 * nq), **e)
+    k = torch.empty((M, 128 * nk), **e)
+    v = torch.empty((M, 128 * nk), **e)
+    rstd = torch.empty((M, nq + nk), device=x.device, dtype=torch.float32) if want_rstd else None
+    pre = torch.empty((M, 128 * (nq + nk)), **e) if want_pre else None
+    Nn = w_qkv.shape[0]
+    rec = _recorder
+    if rec is not None and rec.predicate(x.dtype, M, Nn, Kd, K2, seg_end or [Nn]):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    else:
+        rec = None
+    N.call("unok_gemm_nt_qkv_rope", M, Kd, nq, nk, N.ptr(x), _ld(x), N.ptr(w_qkv), _ld(w_qkv), N.ptr(a2),
+           _ld(a2) if a2 is not None else 0, N.ptr(b2), _ld(b2) if b2 is not None else 0, K2, len(seg_end),
+           N.int_array(seg_end), N.int_array(seg_col), N.ptr(wq), N.ptr(wk), N.ptr(pos), N.ptr(cos_tab),
+           N.ptr(sin_tab), cos_tab.shape[0], float(eps), N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(rstd), N.ptr(pre),
+           N.stream())
+    if rec is not None:
+        ev1.record()
+        rec.records.append((ev0, ev1, 2.0 * M * Nn * (Kd + K2), (M, Nn, Kd, K2)))
+    return q, k, v, rstd, pre
 
 
 def gemm_nt_swiglu(a: torch.Tensor, b_interleaved: torch.Tensor, *, a2: torch.Tensor | None = None,

@@ -63,13 +63,15 @@ class Geometry:
 
 @dataclass
 class StreamContext:
-    """Per-forward data shared by all layers: positions, interval tables, clean K/V."""
+    """Per-forward data shared by all layers: positions, interval tables, clean K/V, RoPE angles."""
     pos: torch.Tensor            # [M] int64 positions of stream rows
     inv_freq: torch.Tensor       # [d/2] fp32
     iv_noisy: torch.Tensor       # [M, 8] int32
     iv_clean: torch.Tensor       # [M, 8] int32
     clean_k: list                # per layer [M, kv]
     clean_v: list
+    rope_cos: torch.Tensor | None = None   # [P, d/2] fp32 tables for the fused q|k|v epilogue
+    rope_sin: torch.Tensor | None = None
 
 
 def _qkv_dtype(x: torch.Tensor):
@@ -79,8 +81,18 @@ def _qkv_dtype(x: torch.Tensor):
     return torch.float32 if x.dtype == torch.bfloat16 else x.dtype
 
 
-def project_qk_v(x1, lw: LayerWeights, g: Geometry, sc: StreamContext, a2=None, b2=None, segments=None):
-    """q/k/v projection (with its LoRA extension), q/k norm and RoPE: (qkv, q, k, v, rstd)."""
+def project_qk_v(x1, lw: LayerWeights, g: Geometry, sc: StreamContext, a2=None, b2=None, segments=None,
+                 for_backward: bool = False):
+    """q/k/v projection (with its LoRA extension), q/k norm and RoPE: (x_qk, q, k, v, rstd), where x_qk
+    holds the pre-norm q/k columns first (what the q/k norm backward reads): the fp32 projection
+    output, or, when the GEMM applies the norm and RoPE in its epilogue, their bf16 copy (only with
+    ``for_backward``; None otherwise)."""
+    K2 = b2.shape[1] if b2 is not None else 0
+    if sc.rope_cos is not None and K.qkv_rope_fused_ok(x1.shape[0], x1.shape[1], K2, g.nq, g.nk, g.d, x1.dtype):
+        q, k, v, rstd, pre = K.gemm_nt_qkv_rope(x1, lw.w_qkv, g.nq, g.nk, lw.q_norm, lw.k_norm, sc.pos, sc.rope_cos,
+                                                sc.rope_sin, g.eps, a2=a2, b2=b2, segments=segments,
+                                                want_rstd=for_backward, want_pre=for_backward)
+        return pre, q, k, v, rstd
     qkv = K.gemm_nt(x1, lw.w_qkv, a2=a2, b2=b2, segments=segments, out_dtype=_qkv_dtype(x1))
     if qkv.dtype == x1.dtype:
         q, k, rstd = K.qknorm_rope_fwd(qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, g.eps)
@@ -126,7 +138,7 @@ def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: St
     h_qkv = K.gemm_nt(x1, lora.a_c(li, "qkv")) if on("qkv") else None
     qkv, q, k, v, rstd_qk = project_qk_v(
         x1, lw, g, sc, a2=h_qkv, b2=lora.sb_c(li, "qkv") if on("qkv") else None,
-        segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)] if on("qkv") else None)
+        segments=[(q_end, 0), (k_end, r), (k_end + g.kv, 2 * r)] if on("qkv") else None, for_backward=True)
     o, lse = K.attn_fwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, g.nq, g.nk, g.d, k2=k, v2=v)
     h_o = K.gemm_nt(o, lora.a_c(li, "o")) if on("o") else None
     h1 = K.gemm_nt(o, lw.w_o, a2=h_o, b2=lora.sb_c(li, "o") if on("o") else None, residual=h0)
@@ -148,10 +160,15 @@ def noisy_layer_forward(h0, lw: LayerWeights, lora, li: int, g: Geometry, sc: St
     return h2, (h0, x1, rstd1, h_qkv, qkv, q, k, v, rstd_qk, o, lse, h_o, h1, x2, rstd2, h_gu, gu, s, h_d)
 
 
-def saved_bytes_per_row(g: Geometry, rank: int, elem: int) -> int:
-    """Bytes of activations one noisy-stream layer keeps per token row for its backward."""
+def saved_bytes_per_row(g: Geometry, rank: int, elem: int, fused_qkv: bool = True) -> int:
+    """Bytes of activations one noisy-stream layer keeps per token row for its backward
+    (``fused_qkv``: the q|k|v epilogue keeps bf16 pre-norm q/k; otherwise a bf16 step keeps the fp32
+    projection output)."""
     stored = 4 * g.H + g.q + g.kv + g.q + 3 * g.F + 7 * rank
-    qkv = (g.q + 2 * g.kv) * (4 if elem == 2 else elem) + (g.kv * elem if elem == 2 else 0)
+    if elem == 2 and not fused_qkv:
+        qkv = (g.q + 2 * g.kv) * 4 + g.kv * elem
+    else:
+        qkv = (g.q + 2 * g.kv) * elem
     return stored * elem + qkv + 4 * (2 + g.nq + g.nk + g.nq)
 
 
@@ -238,10 +255,11 @@ class NoisyLayer(torch.autograd.Function):
         # ---- attention -----------------------------------------------------------------
         # dq and dk in the q/k/v projection's precision (fp32 for a bf16 step) up to the q/k norm
         # backward, which writes the bf16 q/k gradient blocks of dqkv; dv goes straight into dqkv
+        gdt = _qkv_dtype(dh2)
         dqkv = torch.empty((M, g.q + 2 * g.kv), device=dh2.device, dtype=dh2.dtype)
-        dk = torch.empty((M, g.kv), device=dh2.device, dtype=qkv.dtype)
+        dk = torch.empty((M, g.kv), device=dh2.device, dtype=gdt)
         dq = K.attn_bwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, o, lse, do, g.nq, g.nk, g.d,
-                        k2=k, v2=v, ivk=sc.iv_noisy, dk=dk, dv=dqkv[:, k_end:], grad_dtype=qkv.dtype)
+                        k2=k, v2=v, ivk=sc.iv_noisy, dk=dk, dv=dqkv[:, k_end:], grad_dtype=gdt)
         del do
         K.qknorm_rope_bwd(dq, dk, qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, rstd_qk, dqkv)
         del dq, dk

@@ -182,11 +182,12 @@ def bd_prepare(input_ids, model_position_ids, prompt_mask, *, block_size: int, m
            N.ptr(region), N.ptr(noised), N.ptr(tfull), N.ptr(noisy_src), N.ptr(clean_src), N.ptr(iv_noisy),
            N.ptr(iv_clean), N.ptr(noisy_ids), N.ptr(clean_ids), N.stream())
     p_buf = torch.empty(max(B * L, 1), device=dev, dtype=torch.float32)
-    count = torch.empty(1, **i32)
-    N.call("unok_bd_compact", B * L, N.ptr(noised), N.ptr(tfull), N.ptr(p_buf), N.ptr(count), N.stream())
-    n_noised = int(count.item())
+    count = torch.empty(2, **i32)
+    N.call("unok_bd_compact", B * L, N.ptr(noised), N.ptr(tfull), N.ptr(pos), N.ptr(p_buf), N.ptr(count), N.stream())
+    n_noised, max_pos = (int(v) for v in count.tolist())   # one host synchronisation for both
     mask = BlockDiffusionMask(B, L, int(block_size), intra_block, region, noisy_src, clean_src, iv_noisy, iv_clean,
                               noisy_ids, clean_ids, pos.view(-1))
+    mask.max_pos = max_pos
     return concat_ids, concat_pos, mask, noised, tfull, p_buf[:n_noised]
 
 
@@ -346,6 +347,14 @@ class UnoQwen3Model(nn.Module):
         # output are zeros: for callers whose loss reads no teacher (CE on data targets).
         self.clean_final_needed = True
 
+    def _rope_tables(self, P: int):
+        """cos / sin tables of the positions < P (kept, and reused for smaller P)."""
+        cached = getattr(self, "_rope_cache", None)
+        if cached is None or cached[0] < P:
+            cached = (P, *K.rope_table(P, self.inv_freq))
+            self._rope_cache = cached
+        return cached[1], cached[2]
+
     def recompute_plan(self, rows: int, rank: int, elem: int) -> list[bool]:
         """Which noisy-stream layers keep only their input for the backward (recompute) this step.
         "auto" keeps as many layers' activations as the budget allows and recomputes the rest,
@@ -408,6 +417,7 @@ class UnoQwen3Model(nn.Module):
                                    "of the block-diffusion layout.")
         g = self.geo
         sc = Lyr.StreamContext(mask.pos_stream, self.inv_freq, mask.iv_noisy, mask.iv_clean, [], [])
+        sc.rope_cos, sc.rope_sin = self._rope_tables(max(L, getattr(mask, "max_pos", L - 1) + 1))
         lws = [layer.weights() for layer in self.layers]
         emb = self.embed_tokens.weight
         with torch.no_grad():
