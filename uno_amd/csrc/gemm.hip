@@ -1307,31 +1307,39 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
   }
   if constexpr (EPI == 5) {
     // q|k|v projection: each wave's 128 columns are one head. The quadrant is staged through LDS
-    // in fp32 as for the plain epilogue; each row is then handled by 16 lanes of 8 columns: sum
-    // of squares over the head (lane shuffles), normalisation and weight, rotate_half RoPE (the
-    // partner column +-64 sits 8 lanes away), one rounding, 16-byte stores. Interior tiles only
-    // (the caller requires M and N to be multiples of 256).
-    const int rsub = lane >> 4, c16 = lane & 15;
+    // in fp32 as for the plain epilogue; each row is then handled by 8 lanes, lane l holding
+    // columns [8l, 8l+8) and their RoPE partners [64+8l, 64+8l+8): sum of squares over the head
+    // (three lane shuffles), normalisation and weight, rotate_half RoPE within the lane (one
+    // angle-table read serves both halves), one rounding, 16-byte stores. Interior tiles only (the
+    // caller requires M and N to be multiples of 256).
+    const int rsub = lane >> 3, l8 = lane & 7;
     const int64_t rowb = m0 + wm * 128 + rsub;
     const int head = (n0 + wn * 128) >> 7;
     const int nq = p.qk_nq, nqk = p.qk_nq + p.qk_nk;
     const bool isv = head >= nqk, isq = head < nq;
-    const int c0 = 8 * c16;
+    const int c0 = 8 * l8;                   // first column of the lane's lower half (= angle index)
     bf16_t* dst;
     int64_t ldd;
     if (isq) { dst = (bf16_t*)p.qk_q + (int64_t)head * 128 + c0; ldd = (int64_t)nq * 128; }
     else if (!isv) { dst = (bf16_t*)p.qk_k + (int64_t)(head - nq) * 128 + c0; ldd = (int64_t)p.qk_nk * 128; }
     else { dst = (bf16_t*)p.qk_v + (int64_t)(head - nqk) * 128 + c0; ldd = (int64_t)p.qk_nk * 128; }
+    bf16_t* pre = p.qk_pre && !isv ? (bf16_t*)p.qk_pre + (int64_t)head * 128 + c0 : nullptr;
+    const int64_t ldp = (int64_t)nqk * 128;
     const bool norm = !isv && p.qk_wq != nullptr;
-    float wv[8];
+    float wv[16];
     if (norm) {
-      const uint4 u = *(const uint4*)((const bf16_t*)(isq ? p.qk_wq : p.qk_wk) + c0);
-      const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+      const bf16_t* wsrc = (const bf16_t*)(isq ? p.qk_wq : p.qk_wk) + c0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) { wv[2 * e] = __uint_as_float(w4[e] << 16); wv[2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u); }
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint4 u = *(const uint4*)(wsrc + 64 * hh);
+        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wv[8 * hh + 2 * e] = __uint_as_float(w4[e] << 16);
+          wv[8 * hh + 2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
+        }
+      }
     }
-    const int f0 = c0 & 63;                   // angle index of this lane's first column
-    const float sgn = c0 < 64 ? -1.f : 1.f;   // rotate_half: -x[c+64] in the first half, x[c-64] in the second
     asm volatile("s_barrier" ::: "memory");   // every wave's fragment reads have completed
     float* q = (float*)smem + wid * 64 * 128;
 #pragma unroll
@@ -1349,45 +1357,57 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
       __builtin_amdgcn_s_waitcnt(0xC07F);
       __builtin_amdgcn_wave_barrier();
 #pragma unroll 2
-      for (int it = 0; it < 16; ++it) {
-        const int r = it * 4 + rsub;
-        const f32x4_t v0 = *(const f32x4_t*)&q[r * 128 + (((2 * c16) ^ (r & 15)) << 2)];
-        const f32x4_t v1 = *(const f32x4_t*)&q[r * 128 + (((2 * c16 + 1) ^ (r & 15)) << 2)];
-        const int64_t row = rowb + 64 * h + it * 4;
-        float x[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        float out[8];
+      for (int it = 0; it < 8; ++it) {
+        const int r = it * 8 + rsub;
+        float x[16];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {   // chunks 2 l8, 2 l8 + 1 (lower half) and 16 + 2 l8, 17 + 2 l8
+          const int ch = (c < 2 ? 2 * l8 + c : 16 + 2 * l8 + (c - 2));
+          const f32x4_t v = *(const f32x4_t*)&q[r * 128 + ((ch ^ (r & 15)) << 2)];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[4 * c + e] = v[e];
+        }
+        const int64_t row = rowb + 64 * h + it * 8;
+        float out[16];
         if (isv) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) out[e] = x[e];
+          for (int e = 0; e < 16; ++e) out[e] = x[e];
         } else {
-          if (p.qk_pre)
-            *(uint4*)((bf16_t*)p.qk_pre + row * ((int64_t)nqk * 128) + (int64_t)head * 128 + c0) =
-                make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
+          if (pre) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+              *(uint4*)(pre + row * ldp + 64 * hh) =
+                  make_uint4(pack2_bf16(x[8 * hh], x[8 * hh + 1]), pack2_bf16(x[8 * hh + 2], x[8 * hh + 3]),
+                             pack2_bf16(x[8 * hh + 4], x[8 * hh + 5]), pack2_bf16(x[8 * hh + 6], x[8 * hh + 7]));
+          }
           int64_t pr = p.qk_pos[row];
           pr = pr < 0 ? 0 : (pr >= p.qk_P ? p.qk_P - 1 : pr);
-          const float4 ca = *(const float4*)(p.qk_cos + pr * 64 + f0), cb = *(const float4*)(p.qk_cos + pr * 64 + f0 + 4);
-          const float4 sa = *(const float4*)(p.qk_sin + pr * 64 + f0), sb = *(const float4*)(p.qk_sin + pr * 64 + f0 + 4);
+          const float4 ca = *(const float4*)(p.qk_cos + pr * 64 + c0), cb = *(const float4*)(p.qk_cos + pr * 64 + c0 + 4);
+          const float4 sa = *(const float4*)(p.qk_sin + pr * 64 + c0), sb = *(const float4*)(p.qk_sin + pr * 64 + c0 + 4);
           const float cv[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
           const float sv[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
           if (norm) {
             float ss = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+            for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
 #pragma unroll
-            for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            for (int o = 4; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
             const float rs = rsqrtf(ss / 128.f + p.qk_eps);
-            if (c16 == 0 && p.qk_rstd) p.qk_rstd[row * nqk + head] = rs;
+            if (l8 == 0 && p.qk_rstd) p.qk_rstd[row * nqk + head] = rs;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = x[e] * rs * wv[e];
+            for (int e = 0; e < 16; ++e) x[e] = x[e] * rs * wv[e];
           }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float y = __shfl_xor(x[e], 8, 64);   // partner column +- 64
-            out[e] = x[e] * cv[e] + sgn * y * sv[e];
+          for (int e = 0; e < 8; ++e) {      // rotate_half: (x, x') -> (x c - x' s, x' c + x s)
+            out[e] = x[e] * cv[e] - x[8 + e] * sv[e];
+            out[8 + e] = x[8 + e] * cv[e] + x[e] * sv[e];
           }
         }
-        *(uint4*)(dst + row * ldd) = make_uint4(pack2_bf16(out[0], out[1]), pack2_bf16(out[2], out[3]),
-                                                pack2_bf16(out[4], out[5]), pack2_bf16(out[6], out[7]));
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          *(uint4*)(dst + row * ldd + 64 * hh) =
+              make_uint4(pack2_bf16(out[8 * hh], out[8 * hh + 1]), pack2_bf16(out[8 * hh + 2], out[8 * hh + 3]),
+                         pack2_bf16(out[8 * hh + 4], out[8 * hh + 5]), pack2_bf16(out[8 * hh + 6], out[8 * hh + 7]));
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);     // the half's reads are done before the next overwrites
       __builtin_amdgcn_wave_barrier();
