@@ -190,6 +190,20 @@ int unok_attn_bwd(int dtype, int grad_dtype, int Mq, int Mk2, int Hq, int Hkv, i
                   void* dQ, int64_t lddq, void* dK, int64_t lddk, void* dV, int64_t lddv,
                   float scale, void* stream);
 
+/* The noisy stream's backward with the q/k RMSNorm + RoPE backward (modeling_qwen3.py:140-160,
+ * 237-253) applied to the fp32 dQ / dK accumulators: dqkv [Mq, (Hq + 2 Hkv) D] receives the
+ * gradient before the norm in its q and k column blocks and dV in its v block (bf16; source-2
+ * keys are the query rows, Mk2 = Mq). pre [Mq, (Hq + Hkv) D] = the pre-norm q/k columns (bf16),
+ * rstd [Mq, Hq + Hkv] their 1/rms, cos_tab / sin_tab [P, D/2] the angles (unok_rope_table) at
+ * each row's position; wq / wk null: RoPE only. Dsum [Mq, Hq] fp32 is caller scratch. */
+int unok_attn_bwd_qknorm(int Mq, int Hq, int Hkv, int D, const void* Q, int64_t ldq, const void* K1,
+                         int64_t ldk1, const void* V1, int64_t ldv1, const void* K2, int64_t ldk2,
+                         const void* V2, int64_t ldv2, const int32_t* iv, const void* O, int64_t ldo,
+                         const float* LSE, const void* dO, int64_t lddo, float* Dsum, const void* pre,
+                         int64_t ldpre, const float* rstd, const void* wq, const void* wk,
+                         const int64_t* pos, const float* cos_tab, const float* sin_tab, int P,
+                         void* dqkv, int64_t lddqkv, float scale, void* stream);
+
 /* ---- Draft-block attention over the KV cache -------------------------------------------------- */
 
 /* q/k RMSNorm + RoPE of a draft block's fused qkv rows [B*L, (nq + 2 nk) * D] (the arithmetic of

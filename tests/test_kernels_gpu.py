@@ -363,6 +363,48 @@ def test_block_diffusion_attention(dev, dtype, D, L, bs, packed, intra):
         assert torch.equal(dq32.bfloat16(), dq) and torch.equal(dk32.bfloat16(), dk) and torch.equal(dv2, dv)
 
 
+@pytest.mark.parametrize("D,Hq,Hkv,norm", [(128, 8, 2, True), (128, 4, 4, False), (64, 4, 2, True)])
+def test_attention_backward_with_qknorm_epilogue(dev, D, Hq, Hkv, norm):
+    """The noisy stream's backward with the q/k-norm + RoPE backward in the dQ and dK/dV epilogues
+    against the two-kernel path (fp32 dQ / dK, then the stand-alone q/k-norm backward from the same
+    bf16 pre-norm columns): dV bit-identical, the q and k gradient blocks within a bf16 step."""
+    torch.manual_seed(13)
+    B, L, bs = 2, 320, 16
+    ids, labels, pos = _batch(B, L, 512, 8, seed=7, packed=True)
+    _, _, mask, _, _, _ = bd_prepare(ids.to(dev), pos.to(dev), (labels == -100).to(dev), block_size=bs,
+                                     mask_token_id=511)
+    M = B * L
+    bf = torch.bfloat16
+    qn = torch.randn(M, Hq * D, device=dev).to(bf)
+    kc, vc, kn, vn = (torch.randn(M, Hkv * D, device=dev).to(bf) for _ in range(4))
+    on, ln = K.attn_fwd(qn, kc, vc, mask.iv_noisy, Hq, Hkv, D, k2=kn, v2=vn)
+    do = torch.randn(M, Hq * D, device=dev).to(bf)
+    pre = torch.randn(M, (Hq + Hkv) * D, device=dev).to(bf)
+    wq = (1 + 0.1 * torch.randn(D, device=dev)).to(bf) if norm else None
+    wk = (1 + 0.1 * torch.randn(D, device=dev)).to(bf) if norm else None
+    rstd = torch.rsqrt(pre.float().view(M, Hq + Hkv, D).pow(2).mean(-1) + 1e-6).contiguous()
+    inv = (1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.int64).float() / D))).to(dev)
+    pos_s = mask.pos_stream
+    cos, sin = K.rope_table(int(pos_s.max()) + 1, inv)
+    n_all = (Hq + 2 * Hkv) * D
+    fused = torch.zeros(M, n_all, device=dev, dtype=bf)
+    K.attn_bwd_qknorm(qn, kc, vc, mask.iv_noisy, on, ln, do, Hq, Hkv, D, kn, vn, pre, rstd, wq, wk, pos_s, cos, sin,
+                      fused)
+    ref = torch.zeros_like(fused)
+    dk = torch.empty(M, Hkv * D, device=dev, dtype=torch.float32)
+    dq = K.attn_bwd(qn, kc, vc, mask.iv_noisy, on, ln, do, Hq, Hkv, D, k2=kn, v2=vn, ivk=mask.iv_noisy, dk=dk,
+                    dv=ref[:, (Hq + Hkv) * D:], grad_dtype=torch.float32)
+    K.qknorm_rope_bwd(dq, dk, pre, Hq, Hkv, D, wq, wk, pos_s, inv, rstd, ref)
+    e = (Hq + Hkv) * D
+    assert torch.equal(fused[:, e:], ref[:, e:])
+    diff = (fused[:, :e].float() - ref[:, :e].float()).abs()
+    mag = ref[:, :e].float().abs()
+    step = mag.clamp_min(mag.max() * 2 ** -8) * 2 ** -7
+    print(f"[attn bwd + qk-norm] rel L2 {rel(fused[:, :e], ref[:, :e]):.2e}; beyond one bf16 step: "
+          f"{int((diff > step).sum())} of {diff.numel()}", flush=True)
+    assert rel(fused[:, :e], ref[:, :e]) < 2e-3 and bool((diff <= step).all())
+
+
 # ------------------------------------------------------------------------------------------
 # Objectives
 # ------------------------------------------------------------------------------------------

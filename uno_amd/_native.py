@@ -53,6 +53,8 @@ SIGNATURES: dict[str, tuple] = {
     "unok_decode_prep": (_i, [_i, _i, _i, _i, _i, _p, _i64, _p, _p, _p, _p, _f, _p, _p, _i, _p, _p]),
     "unok_attn_bwd": (_i, [_i, _i, _i, _i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
                            _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _f, _p]),
+    "unok_attn_bwd_qknorm": (_i, [_i, _i, _i, _i, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64,
+                                  _p, _p, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i, _p, _i64, _f, _p]),
     "unok_bd_prepare": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _u64, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                              _p, _p, _p]),
     "unok_bd_region": (_i, [_i, _i, _p, _p, _p]),

@@ -40,11 +40,107 @@ struct AttnArgs {
   int Mq, Mk2, Hq, Hkv;
   int q_mod;                           // > 0: query row i reads Q row i % q_mod (split-key decode)
   int grad_f32;                        // bf16 kernels: dQ and dK stored as fp32 (dV keeps bf16)
+  // bf16 kernels with qkn_out set: instead of dQ / dK, the gradient of the q/k projection before
+  // the q/k RMSNorm and RoPE (their backward applied to the fp32 dQ / dK accumulators), written into
+  // the q / k column blocks of qkn_out [Mq, (Hq + 2 Hkv) D]; the q/k head columns of qkn_pre
+  // [Mq, (Hq + Hkv) D] are the pre-norm values (bf16), qkn_rstd [Mq, Hq + Hkv] their 1/rms, and
+  // qkn_cos / qkn_sin [qkn_P, D/2] the angles at each row's position qkn_pos. No norm when qkn_wq is
+  // null (RoPE only).
+  bf16_t* qkn_out; int64_t ld_qkn_out;
+  const bf16_t* qkn_pre; int64_t ld_qkn_pre;
+  const float* qkn_rstd;
+  const bf16_t* qkn_wq; const bf16_t* qkn_wk;
+  const int64_t* qkn_pos;
+  const float* qkn_cos; const float* qkn_sin;
+  int qkn_P;
   float scale;                         // d^-0.5
   float scale_log2;                    // d^-0.5 * log2(e)
 };
 
 __device__ __forceinline__ bf16x8_t ld_bf16x8(const bf16_t* p) { return *(const bf16x8_t*)p; }
+
+// Backward of y = RoPE(w * x * rstd) (q/k RMSNorm then rotate_half RoPE, modeling_qwen3.py:140-160,
+// 237-253) for one row and head, on the fp32 gradient dy held as the MFMA accumulators of the
+// dQ / dK kernels: lane (g, row) holds dims c = 32 t + 8 j4 + 4 g + e of acc[t][4 j4 + e] (times
+// scale), so a dim's RoPE partner c +- D/2 is block t ^ (NDT/2) of the same lane and the other half
+// of the row sits in lane ^ 32. Writes r (g - xhat mean(g xhat)) with g = w * RoPE^-1(dy) (or
+// RoPE^-1(dy) without the norm) as bf16 at dst[c]; pre / rs: the row's pre-norm head and 1/rms;
+// cs / sn: the row's angle-table rows. Lanes with valid false take part in the shuffle only.
+template <int D>
+__device__ __forceinline__ void qknorm_rope_bwd_acc(const f32x16_t (&acc)[D / 32], float scale, int g, bool valid,
+                                                    const bf16_t* pre, float rs, const bf16_t* wn, const float* cs,
+                                                    const float* sn, bf16_t* dst) {
+  constexpr int NDT = D / 32, HT = NDT / 2;
+  // every input load first (independent of each other), then the arithmetic
+  float4 cv[HT][4], sv[HT][4];
+  uint2 xw[NDT][4], ww[NDT][4];
+#pragma unroll
+  for (int t = 0; t < HT; ++t)
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4) {
+      const int f = 32 * t + 8 * j4 + 4 * g;                 // angle index of the lower dim (= c mod D/2)
+      cv[t][j4] = valid ? *(const float4*)(cs + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+      sv[t][j4] = valid ? *(const float4*)(sn + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  if (wn != nullptr) {
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const int c = 32 * t + 8 * j4 + 4 * g;
+        xw[t][j4] = valid ? *(const uint2*)(pre + c) : make_uint2(0, 0);
+        ww[t][j4] = valid ? *(const uint2*)(wn + c) : make_uint2(0, 0);
+      }
+  }
+  float gv[NDT][16];
+#pragma unroll
+  for (int t = 0; t < HT; ++t)
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4) {
+      const float c4[4] = {cv[t][j4].x, cv[t][j4].y, cv[t][j4].z, cv[t][j4].w};
+      const float s4[4] = {sv[t][j4].x, sv[t][j4].y, sv[t][j4].z, sv[t][j4].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = acc[t][4 * j4 + e] * scale, hi = acc[t + HT][4 * j4 + e] * scale;
+        // inverse rotation: dn_c = dy_c cos + dy_{c+h} sin (lower), dy_c cos - dy_{c-h} sin (upper)
+        gv[t][4 * j4 + e] = lo * c4[e] + hi * s4[e];
+        gv[t + HT][4 * j4 + e] = hi * c4[e] - lo * s4[e];
+      }
+    }
+  if (wn != nullptr) {
+    float xh[NDT][16];
+    float dot = 0.f;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const uint2 xv = xw[t][j4], wv = ww[t][j4];
+        const float x4[4] = {__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
+                             __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u)};
+        const float w4[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
+                             __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xh[t][4 * j4 + e] = x4[e] * rs;
+          gv[t][4 * j4 + e] *= w4[e];
+          dot += gv[t][4 * j4 + e] * xh[t][4 * j4 + e];
+        }
+      }
+    dot += __shfl_xor(dot, 32, 64);
+    dot /= (float)D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) gv[t][r] = rs * (gv[t][r] - xh[t][r] * dot);
+  }
+  if (!valid) return;
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4)
+      *(uint2*)(dst + 32 * t + 8 * j4 + 4 * g) =
+          make_uint2(pack2_bf16(gv[t][4 * j4], gv[t][4 * j4 + 1]), pack2_bf16(gv[t][4 * j4 + 2], gv[t][4 * j4 + 3]));
+}
 
 __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
   uint4 u = make_uint4(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]), pack2_bf16(v[4], v[5]), pack2_bf16(v[6], v[7]));
@@ -428,6 +524,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
     ivq = *(const int4*)(p.iv + (int64_t)qrow * 8);
     lse = p.LSE[(int64_t)qrow * p.Hq + h];
   }
+  // the q-norm backward's per-row scalars, read ahead of the tile walk
+  int64_t qkn_ar = 0;
+  float qkn_rs = 1.f;
+  if (p.qkn_out != nullptr && qvalid) {
+    const int64_t pr = p.qkn_pos[qrow];
+    qkn_ar = (pr < 0 ? 0 : (pr >= p.qkn_P ? p.qkn_P - 1 : pr)) * (D / 2);
+    if (p.qkn_wq) qkn_rs = p.qkn_rstd[(int64_t)qrow * (p.Hq + p.Hkv) + h];
+  }
   const bf16_t* Q = (const bf16_t*)p.Q;
   const bf16_t* dO = (const bf16_t*)p.dO;
   const bf16_t* Ob = (const bf16_t*)p.O;
@@ -587,7 +691,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_bf16_kernel(const Att
     tile(t, S0{});
     if (t + 1 < nt) tile(t + 1, S1{});
   }
-  if (qvalid && p.grad_f32) {
+  if (p.qkn_out != nullptr) {       // wave-uniform: the q/k-norm + RoPE backward on the accumulators
+    const int row = qvalid ? qrow : 0;
+    qknorm_rope_bwd_acc<D>(dq, p.scale, g, qvalid, p.qkn_pre + (int64_t)row * p.ld_qkn_pre + h * D, qkn_rs, p.qkn_wq,
+                           p.qkn_cos + qkn_ar, p.qkn_sin + qkn_ar, p.qkn_out + (int64_t)row * p.ld_qkn_out + h * D);
+  } else if (qvalid && p.grad_f32) {
     float* out = (float*)p.dQ + (int64_t)qrow * p.lddq + h * D;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
@@ -665,6 +773,14 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_bf16_kernel(const AttnArgs p)
   }
   // query q sees this key  <=>  (unsigned)(q - qlo) < span  (span = 0: no query, or no key)
   const uint32_t span = (uint32_t)max(qhi - qlo, 0);
+  // the k-norm backward's per-row scalars, read ahead of the walk
+  int64_t qkn_ar = 0;
+  float qkn_rs = 1.f;
+  if (p.qkn_out != nullptr && kvalid) {
+    const int64_t pr = p.qkn_pos[krow];
+    qkn_ar = (pr < 0 ? 0 : (pr >= p.qkn_P ? p.qkn_P - 1 : pr)) * (D / 2);
+    if (p.qkn_wk) qkn_rs = p.qkn_rstd[(int64_t)krow * (p.Hq + p.Hkv) + p.Hq + kvh];
+  }
   const bf16_t* K = (const bf16_t*)p.K2;
   const bf16_t* V = (const bf16_t*)p.V2;
   bf16x8_t kreg[NKS], vreg[NKS];
@@ -761,6 +877,11 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_bf16_kernel(const AttnArgs p)
       }
     }
   }
+  if (p.qkn_out != nullptr) {       // wave-uniform: the k-norm + RoPE backward on the dK accumulators
+    const int row = kvalid ? krow : 0, col = (p.Hq + kvh) * D;
+    qknorm_rope_bwd_acc<D>(dk, p.scale, g, kvalid, p.qkn_pre + (int64_t)row * p.ld_qkn_pre + col, qkn_rs, p.qkn_wk,
+                           p.qkn_cos + qkn_ar, p.qkn_sin + qkn_ar, p.qkn_out + (int64_t)row * p.ld_qkn_out + col);
+  }
   if (kvalid) {
     bf16_t* ov = (bf16_t*)p.dV + (int64_t)krow * p.lddv + kvh * D;
 #pragma unroll
@@ -773,7 +894,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkv_bf16_kernel(const AttnArgs p)
 #pragma unroll
         for (int e = 0; e < 4; ++e) hv[e] = f32_to_bf16(dv[t][j4 * 4 + e]);
         *(uint2*)(ov + c) = uv;
-        if (p.grad_f32) {
+        if (p.qkn_out != nullptr) {
+          // dK went through the k-norm backward above
+        } else if (p.grad_f32) {
           float* ok = (float*)p.dK + (int64_t)krow * p.lddk + kvh * D;
           *(float4*)(ok + c) = make_float4(dk[t][j4 * 4] * p.scale, dk[t][j4 * 4 + 1] * p.scale,
                                            dk[t][j4 * 4 + 2] * p.scale, dk[t][j4 * 4 + 3] * p.scale);
@@ -1039,6 +1162,49 @@ UNOK_EXPORT int unok_attn_bwd(int dtype, int grad_dtype, int Mq, int Mk2, int Hq
   rc = unok::check_launch("attn_dq_bf16");
   if (rc || !want_kv) return rc;
   const unsigned kblocks = (unsigned)(((Mk2 + 127) / 128) * Hkv);
+  if (D == 128) launch_dkv<128>(kblocks, st, a);
+  else launch_dkv<64>(kblocks, st, a);
+  return unok::check_launch("attn_dkv_bf16");
+}
+
+// Backward of the noisy stream with the q/k RMSNorm + RoPE backward in the dQ and dK/dV kernels'
+// epilogues (bf16): instead of dQ and dK, the gradient before the norm is written into the q and k
+// column blocks of dqkv [Mq, (Hq + 2 Hkv) D] (row stride lddqkv), dV into its v block. Source-2
+// keys are the query rows themselves (Mk2 = Mq). pre [Mq, (Hq + Hkv) D] holds the pre-norm q/k
+// columns (bf16, row stride ldpre), rstd [Mq, Hq + Hkv] their 1/rms (read only with wq / wk),
+// cos_tab / sin_tab [P, D/2] the angles at each row's position pos.
+UNOK_EXPORT int unok_attn_bwd_qknorm(int Mq, int Hq, int Hkv, int D, const void* Q, int64_t ldq, const void* K1,
+                                     int64_t ldk1, const void* V1, int64_t ldv1, const void* K2, int64_t ldk2,
+                                     const void* V2, int64_t ldv2, const int32_t* iv, const void* O, int64_t ldo,
+                                     const float* LSE, const void* dO, int64_t lddo, float* Dsum, const void* pre,
+                                     int64_t ldpre, const float* rstd, const void* wq, const void* wk,
+                                     const int64_t* pos, const float* cos_tab, const float* sin_tab, int P,
+                                     void* dqkv, int64_t lddqkv, float scale, void* stream) {
+  if (Mq == 0) return 0;
+  int rc = check_geom(UNOK_BF16, D, Hq, Hkv);
+  if (rc) return rc;
+  UNOK_REQUIRE(K2 != nullptr && V2 != nullptr && P > 0 && (wq == nullptr) == (wk == nullptr), UNOK_EINVAL,
+               "attn_bwd_qknorm: noisy keys, a non-empty angle table and both or neither norm weight required");
+  UNOK_REQUIRE(al16(dO) && al16(O) && al16(pre) && al16(dqkv) && al16(cos_tab) && al16(sin_tab) && lddo % 8 == 0 &&
+                   ldo % 8 == 0 && ldpre % 8 == 0 && lddqkv % 8 == 0 && (D / 2) % 4 == 0,
+               UNOK_EALIGN, "attn_bwd_qknorm: strides must be multiples of 8 and rows 16-byte aligned");
+  AttnArgs a{};
+  a.O = const_cast<void*>(O); a.ldo = ldo;
+  a.Q = Q; a.ldq = ldq; a.K1 = K1; a.ldk1 = ldk1; a.V1 = V1; a.ldv1 = ldv1;
+  a.K2 = K2; a.ldk2 = ldk2; a.V2 = V2; a.ldv2 = ldv2; a.iv = iv; a.ivk = iv; a.LSE = (float*)LSE;
+  a.dO = dO; a.lddo = lddo; a.Dsum = Dsum;
+  a.dV = (bf16_t*)dqkv + (int64_t)(Hq + Hkv) * D; a.lddv = lddqkv;
+  a.Mq = Mq; a.Mk2 = Mq; a.Hq = Hq; a.Hkv = Hkv; a.scale = scale; a.scale_log2 = scale * 1.4426950408889634f;
+  a.qkn_out = (bf16_t*)dqkv; a.ld_qkn_out = lddqkv;
+  a.qkn_pre = (const bf16_t*)pre; a.ld_qkn_pre = ldpre; a.qkn_rstd = rstd;
+  a.qkn_wq = (const bf16_t*)wq; a.qkn_wk = (const bf16_t*)wk; a.qkn_pos = pos;
+  a.qkn_cos = cos_tab; a.qkn_sin = sin_tab; a.qkn_P = P;
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 128) launch_dq<128>(Mq, Hq, st, a);
+  else launch_dq<64>(Mq, Hq, st, a);
+  rc = unok::check_launch("attn_dq_bf16");
+  if (rc) return rc;
+  const unsigned kblocks = (unsigned)(((Mq + 127) / 128) * Hkv);
   if (D == 128) launch_dkv<128>(kblocks, st, a);
   else launch_dkv<64>(kblocks, st, a);
   return unok::check_launch("attn_dkv_bf16");

@@ -538,6 +538,29 @@ def decode_prep(qkv, wq, wk, lengths, inv_freq, eps: float, kc, vc, qd, B: int, 
     return qd
 
 
+def attn_bwd_qknorm(q, k1, v1, iv, o, lse, do, Hq, Hkv, D, k2, v2, pre, rstd, wq, wk, pos, cos_tab, sin_tab, dqkv,
+                    scale=None):
+    """Noisy-stream backward with the q/k RMSNorm + RoPE backward in the dQ / dK epilogues (bf16): writes
+    the gradient before the norm into the q and k column blocks of ``dqkv`` and dV into its v block."""
+    Mq = q.shape[0]
+    scale = D ** -0.5 if scale is None else scale
+    _contig(do, "do")
+    _rowmajor(pre, "pre")
+    _rowmajor(dqkv, "dqkv")
+    if q.dtype != torch.bfloat16 or pre.dtype != torch.bfloat16 or dqkv.dtype != torch.bfloat16:
+        raise RuntimeError("attn_bwd_qknorm: bf16 only")
+    if pre.shape != (Mq, (Hq + Hkv) * D) or dqkv.shape != (Mq, (Hq + 2 * Hkv) * D) or k2.shape[0] != Mq:
+        raise RuntimeError("attn_bwd_qknorm: pre [Mq, (Hq+Hkv) D], dqkv [Mq, (Hq+2Hkv) D] and Mq keys required")
+    if pos.dtype != torch.int64 or pos.numel() != Mq:
+        raise RuntimeError("attn_bwd_qknorm: pos must be int64 [Mq]")
+    dsum = torch.empty((Mq, Hq), device=q.device, dtype=torch.float32)
+    N.call("unok_attn_bwd_qknorm", Mq, Hq, Hkv, D, N.ptr(q), _ld(q), N.ptr(k1), _ld(k1), N.ptr(v1), _ld(v1),
+           N.ptr(k2), _ld(k2), N.ptr(v2), _ld(v2), N.ptr(iv), N.ptr(o), _ld(o), N.ptr(lse), N.ptr(do), _ld(do),
+           N.ptr(dsum), N.ptr(pre), _ld(pre), N.ptr(rstd), N.ptr(wq), N.ptr(wk), N.ptr(pos), N.ptr(cos_tab),
+           N.ptr(sin_tab), cos_tab.shape[0], N.ptr(dqkv), _ld(dqkv), float(scale), N.stream())
+    return dqkv
+
+
 def attn_bwd(q, k1, v1, iv, o, lse, do, Hq, Hkv, D, *, k2=None, v2=None, ivk=None, dk=None, dv=None,
              scale=None, grad_dtype=None):
     """Returns dQ; writes dK/dV of source-2 keys into ``dk``/``dv`` when given. ``grad_dtype`` (default

@@ -255,14 +255,21 @@ class NoisyLayer(torch.autograd.Function):
         # ---- attention -----------------------------------------------------------------
         # dq and dk in the q/k/v projection's precision (fp32 for a bf16 step) up to the q/k norm
         # backward, which writes the bf16 q/k gradient blocks of dqkv; dv goes straight into dqkv
-        gdt = _qkv_dtype(dh2)
         dqkv = torch.empty((M, g.q + 2 * g.kv), device=dh2.device, dtype=dh2.dtype)
-        dk = torch.empty((M, g.kv), device=dh2.device, dtype=gdt)
-        dq = K.attn_bwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, o, lse, do, g.nq, g.nk, g.d,
-                        k2=k, v2=v, ivk=sc.iv_noisy, dk=dk, dv=dqkv[:, k_end:], grad_dtype=gdt)
-        del do
-        K.qknorm_rope_bwd(dq, dk, qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, rstd_qk, dqkv)
-        del dq, dk
+        if qkv.dtype == torch.bfloat16 and qkv.shape[1] == k_end and sc.rope_cos is not None:
+            # the fused forward kept the bf16 pre-norm q/k: the attention backward applies the q/k
+            # norm + RoPE backward to its fp32 dQ / dK accumulators and writes dqkv directly
+            K.attn_bwd_qknorm(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, o, lse, do, g.nq, g.nk, g.d, k, v,
+                              qkv, rstd_qk, lw.q_norm, lw.k_norm, sc.pos, sc.rope_cos, sc.rope_sin, dqkv)
+            del do
+        else:
+            gdt = _qkv_dtype(dh2)
+            dk = torch.empty((M, g.kv), device=dh2.device, dtype=gdt)
+            dq = K.attn_bwd(q, sc.clean_k[li], sc.clean_v[li], sc.iv_noisy, o, lse, do, g.nq, g.nk, g.d,
+                            k2=k, v2=v, ivk=sc.iv_noisy, dk=dk, dv=dqkv[:, k_end:], grad_dtype=gdt)
+            del do
+            K.qknorm_rope_bwd(dq, dk, qkv, g.nq, g.nk, g.d, lw.q_norm, lw.k_norm, sc.pos, sc.inv_freq, rstd_qk, dqkv)
+            del dq, dk
         # ---- q | k | v -----------------------------------------------------------------
         g_qkv = _lora_inner_grads(lora, li, "qkv", dqkv, h_qkv, ((0, q_end), (q_end, k_end), (k_end, k_end + g.kv)),
                                   sc_l)
