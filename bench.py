@@ -41,6 +41,8 @@ WORKLOAD = dict(batch=4, seq_len=4096, prompt=512, block_size=16, lora_rank=64, 
 #                4 x 4096 tokens, rank 64 / alpha 1024, curriculum block 4 -> 8 -> 16 -> 32 across the timed steps
 #   packed_16k   Qwen3-8B shape, one row of 16384 tokens packed from log-normal segment lengths
 #                (median 3000, sigma 0.6, clipped to [512, 16384]; 10% prompt per segment), block 32
+#   qwen3_8b_r128  the released recipe's adapter and micro-batch on the Qwen3-8B shape: rank 128 /
+#                alpha 2048 (alpha = 16 r), 8 x 4096 tokens, block 16 (run with --objective tv)
 WORKLOADS = {
     "qwen3_8b": (QWEN3_8B, WORKLOAD),
     "dense_1b": (dict(vocab_size=151936, hidden_size=2048, intermediate_size=5632, num_hidden_layers=16,
@@ -51,6 +53,8 @@ WORKLOADS = {
                dict(batch=4, seq_len=4096, prompt=512, block_size=4, block_sweep=[4, 8, 16, 32], lora_rank=64,
                     lora_alpha=1024)),
     "packed_16k": (QWEN3_8B, dict(batch=1, seq_len=16384, packed=True, block_size=32, lora_rank=64, lora_alpha=128)),
+    "qwen3_8b_r128": (QWEN3_8B, dict(batch=8, seq_len=4096, prompt=512, block_size=16, lora_rank=128,
+                                     lora_alpha=2048)),
 }
 
 
@@ -78,6 +82,8 @@ WORKLOAD_NAMES = {
     "dense_1b": "1B-class (16 layers, hidden 2048, 16q/8kv) cond-LoRA step, rank 32",
     "mha_7b": "7B MHA (no q/k-norm, vocab 32000) cond-LoRA step, block curriculum 4/8/16/32",
     "packed_16k": "Qwen3-8B-shape step on one 16384-token row of packed segments, block 32",
+    "qwen3_8b_r128": "Qwen3-8B-shape cond-LoRA step at the released recipe's rank 128 / alpha 2048, 8 x 4096 tokens, "
+                     "block 16",
     "draft_8b": "Qwen3-8B-shape draft forward of two-pass block decoding: 8 sequences x 16-row blocks "
                 "over 4096-token KV caches, gated rank-64 LoRA, one HIP graph per block",
 }
