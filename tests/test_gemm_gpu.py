@@ -68,7 +68,7 @@ def test_gemm_nt_lora_segments_gate_residual(dev, dtype):
     assert _rel(out, ref) < (1e-6 if dtype == torch.float32 else 8e-3)
 
 
-@pytest.mark.parametrize("M,N,Kd", [(8192, 8192, 512), (8200, 8448, 576), (16384, 4096, 320)])
+@pytest.mark.parametrize("M,N,Kd", [(8192, 8192, 512), (8200, 8448, 576), (16384, 4096, 320), (32768, 384, 4096)])
 def test_gemm_nt_direct_to_lds_path(dev, M, N, Kd):
     """Shapes large enough (>= 512 tiles of 256x256, K a multiple of 64) for the direct-to-LDS
     kernel, including ragged M/N edges, with fp32 output."""
@@ -138,10 +138,13 @@ def test_gemm_tn(dev, Mr, P, Q, dtype):
 @pytest.mark.parametrize("Mr,P,Q", [(1000, 192, 4096), (16384, 4096, 64), (777, 1000, 96), (4100, 64, 12288),
                                      (300, 1032, 256), (16384, 128, 4096), (2000, 64, 1000), (2000, 1000, 64),
                                      (2000, 1000, 128), (16384, 192, 4096), (3000, 4104, 192),
-                                     (4096, 32, 2048), (3000, 5640, 32)])
+                                     (4096, 32, 2048), (3000, 5640, 32),
+                                     (4100, 384, 4096), (3000, 4104, 384), (2000, 256, 1000), (16384, 4096, 256),
+                                     (777, 384, 12288), (32768, 384, 4096)])
 def test_gemm_tn_skinny_bf16(dev, Mr, P, Q):
-    """LoRA weight-gradient shapes (rank side <= 256 columns): dA = g^T x and dB = dY^T h, with
-    ragged row counts and wide sides that are not a multiple of the 128- or 256-column strips."""
+    """LoRA weight-gradient shapes (rank side <= 256 columns, or 384 = 3r at rank 128): dA = g^T x
+    and dB = dY^T h, with ragged row counts and wide sides that are not a multiple of the 128- or
+    256-column strips."""
     torch.manual_seed(Mr + Q)
     a = torch.randn(Mr, P, device=dev).bfloat16()
     b = torch.randn(Mr, Q, device=dev).bfloat16()

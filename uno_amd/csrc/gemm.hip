@@ -1742,6 +1742,8 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
   const long long big_tiles = (long long)((M + 255) / 256) * ((N + 255) / 256);
   if (N <= 192 && !p.A2 && K % 64 == 0 && M >= 4096) {
     // Skinny products (LoRA x·Aᵀ and dY·B, N = r .. 3r): every activation row is read from HBM once.
+    // (N = 256 and 384 run faster on the 128x128 and 256x256 kernels: 116 / 105 us against 135 /
+    // 208 us for a 64 x N tile at 32768 x 4096.)
     const int bn = (N + 63) / 64 * 64;
     if (bn == 64) launch_nt_skinny_t<64, 4>(p, out_dtype, st);
     else if (bn == 128) launch_nt_skinny_t<128, 4>(p, out_dtype, st);
@@ -1904,13 +1906,147 @@ static void launch_tn_tr_t(const GemmTNSkinny& p, int nz, bool tout, hipStream_t
     hipLaunchKernelGGL((gemm_tn_tr_kernel<NS, false>), dim3(nstrip * nz), dim3(256), lds, st, p);
 }
 
-// Row splits of the transpose-load TN kernel: about one round of workgroups (3 per CU for NS = 64,
-// 2 for NS = 128 on 256 CUs), at most 16 splits for wide sides (2048 columns and more, where the
-// partials and their reduction would grow faster than the parallelism helps) and 64 otherwise,
-// at least 256 rows per split.
+// Wide rank side (NS = 256 or 384: the 2r / 3r LoRA groups at rank 128): the tiles, row splits and
+// partial layout of gemm_tn_tr_kernel, with the waves split over S instead of X. Wave w owns the
+// S columns [NS/4 w, NS/4 (w + 1)) (NS/128 blocks of 32) against all 128 X columns of the strip,
+// so a 16-row step reads 4 + NS/128 transpose-loaded fragments for 4 NS/128 MFMAs (the X-split
+// layout would read 1 + NS/32 for NS/32 and run into the LDS read bandwidth). The S tile is kept
+// as NS/128 swizzled [64 x 128] tiles; two stages take 96 KB (NS = 256) or 128 KB (NS = 384) of
+// LDS, one workgroup per CU.
+template <int NS, bool TOUT>
+__global__ __launch_bounds__(256, 1) void gemm_tn_trw_kernel(const GemmTNSkinny p) {
+  constexpr int BK = 64, XB = 128, NT = NS / 128, TSW = NS / 128;
+  static_assert(NS == 256 || NS == 384, "wide skinny side of 256 or 384 columns");
+  extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
+  bf16_t* Xs = smem;                   // [2][BK * XB]
+  bf16_t* Ss = smem + 2 * BK * XB;     // [2][NT][BK * 128]
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, lq = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(w);
+  const int nstrip = (p.NX + XB - 1) / XB;
+  const int lin = xcd_remap(blockIdx.x, gridDim.x);
+  const int x0 = (lin % nstrip) * XB, z = lin / nstrip;
+  const int mbeg = z * p.rows_per_split;
+  const int mend = min(p.Mrows, mbeg + p.rows_per_split);
+  const int nt = mend > mbeg ? (mend - mbeg + BK - 1) / BK : 0;
+  const uint32_t xo = dma_lane_off<XB>(p.ldx, x0, wid, lane);
+  uint32_t so[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) so[j] = dma_lane_off<128>(p.lds, 128 * j, wid, lane);
+  auto fetch = [&](int t) {
+    const int m0 = mbeg + t * BK;
+    dma_tile<XB>(p.X, p.ldx, xo, m0, mend, Xs + (t & 1) * BK * XB, wid);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) dma_tile<128>(p.S, p.lds, so[j], m0, mend, Ss + ((t & 1) * NT + j) * BK * 128, wid);
+  };
+  int2 xoff[4], soff[TSW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xoff[i] = tr_frag_off<XB>(i, lane);
+#pragma unroll
+  for (int j = 0; j < TSW; ++j) {
+    const int sb = TSW * wid + j;              // this wave's S block j: tile sb / 4, block sb % 4 within it
+    const int2 o = tr_frag_off<128>(sb & 3, lane);
+    soff[j] = make_int2(o.x + (sb >> 2) * BK * 128, o.y + (sb >> 2) * BK * 128);
+  }
+  f32x16_t acc[4][TSW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < TSW; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  if (nt > 0) fetch(0);
+#pragma unroll 1
+  for (int t = 0; t < nt; ++t) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();                       // tile t in LDS; every wave is done with tile t-1
+    if (t + 1 < nt) fetch(t + 1);
+    const uint32_t xb = lds_addr(Xs + (t & 1) * BK * XB), sb = lds_addr(Ss + (t & 1) * NT * BK * 128);
+    u32x2_t xl[4][4], xh[4][4], sl[4][TSW], sh[4][TSW];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        tr_issue_p<XB>(make_uint2(xb + 2 * xoff[i].x, xb + 2 * xoff[i].y), q, xl[q][i], xh[q][i]);
+#pragma unroll
+      for (int j = 0; j < TSW; ++j)
+        tr_issue_p<128>(make_uint2(sb + 2 * soff[j].x, sb + 2 * soff[j].y), q, sl[q][j], sh[q][j]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // The results pass through these empty statements after the wait, so nothing reads them earlier.
+      bf16x8_t xf[4], sf[TSW];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        asm volatile("" : "+v"(xl[q][i]), "+v"(xh[q][i]));
+        xf[i] = tr_join(xl[q][i], xh[q][i]);
+      }
+#pragma unroll
+      for (int j = 0; j < TSW; ++j) {
+        asm volatile("" : "+v"(sl[q][j]), "+v"(sh[q][j]));
+        sf[j] = tr_join(sl[q][j], sh[q][j]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TSW; ++j)
+          acc[i][j] = TOUT ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[i], sf[j], acc[i][j], 0, 0, 0)
+                           : __builtin_amdgcn_mfma_f32_32x32x16_bf16(sf[j], xf[i], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  if (TOUT) {
+    // acc[i][j][r] = result[x = x0 + 32 i + 8 (r / 4) + 4 g + r % 4][s = 32 (TSW w + j) + lq]
+    float* W = p.WS + (int64_t)z * p.NX * NS;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int x = x0 + i * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+        if (x < p.NX) {
+#pragma unroll
+          for (int j = 0; j < TSW; ++j) W[(int64_t)x * NS + (TSW * w + j) * 32 + lq] = acc[i][j][r] * p.alpha;
+        }
+      }
+  } else {
+    // acc[i][j][r] = result[s = 32 (TSW w + j) + 8 (r / 4) + 4 g + r % 4][x = x0 + 32 i + lq]
+    float* W = p.WS + (int64_t)z * NS * p.NX;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = x0 + i * 32 + lq;
+      if (col < p.NX) {
+#pragma unroll
+        for (int j = 0; j < TSW; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = (TSW * w + j) * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+            W[(int64_t)row * p.NX + col] = acc[i][j][r] * p.alpha;
+          }
+      }
+    }
+  }
+}
+
+template <int NS>
+static void launch_tn_trw_t(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
+  constexpr size_t lds = 2 * 64 * (128 + NS) * sizeof(bf16_t);
+  UNOK_SET_LDS_ONCE((gemm_tn_trw_kernel<NS, true>), lds);
+  UNOK_SET_LDS_ONCE((gemm_tn_trw_kernel<NS, false>), lds);
+  const int nstrip = (p.NX + 127) / 128;
+  if (tout)
+    hipLaunchKernelGGL((gemm_tn_trw_kernel<NS, true>), dim3(nstrip * nz), dim3(256), lds, st, p);
+  else
+    hipLaunchKernelGGL((gemm_tn_trw_kernel<NS, false>), dim3(nstrip * nz), dim3(256), lds, st, p);
+}
+
+// Row splits of the transpose-load TN kernels: about one round of workgroups (3 per CU for NS = 64,
+// 2 for NS = 128 and 192, 1 for NS = 256 and 384 on 256 CUs), at most 16 splits for wide sides
+// (2048 columns and more, where the partials and their reduction would grow faster than the
+// parallelism helps) and 64 otherwise, at least 256 rows per split.
 static int tn_tr_splits(int Mrows, int NX, int NS) {
   const int nstrip = (NX + 127) / 128;
-  const int slots = NS == 64 ? 768 : 512;
+  const int slots = NS == 64 ? 768 : NS <= 192 ? 512 : 256;
   int nz = slots / nstrip;
   const int cap = NX >= 2048 ? 16 : 64;
   if (nz > cap) nz = cap;
@@ -1937,11 +2073,16 @@ static void launch_tn_skinny_t(const GemmTNSkinny& p, int nz, bool tout, hipStre
     hipLaunchKernelGGL((gemm_tn_skinny_kernel<NS, false>), dim3(nstrip * nz), dim3(512), 0, st, p);
 }
 
-// NS = 64 and 128 take the transpose-load kernel; other rank widths the register-transposing one.
+// NS = 64, 128 and 192 take the transpose-load kernel, 256 and 384 its wide variant; other rank
+// widths the register-transposing one.
+static bool tn_transpose_load(int NS) { return NS == 64 || NS == 128 || NS == 192 || NS == 256 || NS == 384; }
+
 static void launch_tn_skinny(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
   if (p.NS == 64) { launch_tn_tr_t<64>(p, nz, tout, st); return; }
   if (p.NS == 128) { launch_tn_tr_t<128>(p, nz, tout, st); return; }
   if (p.NS == 192) { launch_tn_tr_t<192>(p, nz, tout, st); return; }
+  if (p.NS == 256) { launch_tn_trw_t<256>(p, nz, tout, st); return; }
+  if (p.NS == 384) { launch_tn_trw_t<384>(p, nz, tout, st); return; }
   switch (p.NS) {
     case 32: launch_tn_skinny_t<32>(p, nz, tout, st); break;
     case 64: launch_tn_skinny_t<64>(p, nz, tout, st); break;
@@ -1965,15 +2106,15 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
   UNOK_REQUIRE(workspace != nullptr && ws_bytes >= need, UNOK_EINVAL,
                "gemm_tn: workspace of %lld bytes needed, %lld given", (long long)need, (long long)ws_bytes);
   if (in_dtype == UNOK_BF16 && Mrows > 0) {
-    // Skinny path: the rank side (<= 256 columns, a multiple of 32) against a wide operand.
+    // Skinny path: the rank side (<= 256 columns and a multiple of 32, or 384) against a wide operand.
     const bool a_small = P <= Q;
     const int NS = a_small ? P : Q, NX = a_small ? Q : P;
     const int64_t lds_ = a_small ? lda : ldb, ldx = a_small ? ldb : lda;
     const void* S = a_small ? A : B;
     const void* X = a_small ? B : A;
-    if (NS % 32 == 0 && NS <= 256 && NX >= TNS_QB && NX % 8 == 0 && lds_ % 8 == 0 && ldx % 8 == 0 &&
-        aligned16(S) && aligned16(X)) {
-      const bool tr = NS == 64 || NS == 128 || NS == 192;
+    if (((NS % 32 == 0 && NS <= 256) || NS == 384) && NX >= TNS_QB && NX % 8 == 0 && lds_ % 8 == 0 &&
+        ldx % 8 == 0 && aligned16(S) && aligned16(X)) {
+      const bool tr = tn_transpose_load(NS);
       const int nz0 = tr ? tn_tr_splits(Mrows, NX, NS) : tn_skinny_splits(Mrows, NX);
       int rps = (Mrows + nz0 - 1) / nz0;
       rps = ((rps + TNS_BK - 1) / TNS_BK) * TNS_BK;
