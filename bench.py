@@ -14,7 +14,8 @@ dispatch by a few microseconds, so the timed steps carry none). ``step_ms`` = me
 10th / 90th percentile of the timed steps from one HIP event between consecutive steps.
 ``cpu_baseline`` = the CPU oracle of the same step timed on this host on a bounded sample (see
 cpu_baseline()). ``--workload draft_8b`` measures the inference-side draft forward instead (see
-run_draft()).
+run_draft()), ``--workload tiny`` the tiny fp32 step with the CPU oracle's whole step beside it
+(see run_tiny()).
 """
 from __future__ import annotations
 
@@ -80,6 +81,8 @@ DRAFT = dict(batch=8, prompt=4096, block_size=16, lora_rank=64, lora_alpha=128)
 WORKLOAD_NAMES = {
     "qwen3_8b": "Qwen3-8B-shape cond-LoRA block-diffusion step (36 layers, 4 x 4096 tokens, block 16, LoRA r64)",
     "dense_1b": "1B-class (16 layers, hidden 2048, 16q/8kv) cond-LoRA step, rank 32",
+    "tiny": "tiny Qwen3-architecture cond-LoRA step in fp32 (2 layers, hidden 256, 4q/2kv heads of 64, vocab 4096, "
+            "rank 8, 2 x 256 tokens, block 4)",
     "mha_7b": "7B MHA (no q/k-norm, vocab 32000) cond-LoRA step, block curriculum 4/8/16/32",
     "packed_16k": "Qwen3-8B-shape step on one 16384-token row of packed segments, block 32",
     "qwen3_8b_r128": "Qwen3-8B-shape cond-LoRA step at the released recipe's rank 128 / alpha 2048, 8 x 4096 tokens, "
@@ -109,7 +112,7 @@ def build_step(cfg_kw: dict, wl: dict, device: str, seed: int = 20260813, total_
     from uno_amd.training.trainer import UnoTrainer, UnoTrainingArguments
 
     cfg = UnoQwen3Config(**cfg_kw, block_size=wl["block_size"], noise_seed=seed)
-    model = UnoQwen3ForCausalLM(cfg, device=device, dtype=torch.bfloat16)
+    model = UnoQwen3ForCausalLM(cfg, device=device, dtype=wl.get("dtype", torch.bfloat16))
     model.random_init(seed, std=0.02)
     lm, _ = create_lora_model(model, LoraSettings("all", wl["lora_rank"], wl["lora_alpha"], 0.0), seed=seed + 1)
     B, L = wl["batch"], wl["seq_len"]
@@ -214,6 +217,71 @@ def draft_bytes(cfg: dict, B: int, L: int, cached: float, r: int) -> dict:
          "embedding": B * L * H * 2, "logits": B * L * V * 2}
     b["total"] = sum(b.values())
     return b
+
+
+TINY = dict(vocab_size=4096, hidden_size=256, intermediate_size=768, num_hidden_layers=2, num_attention_heads=4,
+            num_key_value_heads=2, head_dim=64)
+TINY_WL = dict(batch=2, seq_len=256, prompt=64, block_size=4, lora_rank=8, lora_alpha=16, dtype=torch.float32)
+
+
+def run_tiny(args) -> int:
+    """The tiny Qwen3-architecture step (2 layers, hidden 256, 4 q / 2 kv heads of 64, FFN 768, vocab
+    4096, q/k-norm; LoRA rank 8 / alpha 16 on every projection; 2 x 256 tokens with a 64-token
+    prompt, block 4) in fp32, the precision of the parity runs: compute_loss + backward + clip +
+    AdamW per step on the GPU, and the CPU oracle's full step (the same step in fp32 PyTorch,
+    AdamW included) timed on this host beside it. Launch-bound on the GPU: a handful of
+    microseconds of work per kernel."""
+    wl = dict(TINY_WL, warmup=args.warmup, objective="ce")
+    dev = "cuda:0"
+    model, lm, trainer, batch = build_step(TINY, wl, dev)
+    for _ in range(args.warmup):
+        trainer.train_step(batch)
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    t0 = time.perf_counter()
+    evs[0].record()
+    for i in range(args.steps):
+        trainer.train_step(batch)
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1000.0 / args.steps
+    tokens = wl["batch"] * wl["seq_len"]
+    out = {"metric": "train tokens/s/GPU, tiny cond-LoRA step (fp32)", "value": round(tokens / (ms_step / 1000.0), 2),
+           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f32", "data": "synthetic (uniform token ids, random N(0,0.02) weights)",
+           "config": {"workload": WORKLOAD_NAMES["tiny"], "layers": TINY["num_hidden_layers"],
+                      "global_batch": wl["batch"], "seq_len": wl["seq_len"], "block_size": wl["block_size"],
+                      "lora_rank": wl["lora_rank"], "lora_alpha": wl["lora_alpha"],
+                      "objective": objective("ce")[1], "parallelism": "single GPU"},
+           "step_ms": spread([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]),
+           "roofline": None, "cpu_baseline": None}
+    if not args.no_cpu_baseline:
+        from oracle import step as ostep
+        from oracle.model import Cfg, init_lora, init_params
+        hi = host_info()
+        threads = args.cpu_threads or hi["physical_cores"] or hi["logical_cpus"]
+        torch.set_num_threads(threads)
+        cfg = Cfg(TINY["vocab_size"], TINY["hidden_size"], TINY["intermediate_size"], TINY["num_hidden_layers"],
+                  TINY["num_attention_heads"], TINY["num_key_value_heads"], TINY["head_dim"],
+                  lora_rank=wl["lora_rank"], lora_alpha=wl["lora_alpha"])
+        params, lora = init_params(cfg, seed=0), init_lora(cfg, seed=1)
+        cpu_batch = {k: v.cpu() for k, v in batch.items()}
+        kw = dict(block_size=wl["block_size"], mask_token_id=cfg.vocab_size - 1, seed=20260813)
+        ostep.train_steps(params, lora, cfg, cpu_batch, ostep.Objective(1, 0, 0, "data"), steps=1, **kw)
+        times = []
+        for i in range(10):
+            c0 = time.perf_counter()
+            ostep.train_steps(params, lora, cfg, cpu_batch, ostep.Objective(1, 0, 0, "data"), steps=1,
+                              first_step=i, **kw)
+            times.append(time.perf_counter() - c0)
+        t_cpu = sorted(times)[len(times) // 2]
+        out["cpu_baseline"] = {"value": round(tokens / t_cpu, 1), "unit": "tokens/s", "cores": threads,
+                               "kind": "port",
+                               "sample": f"fp32 CPU oracle, the whole tiny step (compute_loss, backward, AdamW): "
+                                         f"median of 10 steps, {t_cpu * 1000:.1f} ms per step", **hi}
+    print(json.dumps(out))
+    return 0
 
 
 def run_draft(args) -> int:
@@ -398,7 +466,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS) + ["draft_8b"],
+    ap.add_argument("--workload", default="qwen3_8b", choices=sorted(WORKLOADS) + ["draft_8b", "tiny"],
                     help="qwen3_8b is the headline; the others measure further model/batch shapes")
     ap.add_argument("--layers", type=int, default=None,
                     help="decoder layers (default: the workload's full depth)")
@@ -425,6 +493,8 @@ def main() -> int:
         return 2
     if args.workload == "draft_8b":
         return run_draft(args)
+    if args.workload == "tiny":
+        return run_tiny(args)
     from uno_amd import kernels as K
 
     base_cfg, wl = WORKLOADS[args.workload]
