@@ -269,18 +269,20 @@ int unok_ce_grad_chunk(int out_dtype, int R, int Vc, const float* z, int64_t ldz
 /* Cross-entropy over the LM head without materialised logits (BASELINE north star (4); the
  * loss of training/trainer.py:267-283 on the logits of training/losses.py:21-35). Z = H W^T with
  * H [R, K] bf16 (the CE rows' hidden states) and W [V, K] bf16 (LM-head rows vocab0 ..
- * vocab0 + V - 1); K a multiple of 64. Z is produced tile by tile inside the 256x256 MFMA GEMM and
- * never written.
+ * vocab0 + V - 1); K a multiple of 64. Z is produced tile by tile inside the 256x256 MFMA GEMM; it
+ * is written only when the caller asks for it.
  * unok_lmhead_ce_stats: pmax[r * ldp + b] / psum[r * ldp + b] = max / sum exp(z - max) over the
  *   columns [128 b, 128 b + 128) of row r (ldp >= ceil(V / 128)); zt[r] = Z[r, tgt[r] - vocab0]
- *   when the target lies in this product's columns.
+ *   when the target lies in this product's columns; with z non-null also Z itself in fp32
+ *   (z[r * ldz + v], ldz >= V and a multiple of 4, rows 16-byte aligned), for a backward that forms
+ *   dz from the stored logits with unok_ce_grad_chunk instead of recomputing them.
  * unok_ce_parts_reduce: merges a row's blocks into run_max / run_sum (then unok_ce_finish).
  * unok_lmhead_ce_grad: dz[r, v] = bf16(w[r] * g * inv_n * (exp(Z[r, v] - lse[r]) - [vocab0 + v ==
  *   tgt[r]])) for one vocabulary chunk (g, inv_n device scalars), the operand of the data-gradient
  *   GEMM dH += dz W[chunk]. */
 int unok_lmhead_ce_stats(int R, int V, int K, const void* H, int64_t ldh, const void* W, int64_t ldw,
                          const int64_t* tgt, int vocab0, float* pmax, float* psum, int64_t ldp,
-                         float* zt, void* stream);
+                         float* zt, float* z, int64_t ldz, void* stream);
 int unok_ce_parts_reduce(int R, int nparts, const float* pmax, const float* psum, int64_t ldp,
                          float* run_max, float* run_sum, void* stream);
 int unok_lmhead_ce_grad(int R, int V, int K, const void* H, int64_t ldh, const void* W, int64_t ldw,

@@ -451,6 +451,32 @@ def test_chunked_weighted_ce(dev, dtype, R, H, V, chunk, path, monkeypatch):
     assert (am == lg.argmax(-1)).float().mean().item() > (0.999 if dtype == torch.float32 else 0.98)
 
 
+@pytest.mark.parametrize("R,H,V,chunk", [(300, 256, 8192, 3000), (777, 4096, 151936, 32768), (260, 512, 8200, 8200)])
+def test_ce_stored_logits_match_recompute(dev, R, H, V, chunk, monkeypatch):
+    """bf16 CE: the backward that forms dz from the logits the forward stored gives the same loss
+    and data gradient, bit for bit, as the one that recomputes the logits in its GEMM epilogue
+    (ragged row and vocabulary edges, a chunk that does not divide V)."""
+    from uno_amd import objectives
+    from uno_amd.objectives import fused_weighted_ce
+    torch.manual_seed(7)
+    h = (torch.randn(R, H, device=dev) * 0.5).bfloat16()
+    w = (torch.randn(V, H, device=dev) * 0.05).bfloat16()
+    y = torch.randint(0, V, (R,), device=dev)
+    y[:3] = torch.tensor([0, V - 1, chunk], device=dev)       # targets on the vocabulary and chunk edges
+    wts = torch.rand(R, device=dev) * 2 + 0.5
+    inv_n = torch.tensor(1.0 / R, device=dev)
+    out = {}
+    for name, cap in (("stored", objectives.CE_STORED_LOGITS_MAX_BYTES), ("recompute", 0)):
+        monkeypatch.setattr(objectives, "CE_STORED_LOGITS_MAX_BYTES", cap)
+        hh = h.clone().requires_grad_(True)
+        loss = fused_weighted_ce(_Head(w), hh, y, wts, inv_n, chunk=chunk)
+        loss.backward()
+        out[name] = (loss.detach().clone(), hh.grad.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(out["stored"][0], out["recompute"][0])
+    assert torch.equal(out["stored"][1], out["recompute"][1])
+
+
 @pytest.mark.parametrize("kind", ["tv", "kl"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("V", [4099, 8200])   # element-wise rows; 16-byte row walks with a partial last step

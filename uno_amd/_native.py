@@ -60,7 +60,7 @@ SIGNATURES: dict[str, tuple] = {
     "unok_bd_region": (_i, [_i, _i, _p, _p, _p]),
     "unok_bd_compact": (_i, [_i64, _p, _p, _p, _p, _p, _p]),
     "unok_row_lse_update": (_i, [_i, _i, _i, _p, _i64, _i, _p, _p, _p, _p, _i, _p]),
-    "unok_lmhead_ce_stats": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i, _p, _p, _i64, _p, _p]),
+    "unok_lmhead_ce_stats": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i, _p, _p, _i64, _p, _p, _i64, _p]),
     "unok_ce_parts_reduce": (_i, [_i, _i, _p, _p, _i64, _p, _p, _p]),
     "unok_lmhead_ce_grad": (_i, [_i, _i, _i, _p, _i64, _p, _i64, _p, _i, _p, _p, _p, _p, _p, _i64, _p]),
     "unok_row_argmax_update": (_i, [_i, _i, _i, _p, _i64, _i, _p, _p, _i, _p]),

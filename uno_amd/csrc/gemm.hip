@@ -43,6 +43,7 @@ struct GemmNT {
   float* ce_pmax; float* ce_psum;  // EPI 3: [M, ld ce_ldp] per 128-column block max / sum exp(z - max)
   int64_t ce_ldp;
   float* ce_zt;                    // EPI 3: [M] target logit (rows whose target lies in this product)
+  float* ce_z; int64_t ce_ldz;     // EPI 3: [M, ld ce_ldz] the fp32 logits themselves (null: not stored)
   const float* ce_lse;             // EPI 4: [M] log-sum-exp over the whole vocabulary
   const float* ce_w;               // EPI 4: [M] row weights; scaled by *ce_g * *ce_inv_n
   const float* ce_g; const float* ce_inv_n;
@@ -1103,6 +1104,27 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_w4m16_kernel(const GemmNT p)
     // and the target logit of the rows whose target lies in the block.
     const int cb = n0 + wn * 128;
     const int part = cb >> 7;
+    if (p.ce_z) {
+      // the logits for a backward that reads them instead of recomputing them: lane (lr, lk) holds
+      // 4 consecutive columns of each (i, j) block, one 16-byte store each
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = m0 + wm * 128 + i * 16 + lr;
+        if (row >= p.M) continue;
+        float* zrow = p.ce_z + (int64_t)row * p.ce_ldz;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int col = cb + j * 16 + lk * 4;
+          if (col + 4 <= p.N) {
+            *(float4*)(zrow + col) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (col + q < p.N) zrow[col + q] = acc[i][j][q];
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int row = m0 + wm * 128 + i * 16 + lr;
@@ -1656,16 +1678,20 @@ static int ce_operands_ok(const char* what, int R, int V, int K, const void* H, 
 // targets inside [vocab0, vocab0 + V).
 UNOK_EXPORT int unok_lmhead_ce_stats(int R, int V, int K, const void* H, int64_t ldh, const void* W, int64_t ldw,
                                      const int64_t* tgt, int vocab0, float* pmax, float* psum, int64_t ldp,
-                                     float* zt, void* stream) {
+                                     float* zt, float* z, int64_t ldz, void* stream) {
   if (R == 0) return 0;
   int rc = ce_operands_ok("lmhead_ce_stats", R, V, K, H, ldh, W, ldw);
   if (rc) return rc;
   UNOK_REQUIRE(ldp >= (V + 127) / 128, UNOK_EINVAL, "lmhead_ce_stats: ldp=%lld < %d blocks", (long long)ldp,
                (V + 127) / 128);
+  UNOK_REQUIRE(z == nullptr || (ldz >= V && ldz % 4 == 0 && aligned16(z)), UNOK_EALIGN,
+               "lmhead_ce_stats: z rows must be 16-byte aligned with a stride >= V, multiple of 4 (ldz=%lld)",
+               (long long)ldz);
   GemmNT p{};
   p.A = H; p.lda = ldh; p.B = W; p.ldb = ldw; p.M = R; p.N = V; p.K = K; p.alpha = 1.f; p.nseg = 1;
   for (int i = 0; i < 4; ++i) { p.seg_end[i] = V; p.seg_col[i] = 0; }
   p.ce_tgt = tgt; p.ce_vocab0 = vocab0; p.ce_pmax = pmax; p.ce_psum = psum; p.ce_ldp = ldp; p.ce_zt = zt;
+  p.ce_z = z; p.ce_ldz = ldz;
   launch_nt_w4m16<float, 3>(p, (hipStream_t)stream);
   return unok::check_launch("lmhead_ce_stats");
 }

@@ -19,6 +19,9 @@ from . import kernels as K
 
 # Vocabulary columns per chunk of the CE backward (and of the fp32 / argmax chunk buffers).
 DEFAULT_CE_CHUNK = 32768
+# The bf16 CE keeps the LM-head logits of its rows (fp32) from the forward for the backward when
+# they take at most this many bytes; beyond it the backward recomputes them inside its GEMM.
+CE_STORED_LOGITS_MAX_BYTES = 6 << 30
 
 
 def lm_head_logits(lm_head, x: torch.Tensor) -> torch.Tensor:
@@ -55,10 +58,12 @@ def _fused_ce_ok(h: torch.Tensor, w_lm: torch.Tensor) -> bool:
 class ChunkedWeightedCE(torch.autograd.Function):
     """loss = inv_n * sum_r w_r * CE(h_r W^T, y_r); inv_n is a device scalar.
 
-    bf16 (the step): the forward is one LM-head GEMM whose epilogue keeps only per-row softmax
-    statistics per 128 vocabulary columns and the target logit; the backward recomputes the
-    logits chunk by chunk inside a GEMM whose epilogue writes dz (bf16, one [rows x chunk]
-    buffer) and feeds it to the data-gradient GEMM. No [rows x vocab] tensor exists.
+    bf16 (the step): the forward is one LM-head GEMM whose epilogue keeps per-row softmax
+    statistics per 128 vocabulary columns and the target logit. When the rows' fp32 logits fit
+    CE_STORED_LOGITS_MAX_BYTES, the same epilogue also stores them and the backward forms dz
+    (bf16, one [rows x chunk] buffer) from them with a row kernel, chunk by chunk; otherwise it
+    recomputes the logits inside a GEMM whose epilogue writes dz. Both give the same dz bit for
+    bit (the same logits, the same arithmetic), which feeds the data-gradient GEMM.
     fp32 (parity mode) and other shapes: the logits of one vocabulary chunk at a time go through a
     chunk buffer and the row kernels, recomputed in the backward."""
 
@@ -72,11 +77,14 @@ class ChunkedWeightedCE(torch.autograd.Function):
         lse = torch.empty(R, **f32)
         loss = torch.empty((), **f32)
         fused = _fused_ce_ok(h, w_lm)
+        z_all = None
         if fused:
             nparts = (V + 127) // 128
             pmax, psum = torch.empty((R, nparts), **f32), torch.empty((R, nparts), **f32)
+            if V % 4 == 0 and R * V * 4 <= CE_STORED_LOGITS_MAX_BYTES:
+                z_all = torch.empty((R, V), **f32)
             N.call("unok_lmhead_ce_stats", R, V, h.shape[1], N.ptr(h), h.stride(0), N.ptr(w_lm), w_lm.stride(0),
-                   N.ptr(targets), 0, N.ptr(pmax), N.ptr(psum), nparts, N.ptr(zt), N.stream())
+                   N.ptr(targets), 0, N.ptr(pmax), N.ptr(psum), nparts, N.ptr(zt), N.ptr(z_all), V, N.stream())
             N.call("unok_ce_parts_reduce", R, nparts, N.ptr(pmax), N.ptr(psum), nparts, N.ptr(run_max),
                    N.ptr(run_sum), N.stream())
             del pmax, psum
@@ -90,12 +98,12 @@ class ChunkedWeightedCE(torch.autograd.Function):
             del buf
         N.call("unok_ce_finish", R, N.ptr(run_max), N.ptr(run_sum), N.ptr(zt), N.ptr(weights), N.ptr(inv_n),
                N.ptr(lse), N.ptr(loss), N.stream())
-        ctx.save = (h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, fused)
+        ctx.save = (h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, fused, z_all)
         return loss
 
     @staticmethod
     def backward(ctx, g):
-        h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, fused = ctx.save
+        h, w_lm, w_lm_t, targets, weights, inv_n, lse, chunk, fused, z_all = ctx.save
         ctx.save = None
         R, V = h.shape[0], w_lm.shape[0]
         g = g.reshape(1).float().contiguous()
@@ -106,7 +114,11 @@ class ChunkedWeightedCE(torch.autograd.Function):
         buf = None if fused else torch.empty((R, width), **f32)
         for c0, c1 in _chunks(V, chunk):
             d = dz[:, :c1 - c0]
-            if fused:
+            if z_all is not None:
+                N.call("unok_ce_grad_chunk", N.dtype_code(h.dtype), R, c1 - c0, N.ptr(z_all[:, c0:]), z_all.stride(0),
+                       c0, N.ptr(lse), N.ptr(targets), N.ptr(weights), N.ptr(g), N.ptr(inv_n), N.ptr(d), dz.stride(0),
+                       N.stream())
+            elif fused:
                 N.call("unok_lmhead_ce_grad", R, c1 - c0, h.shape[1], N.ptr(h), h.stride(0), N.ptr(w_lm[c0:c1]),
                        w_lm.stride(0), N.ptr(targets), c0, N.ptr(lse), N.ptr(weights), N.ptr(g), N.ptr(inv_n),
                        N.ptr(dz), dz.stride(0), N.stream())
