@@ -4,8 +4,8 @@ causal pass over [prompt, committed seeds, block] with the LoRA gate on the bloc
 only (nano_vllm_uno/layers/linear.py:166-307) equals a prefill into the KV cache followed by draft
 blocks over it (nano_vllm_uno/layers/attention.py:628-668: causal over the cache and the block).
 Sequences with different cached lengths, GQA 4:1 with the largest block the layout holds
-(4 x 32 = 128 query rows per K/V head), fp32 and bf16, and a rank-32 adapter whose bf16 draft
-blocks run on the few-row products."""
+(4 x 32 = 128 query rows per K/V head), fp32 and bf16, and rank-32 and rank-128 adapters whose
+bf16 draft blocks run on the few-row products."""
 import pytest
 import torch
 
@@ -25,6 +25,9 @@ SPECS = {
     # rank 32: bf16 draft blocks take the few-row products (unok_gemm_nt_rows)
     "gqa4_r32": dict(vocab_size=4096, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
                      num_attention_heads=4, num_key_value_heads=1, head_dim=128, rank=32, alpha=64),
+    # rank 128 (the released recipe's): 384 LoRA A rows per q|k|v product, three extra product tiles
+    "gqa4_r128": dict(vocab_size=4096, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=1, head_dim=128, rank=128, alpha=256),
 }
 
 
@@ -41,7 +44,7 @@ def _rel(a, b):
     return ((a.float().cpu() - b).norm() / b.norm()).item()
 
 
-@pytest.mark.parametrize("spec_name,L", [("gqa2", 8), ("gqa4_d128", 32), ("gqa4_r32", 16)])
+@pytest.mark.parametrize("spec_name,L", [("gqa2", 8), ("gqa4_d128", 32), ("gqa4_r32", 16), ("gqa4_r128", 16)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_prefill_then_draft_blocks(dev, spec_name, L, dtype):
     s = SPECS[spec_name]
