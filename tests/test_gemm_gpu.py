@@ -82,11 +82,13 @@ def test_gemm_nt_direct_to_lds_path(dev, M, N, Kd):
 
 
 @pytest.mark.parametrize("M,N,Kd", [(16384, 64, 4096), (16384, 128, 1024), (16384, 192, 4096),
-                                    (8237, 64, 12288), (4096, 100, 512), (5000, 160, 640)])
+                                    (8237, 64, 12288), (4096, 100, 512), (5000, 160, 640),
+                                    (32768, 128, 12288), (32800, 120, 8192)])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_gemm_nt_skinny_path(dev, M, N, Kd, out_dtype):
     """Skinny products (N <= 192, M >= 4096, K a multiple of 64): one 64-row tile spans all N
-    columns. Ragged M and N, a row gate and alpha, bf16 and fp32 outputs."""
+    columns (128-row tiles of 8 waves for N <= 128 at >= 32768 rows and K >= 8192). Ragged M and N,
+    a row gate and alpha, bf16 and fp32 outputs."""
     torch.manual_seed(M + N + Kd)
     a = torch.randn(M, Kd, device=dev).bfloat16()
     b = torch.randn(N, Kd, device=dev).bfloat16()

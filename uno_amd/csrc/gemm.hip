@@ -1772,7 +1772,13 @@ UNOK_EXPORT int unok_gemm_nt(int in_dtype, int out_dtype, int M, int N, int K,
     // 208 us for a 64 x N tile at 32768 x 4096.)
     const int bn = (N + 63) / 64 * 64;
     if (bn == 64) launch_nt_skinny_t<64, 4>(p, out_dtype, st);
-    else if (bn == 128) launch_nt_skinny_t<128, 4>(p, out_dtype, st);
+    else if (bn == 128 && M >= 32768 && K >= 8192) {
+      // many rows and a long K (the rank-128 products over the 12288-wide FFN side at 8 x 4096
+      // rows): 128-row tiles of 8 waves read each weight tile from L2 half as often (221 against
+      // 260 us at 32768 x 128 x 12288; at 4096-deep or 16384-row shapes they do not pay)
+      if (out_dtype == UNOK_F32) launch_nt_dma_t<128, 128, 8, 64, 3, float, true>(p, st);
+      else launch_nt_dma_t<128, 128, 8, 64, 3, bf16_t, true>(p, st);
+    } else if (bn == 128) launch_nt_skinny_t<128, 4>(p, out_dtype, st);
     else launch_nt_skinny_t<192, 3>(p, out_dtype, st);
   } else if (N <= 64 || !segs_ok(128)) {
     UNOK_REQUIRE(segs_ok(64), UNOK_EINVAL, "gemm_nt(bf16): segment ends must be multiples of 64");
