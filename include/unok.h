@@ -114,7 +114,7 @@ int unok_gemm_tn_noalloc(int in_dtype, int Mrows, int P, int Q, const void* A, i
 
 /* ---- Row-wise decoder ops ----------------------------------------------------------------- */
 
-/* y = w * round(x * rsqrt(mean(x^2) + eps)), rstd[M] saved. Qwen3RMSNorm
+/* y = round(x * rsqrt(mean(x^2) + eps) * w) (one rounding), rstd[M] saved. Qwen3RMSNorm
  * (modeling_qwen3.py:50-64); input/post-attention/final norms of the remote decoder. */
 int unok_rmsnorm_fwd(int dtype, int M, int H, const void* x, int64_t ldx, const void* w,
                      void* y, int64_t ldy, float* rstd, float eps, void* stream);

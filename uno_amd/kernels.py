@@ -229,7 +229,7 @@ def _contig(t: torch.Tensor, name: str) -> None:
 
 
 def rmsnorm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | None = None):
-    """y = w * round(x * rsqrt(mean(x^2) + eps)); returns (y, rstd[M] fp32)."""
+    """y = round(x * rsqrt(mean(x^2) + eps) * w); returns (y, rstd[M] fp32)."""
     _rowmajor(x, "x")
     M, Hd = x.shape
     if w.numel() != Hd or w.dtype != x.dtype:
