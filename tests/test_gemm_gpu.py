@@ -140,13 +140,14 @@ def test_gemm_tn(dev, Mr, P, Q, dtype):
 @pytest.mark.parametrize("Mr,P,Q", [(1000, 192, 4096), (16384, 4096, 64), (777, 1000, 96), (4100, 64, 12288),
                                      (300, 1032, 256), (16384, 128, 4096), (2000, 64, 1000), (2000, 1000, 64),
                                      (2000, 1000, 128), (16384, 192, 4096), (3000, 4104, 192),
-                                     (4096, 32, 2048), (3000, 5640, 32),
+                                     (4096, 32, 2048), (3000, 5640, 32), (16384, 5632, 32), (3000, 96, 5640),
+                                     (16384, 96, 2048), (1000, 160, 4104), (2000, 4104, 160),
                                      (4100, 384, 4096), (3000, 4104, 384), (2000, 256, 1000), (16384, 4096, 256),
                                      (777, 384, 12288), (32768, 384, 4096)])
 def test_gemm_tn_skinny_bf16(dev, Mr, P, Q):
-    """LoRA weight-gradient shapes (rank side <= 256 columns, or 384 = 3r at rank 128): dA = g^T x
-    and dB = dY^T h, with ragged row counts and wide sides that are not a multiple of the 128- or
-    256-column strips."""
+    """LoRA weight-gradient shapes (rank side <= 256 columns, or 384 = 3r at rank 128; 32, 96 and 160
+    are r, 3r and 5r at rank 32): dA = g^T x and dB = dY^T h, with ragged row counts and wide sides
+    that are not a multiple of the 128- or 256-column strips."""
     torch.manual_seed(Mr + Q)
     a = torch.randn(Mr, P, device=dev).bfloat16()
     b = torch.randn(Mr, Q, device=dev).bfloat16()
@@ -159,11 +160,12 @@ def test_gemm_tn_skinny_bf16(dev, Mr, P, Q):
     assert _rel(fresh, a.float().T @ b.float()) < 1e-5
 
 
-def test_gemm_tn_skinny_column_slices(dev):
+@pytest.mark.parametrize("r", [64, 32])
+def test_gemm_tn_skinny_column_slices(dev, r):
     """Operands that are column slices of wider buffers (g_gu[:, r:2r], dgu[:, F:2F]) and an
     output that is a row slice of the flat gradient buffer."""
     torch.manual_seed(5)
-    Mr, F, r = 2048, 1536, 64
+    Mr, F = 2048, 1536
     dgu = torch.randn(Mr, 2 * F, device=dev).bfloat16()
     h = torch.randn(Mr, 2 * r, device=dev).bfloat16()
     flat = torch.randn(3 * F * r, device=dev)

@@ -1822,18 +1822,19 @@ static int tn_skinny_splits(int Mrows, int NX) {
 // into two LDS stages by direct-to-LDS loads (kswz-swizzled rows); every MFMA operand is an LDS
 // transpose load of 16 rows (the same permuted row order for both operands, so the products
 // pair up). Wave w owns x columns x0 + 32 w .. + 31 and all NS / 32 row blocks. Partials are
-// written in the layout of gemm_tn_skinny_kernel, for the same split-K reduction. Three
-// workgroups per CU for NS = 64 (48 KB of LDS each), so the split counts of the LoRA shapes
-// (e.g. 96 strips x 6 splits for 12288 columns) run in one round; two for NS = 128 (64 KB) and
-// NS = 192 (80 KB).
+// written in the layout of gemm_tn_skinny_kernel, for the same split-K reduction. Four
+// workgroups per CU for NS = 32 (40 KB of LDS each) and three for NS = 64 (48 KB), so the split
+// counts of the LoRA shapes (e.g. 96 strips x 6 splits for 12288 columns) run in one round; two
+// for NS = 96 .. 192 (56 .. 80 KB).
 template <int NS, bool TOUT>
-__global__ __launch_bounds__(256, NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const GemmTNSkinny p) {
+__global__ __launch_bounds__(256, NS == 32 ? 4 : NS == 64 ? 3 : 2) void gemm_tn_tr_kernel(const GemmTNSkinny p) {
   constexpr int BK = 64, XB = 128, TS = NS / 32;
-  // The skinny operand's tile is one swizzled [64 x NSA] tile and, for NS = 192, a second
-  // [64 x 64] one holding columns 128 .. 191.
-  constexpr int NSA = NS > 128 ? 128 : NS, NSB = NS - NSA, TSA = NSA / 32;
+  // The skinny operand's tile is one swizzled [64 x NSA] tile (NSA = 128, 64 or 32) and, for
+  // NS = 96, 160 and 192, a second [64 x NSB] one (NSB = 32 or 64) holding the columns past NSA.
+  constexpr int NSA = NS >= 128 ? 128 : NS >= 64 ? 64 : 32, NSB = NS - NSA, TSA = NSA / 32;
   constexpr int NSB_ = NSB > 0 ? NSB : 64;   // tile width for the helpers (unused when NSB = 0)
-  static_assert(NS == 64 || NS == 128 || NS == 192, "skinny side of 64, 128 or 192 (128 + 64) columns");
+  static_assert(NS == 32 || NS == 64 || NS == 96 || NS == 128 || NS == 160 || NS == 192,
+                "skinny side of 32, 64, 96 (64 + 32), 128, 160 (128 + 32) or 192 (128 + 64) columns");
   extern __shared__ __attribute__((aligned(16))) bf16_t smem[];
   bf16_t* Xs = smem;                   // [2][BK * XB]
   bf16_t* Ss = smem + 2 * BK * XB;     // [2][BK * NSA]
@@ -2072,13 +2073,13 @@ static void launch_tn_trw_t(const GemmTNSkinny& p, int nz, bool tout, hipStream_
     hipLaunchKernelGGL((gemm_tn_trw_kernel<NS, false>), dim3(nstrip * nz), dim3(256), lds, st, p);
 }
 
-// Row splits of the transpose-load TN kernels: about one round of workgroups (3 per CU for NS = 64,
-// 2 for NS = 128 and 192, 1 for NS = 256 and 384 on 256 CUs), at most 16 splits for wide sides
+// Row splits of the transpose-load TN kernels: about one round of workgroups (4 per CU for NS = 32,
+// 3 for NS = 64, 2 for NS = 96 .. 192, 1 for NS = 256 and 384 on 256 CUs), at most 16 splits for wide sides
 // (2048 columns and more, where the partials and their reduction would grow faster than the
 // parallelism helps) and 64 otherwise, at least 256 rows per split.
 static int tn_tr_splits(int Mrows, int NX, int NS) {
   const int nstrip = (NX + 127) / 128;
-  const int slots = NS == 64 ? 768 : NS <= 192 ? 512 : 256;
+  const int slots = NS == 32 ? 1024 : NS == 64 ? 768 : NS <= 192 ? 512 : 256;
   int nz = slots / nstrip;
   const int cap = NX >= 2048 ? 16 : 64;
   if (nz > cap) nz = cap;
@@ -2105,12 +2106,15 @@ static void launch_tn_skinny_t(const GemmTNSkinny& p, int nz, bool tout, hipStre
     hipLaunchKernelGGL((gemm_tn_skinny_kernel<NS, false>), dim3(nstrip * nz), dim3(512), 0, st, p);
 }
 
-// NS = 64, 128 and 192 take the transpose-load kernel, 256 and 384 its wide variant; other rank
-// widths the register-transposing one.
-static bool tn_transpose_load(int NS) { return NS == 64 || NS == 128 || NS == 192 || NS == 256 || NS == 384; }
+// NS = 32, 64, 96, 128, 160 and 192 take the transpose-load kernel, 256 and 384 its wide variant;
+// NS = 224 the register-transposing one.
+static bool tn_transpose_load(int NS) { return NS <= 192 || NS == 256 || NS == 384; }
 
 static void launch_tn_skinny(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
+  if (p.NS == 32) { launch_tn_tr_t<32>(p, nz, tout, st); return; }
   if (p.NS == 64) { launch_tn_tr_t<64>(p, nz, tout, st); return; }
+  if (p.NS == 96) { launch_tn_tr_t<96>(p, nz, tout, st); return; }
+  if (p.NS == 160) { launch_tn_tr_t<160>(p, nz, tout, st); return; }
   if (p.NS == 128) { launch_tn_tr_t<128>(p, nz, tout, st); return; }
   if (p.NS == 192) { launch_tn_tr_t<192>(p, nz, tout, st); return; }
   if (p.NS == 256) { launch_tn_trw_t<256>(p, nz, tout, st); return; }

@@ -9,9 +9,11 @@
 // over the 64 banks) kswz rotates the row's low four bits: it is a bijection on any 16
 // consecutive rows (16-byte fragment reads: 16 rows, one chunk, per LDS cycle) and its two high
 // bits differ across any 4 aligned rows (transpose loads: 4 rows x 4 consecutive chunks per half
-// wave), so both read patterns hit distinct banks. kswz(r + 16) = kswz(r).
+// wave), so both read patterns hit distinct banks. kswz(r + 16) = kswz(r). D = 32 tiles
+// (64-byte rows) need no swizzle: the half wave of a transpose load reads 4 consecutive whole
+// rows, 256 contiguous bytes.
 template <int D> __device__ __forceinline__ int kswz(int r) {
-  return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((r >> 1) & 7);
+  return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : D == 32 ? 0 : ((r >> 1) & 7);
 }
 
 // A operand of a 16-key MFMA step read straight from a row-major, kswz-swizzled [64 keys x D]
