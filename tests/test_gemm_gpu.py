@@ -143,11 +143,11 @@ def test_gemm_tn(dev, Mr, P, Q, dtype):
                                      (4096, 32, 2048), (3000, 5640, 32), (16384, 5632, 32), (3000, 96, 5640),
                                      (16384, 96, 2048), (1000, 160, 4104), (2000, 4104, 160),
                                      (4100, 384, 4096), (3000, 4104, 384), (2000, 256, 1000), (16384, 4096, 256),
-                                     (777, 384, 12288), (32768, 384, 4096)])
+                                     (777, 384, 12288), (32768, 384, 4096), (2000, 224, 1024), (1000, 4096, 288)])
 def test_gemm_tn_skinny_bf16(dev, Mr, P, Q):
     """LoRA weight-gradient shapes (rank side <= 256 columns, or 384 = 3r at rank 128; 32, 96 and 160
     are r, 3r and 5r at rank 32): dA = g^T x and dB = dY^T h, with ragged row counts and wide sides
-    that are not a multiple of the 128- or 256-column strips."""
+    that are not a multiple of the 128- or 256-column strips; 224 and 288 take the general kernel."""
     torch.manual_seed(Mr + Q)
     a = torch.randn(Mr, P, device=dev).bfloat16()
     b = torch.randn(Mr, Q, device=dev).bfloat16()

@@ -628,150 +628,22 @@ __global__ __launch_bounds__(256) void gemm_tn_f32_kernel(const GemmTN p) {
 // ---------------------------------------------------------------------------------------
 // Skinny TN product of the LoRA weight gradients:
 //   WS[z][s][x] = alpha * sum_{m in rows of split z} S[m, s] X[m, x]
-// S is the rank-side operand (NS <= 256 columns, a multiple of 32: g or h) and X the wide
-// activation or gradient (x, dY). The product is HBM-bound on X, so the kernel streams X once:
-// a workgroup owns a strip of 256 X columns and a contiguous range of rows. Every thread loads
-// one 8x8 block (8 rows x 16 bytes) of X or S, transposes it in registers and writes it to LDS
-// with the token index contiguous ([column][m], 72-element rows, 16-byte chunk c of row r at slot
-// c ^ ((r >> 4) & 7) so both the transposed writes and the MFMA operand reads spread over the
-// banks). Wave w then owns X columns [32w, 32w + 32) of the strip and all NS rows of the result
-// (32x32x16 bf16 MFMAs). The next 64-row tile is fetched into registers during the MFMAs.
+// S is the rank-side operand (g or h: 32 .. 192 columns in steps of 32, or 256 / 384) and X the
+// wide activation or gradient (x, dY). The product is HBM-bound on X, so X is streamed once: a
+// workgroup owns a strip of X columns and a contiguous range of token rows (a split); the splits'
+// fp32 partials are added by splitk_reduce_kernel. The kernels are gemm_tn_tr_kernel and
+// gemm_tn_trw_kernel below, next to the C-ABI.
 // ---------------------------------------------------------------------------------------
 struct GemmTNSkinny {
   const bf16_t* S; int64_t lds;   // [Mrows, NS]
   const bf16_t* X; int64_t ldx;   // [Mrows, NX]
-  float* WS;                       // [nsplit, NS, NX]
+  float* WS;                       // [nsplit, NS, NX] or, transposed, [nsplit, NX, NS]
   int Mrows, NS, NX, rows_per_split;
   float alpha;
 };
 
-constexpr int TNS_QB = 256;   // X columns per workgroup
-constexpr int TNS_BK = 64;    // token rows per tile
-constexpr int TNS_LD = 72;    // LDS row pitch in elements
-
-// out[c] = column c of the 8x8 bf16 block whose rows are in[0..7].
-__device__ __forceinline__ void transpose8x8_bf16(const uint4 (&in)[8], uint4 (&out)[8]) {
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint4 a = in[2 * k], b = in[2 * k + 1];
-      const uint32_t da = (c >> 1) == 0 ? a.x : (c >> 1) == 1 ? a.y : (c >> 1) == 2 ? a.z : a.w;
-      const uint32_t db = (c >> 1) == 0 ? b.x : (c >> 1) == 1 ? b.y : (c >> 1) == 2 ? b.z : b.w;
-      w[k] = (c & 1) ? ((da >> 16) | (db & 0xffff0000u)) : ((da & 0xffffu) | (db << 16));
-    }
-    out[c] = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-}
-
-__device__ __forceinline__ int tns_slot(int row, int chunk) { return chunk ^ ((row >> 4) & 7); }
-
-// TOUT = false: WS[z][s][x] (the result is [rank, wide], e.g. dA = g^T x);
-// TOUT = true:  WS[z][x][s] (the result is [wide, rank], e.g. dB = dY^T h), computed as X^T S so
-// that both layouts are written and reduced with contiguous rows.
-template <int NS, bool TOUT>
-__global__ __launch_bounds__(512) void gemm_tn_skinny_kernel(const GemmTNSkinny p) {
-  constexpr int TM = NS / 32;
-  constexpr int XBLK = (TNS_BK / 8) * (TNS_QB / 8);   // 256 blocks of 8x8 in an X tile
-  constexpr int SCOLS = NS / 8;
-  constexpr int SBLK = (TNS_BK / 8) * SCOLS;
-  static_assert(NS % 32 == 0 && NS <= 256, "NS must be a multiple of 32, at most 256");
-  __shared__ __attribute__((aligned(16))) bf16_t Xs[TNS_QB * TNS_LD];
-  __shared__ __attribute__((aligned(16))) bf16_t Ss[NS * TNS_LD];
-
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int nstrip = (p.NX + TNS_QB - 1) / TNS_QB;
-  const int nz = gridDim.x / nstrip;
-  const int lin = xcd_remap(blockIdx.x, nstrip * nz);
-  const int x0 = (lin % nstrip) * TNS_QB;
-  const int z = lin / nstrip;
-  const int mbeg = z * p.rows_per_split;
-  const int mend = min(p.Mrows, mbeg + p.rows_per_split);
-
-  // This thread's 8x8 block: X block (tid < 256) or S block.
-  const bool isx = tid < XBLK;
-  const int sb = tid - XBLK;
-  const bool active = isx || sb < SBLK;
-  const int mg = isx ? tid / (TNS_QB / 8) : sb / SCOLS;          // row group (8 rows)
-  const int cl = isx ? (tid % (TNS_QB / 8)) * 8 : (sb % SCOLS) * 8;  // first column in the tile
-  const bool colok = active && (isx ? (x0 + cl < p.NX) : true);
-  const bf16_t* src = isx ? p.X + x0 + cl : p.S + cl;
-  const int64_t ld = isx ? p.ldx : p.lds;
-  bf16_t* dst = isx ? Xs : Ss;
-
-  uint4 st[8];
-  auto load = [&](int m0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int gm = m0 + mg * 8 + i;
-      st[i] = (colok && gm < mend) ? *(const uint4*)(src + (int64_t)gm * ld) : make_uint4(0, 0, 0, 0);
-    }
-  };
-
-  f32x16_t acc[TM];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-
-  const int lrow = lane & 31, lg = lane >> 5;
-  load(mbeg);
-  for (int m0 = mbeg; m0 < mend; m0 += TNS_BK) {
-    uint4 tr[8];
-    transpose8x8_bf16(st, tr);
-    __syncthreads();
-    if (active) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int r = cl + c;
-        *(uint4*)&dst[r * TNS_LD + tns_slot(r, mg) * 8] = tr[c];
-      }
-    }
-    __syncthreads();
-    if (m0 + TNS_BK < mend) load(m0 + TNS_BK);
-#pragma unroll
-    for (int ks = 0; ks < TNS_BK / 16; ++ks) {
-      const int chunk = ks * 2 + lg;
-      const int xr = wid * 32 + lrow;
-      const bf16x8_t b = *(const bf16x8_t*)&Xs[xr * TNS_LD + tns_slot(xr, chunk) * 8];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int sr = i * 32 + lrow;
-        const bf16x8_t a = *(const bf16x8_t*)&Ss[sr * TNS_LD + tns_slot(sr, chunk) * 8];
-        if (TOUT)
-          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, acc[i], 0, 0, 0);
-        else
-          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[i], 0, 0, 0);
-      }
-    }
-  }
-
-  if (TOUT) {
-    // acc[i][r] = result[x = x0 + 32 wid + 8 (r / 4) + 4 lg + r % 4][s = 32 i + lrow]
-    float* W = p.WS + (int64_t)z * p.NX * NS;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int x = x0 + wid * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
-      if (x < p.NX) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) W[(int64_t)x * NS + i * 32 + lrow] = acc[i][r] * p.alpha;
-      }
-    }
-  } else {
-    const int col = x0 + wid * 32 + lrow;
-    if (col < p.NX) {
-      float* W = p.WS + (int64_t)z * NS * p.NX + col;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = i * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
-          W[(int64_t)row * p.NX] = acc[i][r] * p.alpha;
-        }
-    }
-  }
-}
+constexpr int TNS_MIN_NX = 256;   // narrowest wide side the skinny path takes
+constexpr int TNS_BK = 64;        // token rows per tile (split ranges are whole tiles)
 
 // C[P,Q] (row stride ldc, fp32) = beta * C + sum_z WS[z], partials summed in z order. With Q and
 // ldc multiples of 4 and 16-byte aligned buffers each thread takes 4 consecutive elements, and
@@ -1805,24 +1677,13 @@ static int tn_general_splits(int Mrows, int P, int Q) {
   return nsplit < 1 ? 1 : (int)nsplit;
 }
 
-// Workgroups the register-transposing skinny TN kernel aims for: one per CU.
-static int tn_skinny_target() { return 256; }
-
-static int tn_skinny_splits(int Mrows, int NX) {
-  const int nstrip = (NX + TNS_QB - 1) / TNS_QB;
-  int nz = (tn_skinny_target() + nstrip - 1) / nstrip;
-  const int max_split = (Mrows + 255) / 256;
-  if (nz > max_split) nz = max_split;
-  return nz < 1 ? 1 : nz;
-}
-
 // Skinny TN product with both operands read as columns of row-major LDS tiles: per workgroup,
 // out tile [NS x 128] (rows s of the skinny operand S, columns x0 .. x0 + 127 of the wide operand
 // X) over one split of the token rows. 64-row tiles of X (128 columns) and S (NS columns) stream
 // into two LDS stages by direct-to-LDS loads (kswz-swizzled rows); every MFMA operand is an LDS
 // transpose load of 16 rows (the same permuted row order for both operands, so the products
 // pair up). Wave w owns x columns x0 + 32 w .. + 31 and all NS / 32 row blocks. Partials are
-// written in the layout of gemm_tn_skinny_kernel, for the same split-K reduction. Four
+// written as WS[z][s][x] (TOUT: WS[z][x][s]), for the split-K reduction. Four
 // workgroups per CU for NS = 32 (40 KB of LDS each) and three for NS = 64 (48 KB), so the split
 // counts of the LoRA shapes (e.g. 96 strips x 6 splits for 12288 columns) run in one round; two
 // for NS = 96 .. 192 (56 .. 80 KB).
@@ -2090,44 +1951,24 @@ static int tn_tr_splits(int Mrows, int NX, int NS) {
 
 UNOK_EXPORT int64_t unok_gemm_tn_workspace(int Mrows, int P, int Q) {
   const int a = tn_general_splits(Mrows, P, Q);
-  const int b = tn_skinny_splits(Mrows, P <= Q ? Q : P);
   const int c = tn_tr_splits(Mrows, P <= Q ? Q : P, P <= Q ? P : Q);
-  int m = a > b ? a : b;
-  if (c > m) m = c;
-  return (int64_t)m * P * Q * 4;
+  return (int64_t)(a > c ? a : c) * P * Q * 4;
 }
 
-template <int NS>
-static void launch_tn_skinny_t(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
-  const int nstrip = (p.NX + TNS_QB - 1) / TNS_QB;
-  if (tout)
-    hipLaunchKernelGGL((gemm_tn_skinny_kernel<NS, true>), dim3(nstrip * nz), dim3(512), 0, st, p);
-  else
-    hipLaunchKernelGGL((gemm_tn_skinny_kernel<NS, false>), dim3(nstrip * nz), dim3(512), 0, st, p);
-}
-
-// NS = 32, 64, 96, 128, 160 and 192 take the transpose-load kernel, 256 and 384 its wide variant;
-// NS = 224 the register-transposing one.
-static bool tn_transpose_load(int NS) { return NS <= 192 || NS == 256 || NS == 384; }
+// Rank-side widths of the skinny path: 32 .. 192 in steps of 32 on the transpose-load kernel,
+// 256 and 384 on its wide variant; other widths take the general TN kernel.
+static bool tn_skinny_width(int NS) { return (NS % 32 == 0 && NS <= 192) || NS == 256 || NS == 384; }
 
 static void launch_tn_skinny(const GemmTNSkinny& p, int nz, bool tout, hipStream_t st) {
-  if (p.NS == 32) { launch_tn_tr_t<32>(p, nz, tout, st); return; }
-  if (p.NS == 64) { launch_tn_tr_t<64>(p, nz, tout, st); return; }
-  if (p.NS == 96) { launch_tn_tr_t<96>(p, nz, tout, st); return; }
-  if (p.NS == 160) { launch_tn_tr_t<160>(p, nz, tout, st); return; }
-  if (p.NS == 128) { launch_tn_tr_t<128>(p, nz, tout, st); return; }
-  if (p.NS == 192) { launch_tn_tr_t<192>(p, nz, tout, st); return; }
-  if (p.NS == 256) { launch_tn_trw_t<256>(p, nz, tout, st); return; }
-  if (p.NS == 384) { launch_tn_trw_t<384>(p, nz, tout, st); return; }
   switch (p.NS) {
-    case 32: launch_tn_skinny_t<32>(p, nz, tout, st); break;
-    case 64: launch_tn_skinny_t<64>(p, nz, tout, st); break;
-    case 96: launch_tn_skinny_t<96>(p, nz, tout, st); break;
-    case 128: launch_tn_skinny_t<128>(p, nz, tout, st); break;
-    case 160: launch_tn_skinny_t<160>(p, nz, tout, st); break;
-    case 192: launch_tn_skinny_t<192>(p, nz, tout, st); break;
-    case 224: launch_tn_skinny_t<224>(p, nz, tout, st); break;
-    default: launch_tn_skinny_t<256>(p, nz, tout, st); break;
+    case 32: launch_tn_tr_t<32>(p, nz, tout, st); break;
+    case 64: launch_tn_tr_t<64>(p, nz, tout, st); break;
+    case 96: launch_tn_tr_t<96>(p, nz, tout, st); break;
+    case 128: launch_tn_tr_t<128>(p, nz, tout, st); break;
+    case 160: launch_tn_tr_t<160>(p, nz, tout, st); break;
+    case 192: launch_tn_tr_t<192>(p, nz, tout, st); break;
+    case 256: launch_tn_trw_t<256>(p, nz, tout, st); break;
+    default: launch_tn_trw_t<384>(p, nz, tout, st); break;
   }
 }
 
@@ -2142,16 +1983,15 @@ UNOK_EXPORT int unok_gemm_tn(int in_dtype, int Mrows, int P, int Q, const void* 
   UNOK_REQUIRE(workspace != nullptr && ws_bytes >= need, UNOK_EINVAL,
                "gemm_tn: workspace of %lld bytes needed, %lld given", (long long)need, (long long)ws_bytes);
   if (in_dtype == UNOK_BF16 && Mrows > 0) {
-    // Skinny path: the rank side (<= 256 columns and a multiple of 32, or 384) against a wide operand.
+    // Skinny path: the rank side (tn_skinny_width) against a wide operand.
     const bool a_small = P <= Q;
     const int NS = a_small ? P : Q, NX = a_small ? Q : P;
     const int64_t lds_ = a_small ? lda : ldb, ldx = a_small ? ldb : lda;
     const void* S = a_small ? A : B;
     const void* X = a_small ? B : A;
-    if (((NS % 32 == 0 && NS <= 256) || NS == 384) && NX >= TNS_QB && NX % 8 == 0 && lds_ % 8 == 0 &&
-        ldx % 8 == 0 && aligned16(S) && aligned16(X)) {
-      const bool tr = tn_transpose_load(NS);
-      const int nz0 = tr ? tn_tr_splits(Mrows, NX, NS) : tn_skinny_splits(Mrows, NX);
+    if (tn_skinny_width(NS) && NX >= TNS_MIN_NX && NX % 8 == 0 && lds_ % 8 == 0 && ldx % 8 == 0 && aligned16(S) &&
+        aligned16(X)) {
+      const int nz0 = tn_tr_splits(Mrows, NX, NS);
       int rps = (Mrows + nz0 - 1) / nz0;
       rps = ((rps + TNS_BK - 1) / TNS_BK) * TNS_BK;
       const int nz = (Mrows + rps - 1) / rps;
