@@ -2,9 +2,11 @@
 
 * ``fused_weighted_ce``: CE with the diffusion 1/t weighting (training/trainer.py:267-283). In
   bf16 the LM-head GEMM's epilogue reduces each 128-column block of logits to per-row softmax
-  statistics and picks the target logit, so the forward stores no logits; the backward recomputes
-  the logits one vocabulary chunk at a time in a GEMM whose epilogue emits dz = g w (softmax -
-  onehot) for the data-gradient GEMM. Only a [rows x chunk] bf16 buffer exists.
+  statistics and picks the target logit; it also stores the rows' fp32 logits when they fit
+  CE_STORED_LOGITS_MAX_BYTES, and the backward then forms dz = g w (softmax - onehot) from them one
+  vocabulary chunk at a time. Above that size the forward stores no logits and the backward
+  recomputes them chunk by chunk in a GEMM whose epilogue emits dz. Either way dz passes through
+  one [rows x chunk] bf16 buffer into the data-gradient GEMM.
 * ``teacher_argmax``: first-index argmax of the clean-stream logits, chunked the same way
   (training/losses.py:38-56, target source "clean_argmax").
 * ``distribution_losses``: reverse KL and total variation (training/losses.py:59-183) over
