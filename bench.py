@@ -15,7 +15,8 @@ dispatch by a few microseconds, so the timed steps carry none). ``step_ms`` = me
 ``cpu_baseline`` = the CPU oracle of the same step timed on this host on a bounded sample (see
 cpu_baseline()). ``--workload draft_8b`` measures the inference-side draft forward instead (see
 run_draft()), ``--workload tiny`` the tiny fp32 step with the CPU oracle's whole step beside it
-(see run_tiny()).
+(see run_tiny()), ``--gemm-shapes`` the step's GEMM products one by one beside the vendor library
+(see run_gemm_shapes()).
 """
 from __future__ import annotations
 
@@ -461,6 +462,83 @@ def host_info() -> dict:
             "ram_gib": ram}
 
 
+def run_gemm_shapes(args) -> int:
+    """Per-shape timing of the step's 256x256 GEMM products at the Qwen3-8B shape (16384 rows) beside
+    torch.mm on the same operands (the vendor library: hipBLASLt on ROCm), for the fused products
+    against the plain product they contain. HIP events around 20 launches after 3 warm-up launches;
+    prints a markdown table (not the JSON line of a step run)."""
+    from uno_amd import kernels as K
+    dev, bf = "cuda:0", torch.bfloat16
+    M, H, F, R = 16384, 4096, 12288, 64
+    torch.manual_seed(0)
+
+    def t_ms(fn, n=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    def rnd(*shape):
+        return (torch.randn(*shape, device=dev) * 0.02).to(bf)
+
+    rows = []
+    wa, wb = rnd(M, H), rnd(8192, H)
+    t_ms(lambda: K.gemm_nt(wa, wb), n=40)           # the clocks settle before the first timed product
+    del wa, wb
+    # (product, N, K, LoRA K-extension (one 64-wide extension per output column, as in the step),
+    # residual): the linears of one layer and their data gradients
+    for name, N, Kd, K2, res in [("q|k|v", 6144, H, 0, False), ("q|k|v + LoRA", 6144, H, R, False),
+                                 ("o + residual", H, H, 0, True), ("o + LoRA + residual", H, H, R, True),
+                                 ("down + residual", H, F, 0, True), ("down + LoRA + residual", H, F, R, True),
+                                 ("data grad. of gate|up", H, 2 * F, 2 * R, False), ("data grad. of o", H, H, R, False),
+                                 ("data grad. of q|k|v", H, 6144, 3 * R, False)]:
+        a, b = rnd(M, Kd), rnd(N, Kd)
+        a2, b2 = (rnd(M, K2), rnd(N, K2)) if K2 else (None, None)
+        r = rnd(M, N) if res else None
+        out = torch.empty(M, N, device=dev, dtype=bf)
+        ms = t_ms(lambda: K.gemm_nt(a, b, a2=a2, b2=b2, residual=r, out=out))
+        at, bt = (torch.cat([a, a2], 1), torch.cat([b, b2], 1)) if K2 else (a, b)
+        ref = torch.mm(at, bt.t()).float() + (r.float() if res else 0.0)
+        err = ((out.float() - ref).norm() / ref.norm()).item()
+        if err > 1e-2:
+            raise RuntimeError(f"{name}: relative error {err:.2e} against torch.mm")
+        ms_lib = t_ms(lambda: torch.mm(at, bt.t(), out=out))
+        rows.append((name, N, Kd + K2, ms, ms_lib, 2.0 * M * N * (Kd + K2)))
+        del a, b, a2, b2, r, out, at, bt, ref
+    # gate/up with the SwiGLU epilogue (output [M, F]) against the plain [M, 2F] product
+    a, w = rnd(M, H), rnd(2 * F, H)
+    wi = K.interleave_gate_up(w, F)
+    s = torch.empty(M, F, device=dev, dtype=bf)
+    ms = t_ms(lambda: K.gemm_nt_swiglu(a, wi, out=s))
+    big = torch.empty(M, 2 * F, device=dev, dtype=bf)
+    ms_lib = t_ms(lambda: torch.mm(a, w.t(), out=big))
+    rows.append(("gate|up + SwiGLU", 2 * F, H, ms, ms_lib, 2.0 * M * 2 * F * H))
+    gu = big
+    # down-projection data gradient with the SwiGLU backward epilogue against the plain [M, F] product
+    dy, wdt = rnd(M, H), rnd(F, H)
+    la2, lb2 = rnd(M, R), rnd(F, R)
+    dgu = torch.empty(M, 2 * F, device=dev, dtype=bf)
+    ms = t_ms(lambda: K.gemm_nt_swiglu_bwd(dy, wdt, la2, lb2, gu, dgu))
+    at, bt = torch.cat([dy, la2], 1), torch.cat([wdt, lb2], 1)
+    ms_lib = t_ms(lambda: torch.mm(at, bt.t(), out=s))
+    rows.append(("SwiGLU backward (+ LoRA)", F, H + R, ms, ms_lib, 2.0 * M * F * (H + R)))
+    lib = getattr(torch.backends.cuda, "preferred_blas_library", lambda: "default")()
+    print(f"M = {M} rows; vendor library: torch.mm ({lib}) on the same operands (the LoRA extension concatenated "
+          f"into K), plain product only (no residual, SwiGLU or its backward); bf16 in, bf16 out\n")
+    print("| product | N | K | this build ms | TFLOP/s | torch.mm ms | TFLOP/s | time ratio |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|")
+    for name, N, Kt, ms, ms_lib, fl in rows:
+        print(f"| {name} | {N} | {Kt} | {ms:.3f} | {fl / ms / 1e9:.0f} | {ms_lib:.3f} | {fl / ms_lib / 1e9:.0f} | "
+              f"{ms / ms_lib:.3f} |", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -480,6 +558,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=None,
                     help="threads of the CPU baseline (default: every physical core this process may use)")
+    ap.add_argument("--gemm-shapes", action="store_true",
+                    help="instead of a step: the step's GEMM products one by one beside torch.mm (markdown table)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run three plain 1 GiB device copies (the reference kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -491,6 +571,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.gemm_shapes:
+        return run_gemm_shapes(args)
     if args.workload == "draft_8b":
         return run_draft(args)
     if args.workload == "tiny":
