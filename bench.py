@@ -11,7 +11,8 @@ accounting). ``roofline`` = the dominant kernel (256x256 bf16 MFMA GEMM of the f
 linears and the LM head): algorithmic FLOPs per launch / mean launch time, from HIP events around
 every such launch in as many steps again right after the timed ones (an event delays the next
 dispatch by a few microseconds, so the timed steps carry none). ``step_ms`` = median and
-10th / 90th percentile of the timed steps from one HIP event between consecutive steps.
+10th / 90th percentile of the timed steps from one HIP event between consecutive steps; ``loss`` =
+the first and the last timed step's loss (a non-finite loss fails the run).
 ``cpu_baseline`` = the CPU oracle of the same step timed on this host on a bounded sample (see
 cpu_baseline()). ``--workload draft_8b`` measures the inference-side draft forward instead (see
 run_draft()), ``--workload tiny`` the tiny fp32 step with the CPU oracle's whole step beside it
@@ -22,6 +23,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -633,12 +635,16 @@ def main() -> int:
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
     evs[0].record()
+    losses = []
     for i in range(args.steps):
-        trainer.train_step(batch)
+        losses.append(trainer.train_step(batch))
         evs[i + 1].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     per_step = [evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]
+    losses = [float(x) for x in losses]
+    if not all(math.isfinite(x) for x in losses):
+        raise RuntimeError(f"non-finite loss in the timed steps: {losses}")
     # Roofline window: as many further steps with HIP events around every 256x256 GEMM launch.
     # A recorded event delays the next dispatch by a few microseconds, so these steps are not the
     # ones that give the step time.
@@ -667,6 +673,7 @@ def main() -> int:
                    "lora_rank": wl["lora_rank"], "lora_alpha": wl["lora_alpha"],
                    "objective": objective(wl.get("objective", "ce"))[1], "parallelism": "single GPU"},
         "step_ms": spread(per_step),
+        "loss": {"first": round(losses[0], 5), "last": round(losses[-1], 5)},
         "mfu": round(mfu, 4), "algorithmic_tflop_per_step": round(flops["total"] / 1e12, 2),
         "flops_breakdown_tflop": {k: round(v / 1e12, 2) for k, v in flops.items() if k != "total"},
         "roofline": {"kernel": "gemm_nt_bf16_w4m16_kernel (256x256 tiles, 16x16x32 MFMA; fused LoRA linears, "
