@@ -533,7 +533,7 @@ def run_gemm_shapes(args) -> int:
     lib = getattr(torch.backends.cuda, "preferred_blas_library", lambda: "default")()
     print(f"M = {M} rows; vendor library: torch.mm ({lib}) on the same operands (the LoRA extension concatenated "
           f"into K), plain product only (no residual, SwiGLU or its backward); bf16 in, bf16 out\n")
-    print("| product | N | K | this build ms | TFLOP/s | torch.mm ms | TFLOP/s | time ratio |")
+    print("| product | N | K | uno_amd ms | TFLOP/s | torch.mm ms | TFLOP/s | time ratio |")
     print("|---|---:|---:|---:|---:|---:|---:|---:|")
     for name, N, Kt, ms, ms_lib, fl in rows:
         print(f"| {name} | {N} | {Kt} | {ms:.3f} | {fl / ms / 1e9:.0f} | {ms_lib:.3f} | {fl / ms_lib / 1e9:.0f} | "

@@ -266,7 +266,7 @@ int unok_ce_finish(int R, const float* run_max, const float* run_sum, const floa
 int unok_ce_grad_chunk(int out_dtype, int R, int Vc, const float* z, int64_t ldz, int c0,
                        const float* lse, const int64_t* tgt, const float* w, const float* gscale,
                        const float* inv_n, void* dz, int64_t lddz, void* stream);
-/* Cross-entropy over the LM head without materialised logits (BASELINE north star (4); the
+/* Cross-entropy over the LM head with the logit statistics formed in the GEMM's epilogue (the
  * loss of training/trainer.py:267-283 on the logits of training/losses.py:21-35). Z = H W^T with
  * H [R, K] bf16 (the CE rows' hidden states) and W [V, K] bf16 (LM-head rows vocab0 ..
  * vocab0 + V - 1); K a multiple of 64. Z is produced tile by tile inside the 256x256 MFMA GEMM; it

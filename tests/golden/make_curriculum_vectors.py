@@ -7,7 +7,7 @@ Run in the build container, where the reference tree is present:
 It loads training/curriculum.py from /root/reference by file path (that module needs only the
 standard library and PyYAML) and, for the released schedule file and a few synthetic schedules
 written as YAML, records the stage boundaries, the manifest and ``sha256()``. A boundary checkpoint
-stores that hash (training/trainer.py:110-146), so a resume validates only when this build's hash of
+stores that hash (training/trainer.py:110-146), so a resume validates only when uno_amd's hash of
 the same schedule is bit-identical; nothing else in the reference pins it.
 """
 from __future__ import annotations

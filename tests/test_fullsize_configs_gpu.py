@@ -12,7 +12,7 @@ layer each, against the fp32 oracle on the same bf16-rounded weights:
 * mha_7b    hidden 4096, 32 q = 32 kv heads, no q/k-norm, FFN 11008, vocab 32000, r 64 / alpha 1024
             (16 r), one 4096-token row, at block 16 and at every block size of the 4 -> 32 curriculum.
 
-The GPU step keeps bf16 weights, adapters and activations. Bars (BASELINE north star): loss within
+The GPU step keeps bf16 weights, adapters and activations. Bars: loss within
 1e-3 relative, LoRA gradient cosine >= 0.999 and relative L2 error <= 1e-2 per tensor against the
 fp32 oracle. The configurations with alpha = 16 r (7B MHA, rank 128) are held to max(1e-2, 1.3 x
 the reference's own bf16 arithmetic on the same inputs) instead: there the error that bf16 storage
