@@ -393,6 +393,8 @@ __global__ __launch_bounds__(1024) void sum_scaled_kernel(int64_t n, const float
 
 UNOK_EXPORT int unok_row_lse_update(int dtype, int R, int Vc, const void* z, int64_t ldz, int c0, const int64_t* tgt,
                                     float* run_max, float* run_sum, float* zt, int first, void* stream) {
+  UNOK_REQUIRE(R >= 0 && Vc >= 0 && (R <= 1 || ldz >= Vc), UNOK_EINVAL, "row_lse_update: R=%d Vc=%d ldz=%lld", R, Vc,
+               (long long)ldz);
   if (R == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   DISPATCH_T(dtype, hipLaunchKernelGGL(row_lse_update_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)z, ldz, Vc, c0,
@@ -429,6 +431,8 @@ UNOK_EXPORT int unok_ce_parts_reduce(int R, int nparts, const float* pmax, const
 
 UNOK_EXPORT int unok_row_argmax_update(int dtype, int R, int Vc, const void* z, int64_t ldz, int c0, float* best_val,
                                        int64_t* best_idx, int first, void* stream) {
+  UNOK_REQUIRE(R >= 0 && Vc >= 0 && (R <= 1 || ldz >= Vc), UNOK_EINVAL, "row_argmax_update: R=%d Vc=%d ldz=%lld", R, Vc,
+               (long long)ldz);
   if (R == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   DISPATCH_T(dtype, hipLaunchKernelGGL(row_argmax_update_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)z, ldz, Vc,
@@ -438,6 +442,7 @@ UNOK_EXPORT int unok_row_argmax_update(int dtype, int R, int Vc, const void* z, 
 
 UNOK_EXPORT int unok_ce_finish(int R, const float* run_max, const float* run_sum, const float* zt, const float* w,
                                const float* inv_n, float* lse, float* loss, void* stream) {
+  UNOK_REQUIRE(R >= 0, UNOK_EINVAL, "ce_finish: R=%d", R);
   hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, R, run_max, run_sum, zt, w, inv_n,
                      lse, loss);
   return unok::check_launch("ce_finish");
@@ -446,6 +451,9 @@ UNOK_EXPORT int unok_ce_finish(int R, const float* run_max, const float* run_sum
 UNOK_EXPORT int unok_ce_grad_chunk(int out_dtype, int R, int Vc, const float* z, int64_t ldz, int c0, const float* lse,
                                    const int64_t* tgt, const float* w, const float* gscale, const float* inv_n,
                                    void* dz, int64_t lddz, void* stream) {
+  UNOK_REQUIRE(R >= 0 && Vc >= 0 && (R <= 1 || (ldz >= Vc && lddz >= Vc)), UNOK_EINVAL,
+               "ce_grad_chunk: R=%d Vc=%d ldz=%lld lddz=%lld", R, Vc, (long long)ldz, (long long)lddz);
+  UNOK_REQUIRE(out_dtype == UNOK_BF16 || out_dtype == UNOK_F32, UNOK_EINVAL, "ce_grad_chunk: bad dtype %d", out_dtype);
   if (R == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   if (out_dtype == UNOK_BF16)
@@ -459,6 +467,7 @@ UNOK_EXPORT int unok_ce_grad_chunk(int out_dtype, int R, int Vc, const float* z,
 
 UNOK_EXPORT int unok_softmax_stats(int dtype, int R, int V, const void* z, int64_t ldz, float* mx, float* se,
                                    void* stream) {
+  UNOK_REQUIRE(R >= 0 && V >= 0 && (R <= 1 || ldz >= V), UNOK_EINVAL, "softmax_stats: R=%d V=%d ldz=%lld", R, V, (long long)ldz);
   if (R == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   DISPATCH_T(dtype, hipLaunchKernelGGL(softmax_stats_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)z, ldz, V, mx, se));
@@ -468,6 +477,7 @@ UNOK_EXPORT int unok_softmax_stats(int dtype, int R, int V, const void* z, int64
 UNOK_EXPORT int unok_tv_fwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
                             const float* ms, const float* ss, const float* mt, const float* st_, float* row_l1,
                             float* row_S, void* stream) {
+  UNOK_REQUIRE(R >= 0 && V >= 0 && (R <= 1 || (lds >= V && ldt >= V)), UNOK_EINVAL, "tv_fwd: R=%d V=%d", R, V);
   if (R == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   DISPATCH_T(dtype, hipLaunchKernelGGL(tv_fwd_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)zs, lds, (const T*)zt,
@@ -478,6 +488,7 @@ UNOK_EXPORT int unok_tv_fwd(int dtype, int R, int V, const void* zs, int64_t lds
 UNOK_EXPORT int unok_tv_bwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
                             const float* ms, const float* ss, const float* mt, const float* st_, const float* row_S,
                             const float* gscale, const float* inv_n, void* grad, int64_t ldg, void* stream) {
+  UNOK_REQUIRE(R >= 0 && V >= 0 && (R <= 1 || (lds >= V && ldt >= V && ldg >= V)), UNOK_EINVAL, "tv_bwd: R=%d V=%d", R, V);
   if (R == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   DISPATCH_T(dtype, hipLaunchKernelGGL(tv_bwd_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)zs, lds, (const T*)zt,
@@ -488,6 +499,7 @@ UNOK_EXPORT int unok_tv_bwd(int dtype, int R, int V, const void* zs, int64_t lds
 UNOK_EXPORT int unok_kl_fwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
                             const float* ms, const float* ss, const float* mt, const float* st_, float* row_kl,
                             void* stream) {
+  UNOK_REQUIRE(R >= 0 && V >= 0 && (R <= 1 || (lds >= V && ldt >= V)), UNOK_EINVAL, "kl_fwd: R=%d V=%d", R, V);
   if (R == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   DISPATCH_T(dtype, hipLaunchKernelGGL(kl_fwd_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)zs, lds, (const T*)zt,
@@ -498,6 +510,7 @@ UNOK_EXPORT int unok_kl_fwd(int dtype, int R, int V, const void* zs, int64_t lds
 UNOK_EXPORT int unok_kl_bwd(int dtype, int R, int V, const void* zs, int64_t lds, const void* zt, int64_t ldt,
                             const float* ms, const float* ss, const float* mt, const float* st_, const float* row_kl,
                             const float* gscale, const float* inv_n, void* grad, int64_t ldg, void* stream) {
+  UNOK_REQUIRE(R >= 0 && V >= 0 && (R <= 1 || (lds >= V && ldt >= V && ldg >= V)), UNOK_EINVAL, "kl_bwd: R=%d V=%d", R, V);
   if (R == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   DISPATCH_T(dtype, hipLaunchKernelGGL(kl_bwd_kernel<T>, dim3(R), dim3(256), 0, st, (const T*)zs, lds, (const T*)zt,
@@ -506,6 +519,7 @@ UNOK_EXPORT int unok_kl_bwd(int dtype, int R, int V, const void* zs, int64_t lds
 }
 
 UNOK_EXPORT int unok_sum_scaled(int64_t n, const float* x, const float* inv_n, float* out, void* stream) {
+  UNOK_REQUIRE(n >= 0, UNOK_EINVAL, "sum_scaled: n=%lld", (long long)n);
   hipLaunchKernelGGL(sum_scaled_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, n, x, inv_n, out);
   return unok::check_launch("sum_scaled");
 }
