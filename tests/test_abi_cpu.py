@@ -101,6 +101,8 @@ BAD_CALLS = [
     ("unok_sum_scaled", dict(a0=-1), -1, "sum_scaled"),
     ("unok_grad_clip_coef", dict(a3=0), -1, "nparts=0"),
     ("unok_adamw_step", dict(a11=0), -1, "step must be >= 1"),
+    ("unok_cast_copy", dict(a0=5, a1=8), -1, "bad dtype"),
+    ("unok_transpose_jobs", dict(a0=1, a2=-1), -1, "njobs=-1"),
 ]
 
 

@@ -208,6 +208,9 @@ UNOK_EXPORT int unok_adamw_step(int64_t n, float* p, float* g, float* m, float* 
 
 UNOK_EXPORT int unok_cast_copy(int copy_dtype, int64_t n, int64_t n_unscaled, float scale, const float* p, void* copy,
                                void* stream) {
+  UNOK_REQUIRE(n >= 0 && n_unscaled >= 0, UNOK_EINVAL, "cast_copy: n=%lld n_unscaled=%lld", (long long)n,
+               (long long)n_unscaled);
+  UNOK_REQUIRE(copy_dtype == UNOK_F32 || copy_dtype == UNOK_BF16, UNOK_EINVAL, "cast_copy: bad dtype %d", copy_dtype);
   if (n == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   if (copy_dtype == UNOK_F32)
@@ -221,6 +224,9 @@ UNOK_EXPORT int unok_cast_copy(int copy_dtype, int64_t n, int64_t n_unscaled, fl
 
 UNOK_EXPORT int unok_transpose_jobs(int dtype, const int64_t* jobs, int njobs, int64_t total_tiles, const void* src,
                                     void* dst, void* stream) {
+  UNOK_REQUIRE(njobs >= 0 && total_tiles >= 0 && total_tiles <= 0xFFFFFFFFll, UNOK_EINVAL,
+               "transpose_jobs: njobs=%d total_tiles=%lld", njobs, (long long)total_tiles);
+  UNOK_REQUIRE(dtype == UNOK_F32 || dtype == UNOK_BF16, UNOK_EINVAL, "transpose_jobs: bad dtype %d", dtype);
   if (njobs == 0 || total_tiles == 0) return 0;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == UNOK_F32)
